@@ -1,0 +1,52 @@
+"""Host-side SpMV call over device tensors (the Recon layout of
+spmv/src/dia_reconstruct.cuh:61-118, the launcher of
+spmv/src/tc_spmv_regdirect_kernel.cu:135-147).
+
+torch tensors only carry device memory and the stream; the work is done by
+diagpu_spmv_recon_f32 / _f64 in libdiagpu.so.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from . import _lib
+
+
+def _stream_handle(stream) -> int:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, torch.cuda.Stream):
+        return stream.cuda_stream
+    return int(stream)
+
+
+def recon_view(offsets: torch.Tensor, values: torch.Tensor, rows: int, cols: int):
+    """ReconView over device tensors: offsets int32 [K], values [K * cols]."""
+    if offsets.dtype != torch.int32 or not offsets.is_cuda:
+        raise TypeError("offsets must be an int32 device tensor")
+    if not values.is_cuda or not values.is_contiguous():
+        raise TypeError("values must be a contiguous device tensor")
+    K = offsets.numel()
+    if values.numel() != K * cols:
+        raise ValueError(f"values has {values.numel()} elements, expected K*cols = {K * cols}")
+    cls = {torch.float32: _lib.ReconViewF32, torch.float64: _lib.ReconViewF64}.get(values.dtype)
+    if cls is None:
+        raise TypeError(f"unsupported dtype {values.dtype}")
+    return cls(rows, cols, K, offsets.data_ptr(), values.data_ptr())
+
+
+def spmv_recon(offsets: torch.Tensor, values: torch.Tensor, rows: int, cols: int,
+               x: torch.Tensor, y: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """y = H x for the Recon matrix (offsets, values); y is overwritten."""
+    view = recon_view(offsets, values, rows, cols)
+    if x.dtype != values.dtype or not x.is_cuda:
+        raise TypeError("x must be a device tensor of the values' dtype")
+    if y is None:
+        y = torch.empty(rows, dtype=values.dtype, device=values.device)
+    if y.dtype != values.dtype or y.numel() < rows or not y.is_cuda:
+        raise TypeError("y must be a device tensor of the values' dtype with >= rows elements")
+    name = "diagpu_spmv_recon_f32" if values.dtype == torch.float32 else "diagpu_spmv_recon_f64"
+    _lib.call(name, C.byref(view), x.data_ptr(), x.numel(), y.data_ptr(), _stream_handle(stream))
+    return y

@@ -1,0 +1,194 @@
+"""Seeded synthetic inputs of the BASELINE.json configurations, built on the
+device with torch (plain tensor fills: they are inputs, not the product).
+
+Recon matrices follow spmv/src/dia_reconstruct.cuh:9-17 (column-indexed,
+offsets descending, padding zero); HM matrices follow
+spmspm/bench_spmspm.cu:74-86 (offsets ascending, position min(row, col),
+int64 starts).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+
+def _gen(device, seed: int) -> torch.Generator:
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return g
+
+
+def _uniform(shape, lo, hi, g, device, dtype):
+    return torch.rand(shape, generator=g, device=device, dtype=dtype) * (hi - lo) + lo
+
+
+@dataclass
+class Recon:
+    rows: int
+    cols: int
+    offsets: torch.Tensor      # int32 [K], descending
+    values: torch.Tensor       # [K * cols]
+    x: torch.Tensor            # [cols]
+
+    @property
+    def K(self) -> int:
+        return self.offsets.numel()
+
+    def useful_terms(self) -> int:
+        """Number of in-range (row, diagonal) terms, sum_k len(d_k)."""
+        o = self.offsets.cpu().numpy().astype(np.int64)
+        lo = np.maximum(0, -o)
+        hi = np.minimum(self.rows, self.cols - o)
+        return int(np.maximum(0, hi - lo).sum())
+
+
+def zero_recon_padding(offsets: torch.Tensor, values: torch.Tensor, rows: int, cols: int) -> None:
+    """Zero Recon[k][c] where row c - d_k is outside [0, rows)."""
+    K = offsets.numel()
+    v = values.view(K, cols)
+    c = torch.arange(cols, device=values.device, dtype=torch.int64)
+    for k, d in enumerate(offsets.cpu().tolist()):
+        r = c - d
+        v[k].masked_fill_((r < 0) | (r >= rows), 0)
+
+
+def recon_random(n: int, offsets, seed: int, device="cuda", dtype=torch.float32,
+                 x_dist: str = "normal") -> Recon:
+    """Values U[-1, 1] on every in-range entry, x ~ N(0, 1) or U[-1, 1]."""
+    offs = sorted({int(d) for d in offsets}, reverse=True)
+    g = _gen(device, seed)
+    K = len(offs)
+    vals = _uniform((K * n,), -1.0, 1.0, g, device, dtype)
+    ot = torch.tensor(offs, dtype=torch.int32, device=device)
+    zero_recon_padding(ot, vals, n, n)
+    if x_dist == "normal":
+        x = torch.randn(n, generator=g, device=device, dtype=dtype)
+    else:
+        x = _uniform((n,), -1.0, 1.0, g, device, dtype)
+    return Recon(n, n, ot, vals, x)
+
+
+def recon_poisson5(side: int, seed: int, device="cuda", dtype=torch.float32) -> Recon:
+    """2-D 5-point Poisson stencil on a side x side grid:
+    offsets {side, 1, 0, -1, -side}, diagonal 4, off-diagonals -1, the +-1
+    entries that wrap across a grid row zeroed, x ~ N(0, 1)."""
+    n = side * side
+    offs = [side, 1, 0, -1, -side]
+    vals = torch.full((5, n), -1.0, device=device, dtype=dtype)
+    vals[2].fill_(4.0)
+    c = torch.arange(n, device=device, dtype=torch.int64)
+    vals[1].masked_fill_(c % side == 0, 0)          # H[r, r+1] with r % side == side-1
+    vals[3].masked_fill_(c % side == side - 1, 0)   # H[r, r-1] with r % side == 0
+    ot = torch.tensor(offs, dtype=torch.int32, device=device)
+    vals = vals.reshape(-1).contiguous()
+    zero_recon_padding(ot, vals, n, n)
+    g = _gen(device, seed)
+    x = torch.randn(n, generator=g, device=device, dtype=dtype)
+    return Recon(n, n, ot, vals, x)
+
+
+def random_band_offsets(count: int, half_width: int, seed: int) -> list[int]:
+    """0 plus count-1 distinct offsets drawn uniformly from [-hw, hw] \\ {0}."""
+    rng = np.random.default_rng(seed)
+    pool = np.array([d for d in range(-half_width, half_width + 1) if d != 0])
+    pick = rng.choice(pool, size=count - 1, replace=False)
+    return sorted({0, *map(int, pick)})
+
+
+def spmv_config(cfg: int, seed: int = 0, device="cuda", dtype=torch.float32) -> Recon:
+    """BASELINE.json SpMV configs 1-3 (1-based numbering of BASELINE.md)."""
+    if cfg == 1:
+        return recon_random(1 << 20, [-1, 0, 1], seed, device, dtype, x_dist="uniform")
+    if cfg == 2:
+        return recon_poisson5(2048, seed, device, dtype)
+    if cfg == 3:
+        return recon_random(4_194_304, random_band_offsets(64, 512, seed), seed, device, dtype)
+    raise ValueError(f"no SpMV config {cfg}")
+
+
+# --------------------------------------------------------------------------
+# HM (compact) operands for SpGEMM
+# --------------------------------------------------------------------------
+
+@dataclass
+class HM:
+    n: int
+    offsets: torch.Tensor      # int32 [D], ascending
+    lengths: torch.Tensor      # int32 [D] = n - |d|
+    starts: torch.Tensor       # int64 [D]
+    values: torch.Tensor       # float32 [sum lengths]
+
+    @property
+    def ndiag(self) -> int:
+        return self.offsets.numel()
+
+    @property
+    def nnz(self) -> int:
+        return int(self.values.numel())
+
+
+def hm_layout(n: int, offsets) -> tuple[list[int], list[int], list[int]]:
+    offs = sorted({int(d) for d in offsets})
+    lens = [n - abs(d) for d in offs]
+    starts = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64).tolist() if offs else []
+    return offs, lens, starts
+
+
+def hm_from_values(n: int, offsets, values: torch.Tensor, device="cuda") -> HM:
+    offs, lens, starts = hm_layout(n, offsets)
+    return HM(n, torch.tensor(offs, dtype=torch.int32, device=device),
+              torch.tensor(lens, dtype=torch.int32, device=device),
+              torch.tensor(starts, dtype=torch.int64, device=device), values)
+
+
+def hm_random(n: int, offsets, seed: int, device="cuda") -> HM:
+    offs, lens, _ = hm_layout(n, offsets)
+    g = _gen(device, seed)
+    vals = _uniform((sum(lens),), -1.0, 1.0, g, device, torch.float32)
+    return hm_from_values(n, offs, vals, device)
+
+
+def hm_stencil7(nx: int, ny: int, nz: int, device="cuda") -> HM:
+    """3-D 7-point stencil on an nx x ny x nz grid (x fastest): offsets
+    {0, +-1, +-nx, +-nx*ny}, diagonal 6, off-diagonals -1, entries whose
+    neighbour wraps across a grid line or plane zeroed."""
+    n = nx * ny * nz
+    offs, lens, _ = hm_layout(n, [0, 1, -1, nx, -nx, nx * ny, -nx * ny])
+    parts = []
+    for d, ln in zip(offs, lens):
+        v = torch.full((ln,), -1.0, device=device, dtype=torch.float32)
+        if d == 0:
+            v.fill_(6.0)
+        else:
+            # HM position p -> row i = p - min(d, 0); neighbour of row i is i + d.
+            p = torch.arange(ln, device=device, dtype=torch.int64)
+            i = p - min(d, 0)
+            ad = abs(d)
+            if ad == 1:
+                bad = (i % nx == nx - 1) if d > 0 else (i % nx == 0)
+            elif ad == nx:
+                bad = ((i // nx) % ny == ny - 1) if d > 0 else ((i // nx) % ny == 0)
+            else:
+                bad = torch.zeros_like(i, dtype=torch.bool)   # z planes: padding covers it
+            v.masked_fill_(bad, 0)
+        parts.append(v)
+    return hm_from_values(n, offs, torch.cat(parts), device)
+
+
+def spgemm_config(cfg: int, seed: int = 0, device="cuda") -> tuple[HM, HM]:
+    """BASELINE.json SpGEMM configs 4 and 5."""
+    if cfg == 4:
+        n = 1 << 20
+        A = hm_random(n, range(-4, 5), seed, device)
+        B = hm_stencil7(128, 128, 64, device)     # offsets {0, +-1, +-128, +-16384}
+        assert B.n == n
+        return A, B
+    if cfg == 5:
+        n = 262_144
+        rng = np.random.default_rng(seed)
+        oa = rng.choice(np.arange(-4096, 4097), size=128, replace=False)
+        ob = rng.choice(np.arange(-4096, 4097), size=128, replace=False)
+        return hm_random(n, oa, seed, device), hm_random(n, ob, seed + 1, device)
+    raise ValueError(f"no SpGEMM config {cfg}")

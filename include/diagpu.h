@@ -1,0 +1,176 @@
+/*
+ * diagpu.h -- C ABI of the MI355X (gfx950) diagonal-format sparse kernels.
+ *
+ * Every entry point:
+ *   - takes plain pointers and sizes (device pointers unless marked "host"),
+ *     a HIP stream as void* (NULL = the default stream);
+ *   - returns 0 (DIAGPU_OK) or a DIAGPU_ERR_* code, never exits; the text of
+ *     the last failure on the calling thread is in diagpu_last_error();
+ *   - validates its host-visible arguments before any HIP call, so argument
+ *     errors are reported without touching the GPU;
+ *   - is asynchronous on `stream` unless stated otherwise, allocates nothing
+ *     and takes no ownership: the caller allocates and frees every buffer.
+ *
+ * Layouts (all square n x n for SpGEMM; rows x cols for SpMV):
+ *   Recon      K x cols row-major, Recon[k][c] = H[c - d_k, c], rows sorted by
+ *              offset descending (spmv/src/dia_reconstruct.cuh:9-17).
+ *   HM         compact concatenation; diagonal d has length n - |d|, element
+ *              (i, j) sits at position min(i, j) from starts[k]
+ *              (spmspm/paper_hm.cuh:18-37, spmspm/bench_spmspm.cu:74-86).
+ *   row-packed P x n, DA[i][t] = A[t, t + d_i], zero outside the diagonal
+ *              (gemm_diag/gemm_diag.cu:9-15, 362-382).
+ * Element starts are int64 everywhere (the reference's int starts overflow
+ * for C outputs above 2^31 elements).
+ */
+#ifndef DIAGPU_H
+#define DIAGPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DIAGPU_API __attribute__((visibility("default")))
+
+enum {
+    DIAGPU_OK            = 0,
+    DIAGPU_ERR_ARG       = 1,  /* NULL pointer, negative size, bad flag          */
+    DIAGPU_ERR_OFFSET    = 2,  /* |offset| >= n or length != n - |offset|        */
+    DIAGPU_ERR_DUPLICATE = 3,  /* repeated diagonal offset in one operand        */
+    DIAGPU_ERR_OVERFLOW  = 4,  /* an index or count exceeds its integer type     */
+    DIAGPU_ERR_CAPACITY  = 5,  /* output capacity or workspace too small         */
+    DIAGPU_ERR_HIP       = 6   /* HIP runtime error (launch, copy, sync)          */
+};
+
+/* Text of the last error on this thread ("" if none). */
+DIAGPU_API const char* diagpu_last_error(void);
+/* Static name of a status code. */
+DIAGPU_API const char* diagpu_status_name(int status);
+/* ABI version: major * 10000 + minor * 100 + patch. */
+DIAGPU_API int diagpu_abi_version(void);
+
+/* ======================================================================
+ * SpMV on the Recon layout
+ * ====================================================================== */
+
+/* Non-owning device view of a Recon matrix.  Same members, order and types
+ * as ReconView (spmv/src/dia_reconstruct.cuh:112-118), so a ReconView can be
+ * passed by address. */
+typedef struct diagpu_recon_view_f32 {
+    int32_t        rows;
+    int32_t        cols;
+    int32_t        num_diags;
+    const int32_t* diag_offsets;   /* device [num_diags]             */
+    const float*   values;         /* device [num_diags * cols]      */
+} diagpu_recon_view_f32;
+
+typedef struct diagpu_recon_view_f64 {
+    int32_t        rows;
+    int32_t        cols;
+    int32_t        num_diags;
+    const int32_t* diag_offsets;
+    const double*  values;
+} diagpu_recon_view_f64;
+
+/* y[r] = sum_k [0 <= r + d_k < min(cols, x_size)] Recon[k][r + d_k] * x[r + d_k]
+ * for 0 <= r < rows; y is overwritten (beta = 0); rows == 0 is a successful
+ * no-op.  Offsets may be in any order and out of range (such terms drop).
+ * fp32 operands with fp32 accumulation (the reference rounds operands to
+ * TF32 first; this path keeps full fp32).  x and y must not overlap.
+ * Replaces launch_tc_spmv_regdirect (spmv/src/dia_reconstruct.cuh:139-144,
+ * spmv/src/tc_spmv_regdirect_kernel.cu:135-147). */
+DIAGPU_API int diagpu_spmv_recon_f32(const diagpu_recon_view_f32* R, const float* x,
+                                     int64_t x_size, float* y, void* stream);
+
+/* fp64 variant of diagpu_spmv_recon_f32 (no reference counterpart: the
+ * reference is fp32/TF32 only; BASELINE config 2 asks for fp64). */
+DIAGPU_API int diagpu_spmv_recon_f64(const diagpu_recon_view_f64* R, const double* x,
+                                     int64_t x_size, double* y, void* stream);
+
+/* ======================================================================
+ * DIA x DIA SpGEMM, HM layout: C = A * B
+ * ====================================================================== */
+
+/* One entry of the pair plan: C[k][p] += Av[ab + p + ash] * Bv[bb + p + bsh]
+ * for positions with 0 <= p + ash < al and 0 <= p + bsh < bl.  Same layout as
+ * GPair (spmspm/gather_flat.cuh:21): {size_t ab, bb; int ash, bsh, al, bl}. */
+typedef struct diagpu_gpair {
+    uint64_t ab, bb;
+    int32_t  ash, bsh, al, bl;
+} diagpu_gpair;
+
+/* Result counts of the symbolic phase (written to host memory). */
+typedef struct diagpu_spgemm_info {
+    int64_t c_ndiag;         /* number of C diagonals                       */
+    int64_t c_nnz;           /* sum of C lengths = C value count            */
+    int64_t n_pairs;         /* number of pair-plan entries                 */
+    int64_t max_pairs;       /* largest pair count of one C diagonal        */
+    int64_t useful_flops;    /* 2 * sum over pairs of the overlap length    */
+} diagpu_spgemm_info;
+
+/* Device workspace the symbolic phase needs for dimension n and operand
+ * diagonal counts a_ndiag, b_ndiag (bytes, host out).  Capacities the caller
+ * must provide: C arrays min(a_ndiag * b_ndiag, 2n - 1) entries (+1 for
+ * pair_ptr), pairs a_ndiag * b_ndiag entries. */
+DIAGPU_API int diagpu_spgemm_symbolic_workspace(int32_t n, int32_t a_ndiag, int32_t b_ndiag,
+                                                size_t* bytes);
+
+/* Symbolic (integer) phase, bit-exact with the reference host planners:
+ *   C offsets  = every da + db with |da + db| < n, ascending, once each
+ *                (make_c_structure, spmspm/bench_spmspm.cu:109-131;
+ *                 compute_c_hm_structure, spmspm/paper_hm.cuh:87-117);
+ *   C lengths  = n - |dc|; C starts = exclusive prefix sum of the lengths;
+ *   c_lookup   = dc + n - 1 -> C index, -1 where absent (optional, 2n - 1
+ *                entries; build_c_diag_lookup, spmspm/paper_hm.cuh:121-130);
+ *   pair plan  = per C diagonal in order, per B diagonal in B's order, the A
+ *                diagonal with da = dc - db if present, as GPair
+ *                (build_pairs_only, spmspm/gather_flat.cuh:231-255);
+ *                pair_ptr has c_ndiag + 1 entries.
+ * Operand offsets may be in any order but must be distinct with |d| < n, and
+ * lengths must equal n - |d| (DIAGPU_ERR_DUPLICATE / DIAGPU_ERR_OFFSET).
+ * Synchronises `stream` and writes *info (host).  The C starts of the
+ * operands are only copied into the plan (ab, bb), never dereferenced. */
+DIAGPU_API int diagpu_spgemm_symbolic(
+    int32_t n,
+    const int32_t* A_off, const int32_t* A_len, const int64_t* A_starts, int32_t a_ndiag,
+    const int32_t* B_off, const int32_t* B_len, const int64_t* B_starts, int32_t b_ndiag,
+    int32_t* C_off, int32_t* C_len, int64_t* C_starts, int64_t c_capacity,
+    int64_t* pair_ptr, diagpu_gpair* pairs, int64_t pair_capacity,
+    int32_t* c_lookup,
+    void* workspace, size_t workspace_bytes,
+    diagpu_spgemm_info* info, void* stream);
+
+/* Numeric phase: C_vals[C_starts[k] + p] = sum over the plan entries of C
+ * diagonal k (fp32 products, fp32 accumulation in plan order), for every
+ * 0 <= p < C_len[k]; every C value is written exactly once (no atomics, no
+ * pre-zeroing needed).  The shifted multiply-accumulate of
+ * hm_structured_sparse_matmul_kernel (spmspm/paper_hm_kernel.cu:31-93) and
+ * of the gather kernels (spmspm/spmspm.cu:196-319,
+ * spmspm/gather_flat.cuh:23-64), computed from the plan of
+ * diagpu_spgemm_symbolic.  c_ndiag and max_pairs come from its info. */
+DIAGPU_API int diagpu_spgemm_numeric_f32(
+    int32_t n, const float* A_vals, const float* B_vals,
+    const int32_t* C_off, const int32_t* C_len, const int64_t* C_starts, int64_t c_ndiag,
+    const int64_t* pair_ptr, const diagpu_gpair* pairs, int64_t max_pairs,
+    float* C_vals, void* stream);
+
+/* ======================================================================
+ * gemm_diag: row-packed operands, HM-layout C
+ * ====================================================================== */
+
+/* Starts and lengths that address a P x n row-packed array as an HM matrix:
+ * starts[i] = i * n + max(-d_i, 0), lengths[i] = n - |d_i| (the HM position
+ * of row t's element is t + min(d_i, 0)).  Device kernel; offsets must
+ * satisfy |d| < n (checked by the symbolic phase).  Lets gemm_diag run the
+ * SpGEMM symbolic and numeric phases unchanged on DA/DB as given
+ * (gemm_diag/gemm_diag.cu:119-329 computes the same product with atomics). */
+DIAGPU_API int diagpu_rowpacked_as_hm(int32_t n, const int32_t* offsets, int32_t ndiag,
+                                      int64_t* starts, int32_t* lengths, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DIAGPU_H */

@@ -1,0 +1,67 @@
+"""C ABI of libdiagpu.so on the CPU: every symbol include/diagpu.h declares is
+exported, and argument errors come back as status codes before any HIP call
+(none of these calls reaches the GPU)."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from diagpu_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols():
+    text = (ROOT / "include" / "diagpu.h").read_text()
+    return sorted(set(re.findall(r"DIAGPU_API\s+[\w\s\*]+?\b(diagpu_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_symbols()
+    assert len(names) >= 8
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _lib.PROTOTYPES, f"{name} has no ctypes prototype"
+    assert set(_lib.PROTOTYPES) == set(names)
+
+
+def test_status_names():
+    lib = _lib.load()
+    assert lib.diagpu_abi_version() >= 100
+    for code, name in [(0, b"DIAGPU_OK"), (1, b"DIAGPU_ERR_ARG"), (5, b"DIAGPU_ERR_CAPACITY")]:
+        assert lib.diagpu_status_name(code) == name
+
+
+def _status(name, *args):
+    return getattr(_lib.load(), name)(*args)
+
+
+def test_spmv_argument_errors():
+    V = _lib.ReconViewF32
+    fake = C.c_void_p(0x1000)   # never dereferenced: validation fails first
+    assert _status("diagpu_spmv_recon_f32", None, fake, 4, fake, None) == _lib.ERR_ARG
+    assert b"R is NULL" in _lib.load().diagpu_last_error()
+    v = V(-1, 4, 1, fake.value, fake.value)
+    assert _status("diagpu_spmv_recon_f32", C.byref(v), fake, 4, fake, None) == _lib.ERR_ARG
+    v = V(4, 4, 1, None, fake.value)
+    assert _status("diagpu_spmv_recon_f32", C.byref(v), fake, 4, fake, None) == _lib.ERR_ARG
+    v = V(4, 4, 1, fake.value, None)
+    assert _status("diagpu_spmv_recon_f32", C.byref(v), fake, 4, fake, None) == _lib.ERR_ARG
+    v = V(4, 4, 1, fake.value, fake.value)
+    assert _status("diagpu_spmv_recon_f32", C.byref(v), None, 4, fake, None) == _lib.ERR_ARG
+    assert _status("diagpu_spmv_recon_f32", C.byref(v), fake, 4, None, None) == _lib.ERR_ARG
+    assert _status("diagpu_spmv_recon_f32", C.byref(v), fake, -1, fake, None) == _lib.ERR_ARG
+    # rows == 0 is a successful no-op (tc_spmv_regdirect_kernel.cu:143)
+    v = V(0, 4, 1, None, None)
+    assert _status("diagpu_spmv_recon_f32", C.byref(v), None, 0, None, None) == _lib.OK
+    w = _lib.ReconViewF64(0, 0, 0, None, None)
+    assert _status("diagpu_spmv_recon_f64", C.byref(w), None, 0, None, None) == _lib.OK
+
+
+def test_python_wrapper_rejects_bad_tensors():
+    import torch
+    from diagpu_amd.spmv import recon_view
+    with pytest.raises(TypeError):
+        recon_view(torch.zeros(2, dtype=torch.int32), torch.zeros(8), 4, 4)

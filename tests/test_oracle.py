@@ -1,0 +1,260 @@
+"""Pins the CPU oracle (oracle/dia_oracle.c) -- CPU only.
+
+Each restated function is checked against something other than itself:
+the reference's own known-answer output (tests/golden, produced by the
+reference programs built from its sources), the reference programs run
+live where oracle/_ref is built, scipy's independent DIA definition, dense
+numpy products, closed forms, and a second traversal of the same algebra.
+"""
+import json
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+REF = Path(__file__).resolve().parents[1] / "oracle" / "_ref"
+
+TC_CASES = [  # spmv/test/test_tc_spmv.cu:168-179
+    ("tridiagonal", 48, [-1, 0, 1]),
+    ("tridiag ragged", 37, [-1, 0, 1]),
+    ("pentadiagonal", 64, [-2, -1, 0, 1, 2]),
+    ("9-diag wide band", 80, [-9, -5, -2, -1, 0, 1, 2, 5, 9]),
+    ("asymmetric band", 71, [-3, 0, 2, 4, 7]),
+    ("main diagonal", 16, [0]),
+]
+
+
+def hm_to_dense(n, offs, starts, vals):
+    """hm_to_dense of spmspm/paper_hm.cuh:68-83."""
+    D = np.zeros((n, n))
+    for d, s in zip(offs, starts):
+        sr, sc = (0, d) if d >= 0 else (-d, 0)
+        for p in range(n - abs(d)):
+            D[sr + p, sc + p] = vals[s + p]
+    return D
+
+
+def hm_random_np(n, offs, rng):
+    offs = sorted(set(int(d) for d in offs))
+    lens = [n - abs(d) for d in offs]
+    starts = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+    vals = rng.uniform(-1, 1, size=sum(lens)).astype(np.float32)
+    return (np.array(offs, np.int32), np.array(lens, np.int32), starts, vals)
+
+
+# ---------------------------------------------------------------- SpMV ----
+
+def test_known_answer_5x5(oracle):
+    kat = json.loads((GOLDEN / "reconstruct_kat.json").read_text())
+    H = np.array(kat["H"], dtype=np.float32)
+    x = np.array(kat["x"], dtype=np.float32)
+    offs, starts, lens, vals = oracle.dense_to_dia(H)
+    assert offs.tolist() == kat["dia_offsets"]
+    r_off, r_val = oracle.build_recon(5, 5, offs, starts, lens, vals)
+    assert r_off.tolist() == kat["recon_offsets"]
+    assert r_val.reshape(5, 5).tolist() == kat["recon_rows"]
+    y = oracle.spmv_recon_f32(5, 5, r_off, r_val, x)
+    assert y.tolist() == kat["y"]
+    assert np.array_equal(oracle.recon_to_dense(5, 5, r_off, r_val), H)
+    assert kat["checks"] == ["OK", "OK"]
+
+
+@pytest.mark.skipif(not (REF / "test_reconstruct").exists(), reason="oracle/_ref not built")
+def test_known_answer_live_reference():
+    """The reference program, built from its sources, still prints the fixture."""
+    import sys
+    sys.path.insert(0, str(GOLDEN))
+    from make_golden import parse_reconstruct
+    live = parse_reconstruct(subprocess.run([str(REF / "test_reconstruct")], capture_output=True,
+                                            text=True, check=True).stdout)
+    kat = json.loads((GOLDEN / "reconstruct_kat.json").read_text())
+    for key in ("H", "x", "dia_offsets", "recon_offsets", "recon_rows", "y", "checks"):
+        assert live[key] == kat[key], key
+
+
+def _parse_mtx(path):
+    lines = [ln for ln in Path(path).read_text().splitlines() if not ln.startswith("%")]
+    rows, cols, nnz = map(int, lines[0].split())
+    ents = [ln.split() for ln in lines[1:]]
+    assert len(ents) == nnz
+    return rows, ents
+
+
+def test_hash_band_matches_reference_mtx(oracle):
+    """hval of bench_cusparse.cu:70-76 vs gen_banded_mtx's printed values."""
+    N, ents = _parse_mtx(GOLDEN / "gen_banded_n64.mtx")
+    assert N == 64
+    for r, c, v in ents:
+        r, c = int(r) - 1, int(c) - 1
+        assert "%.7g" % oracle.hval(r, c - r) == v
+    # the Recon built from the same hash holds those values at [k][c]
+    offs = [-9, -5, -2, -1, 0, 1, 2, 5, 9]
+    r_off, r_val, x = oracle.hash_band_recon(N, offs)
+    assert r_off.tolist() == sorted(offs, reverse=True)
+    R = r_val.reshape(len(offs), N)
+    k_of = {d: k for k, d in enumerate(r_off.tolist())}
+    for r, c, v in ents:
+        r, c = int(r) - 1, int(c) - 1
+        assert "%.7g" % R[k_of[c - r], c] == v
+    assert np.count_nonzero(R) <= len(ents)
+
+
+@pytest.mark.skipif(not (REF / "gen_banded_mtx").exists(), reason="oracle/_ref not built")
+def test_hash_band_live_reference(tmp_path, oracle):
+    out = tmp_path / "b.mtx"
+    subprocess.run([str(REF / "gen_banded_mtx"), "200", str(out)], check=True,
+                   capture_output=True)
+    N, ents = _parse_mtx(out)
+    for r, c, v in ents:
+        r, c = int(r) - 1, int(c) - 1
+        assert "%.7g" % oracle.hval(r, c - r) == v
+
+
+@pytest.mark.parametrize("name,N,offsets", TC_CASES)
+def test_tc_cases_against_dense_and_scipy(oracle, name, N, offsets):
+    import scipy.sparse as sp
+    H, x = oracle.tc_spmv_case(N, offsets)
+    offs, starts, lens, vals = oracle.dense_to_dia(H)
+    assert sorted(offs.tolist()) == sorted(o for o in offsets if abs(o) < N)
+    r_off, r_val = oracle.build_recon(N, N, offs, starts, lens, vals)
+    # scipy.sparse.dia_matrix stores data[k][j] = A[j - off_k, j]: the Recon layout.
+    S = sp.dia_matrix((r_val.reshape(len(r_off), N), r_off), shape=(N, N)).toarray()
+    assert np.array_equal(S, H)
+    y_dense = H.astype(np.float64) @ x.astype(np.float64)
+    y64, absum = oracle.spmv_recon_ref64(N, N, r_off, r_val, x)
+    assert np.allclose(y64, y_dense, rtol=0, atol=1e-12)
+    y32 = oracle.spmv_recon_f32(N, N, r_off, r_val, x)
+    assert np.all(np.abs(y32 - y64) <= 1e-6 * absum + 1e-30)
+    assert np.array_equal(oracle.recon_to_dense(N, N, r_off, r_val), H)
+
+
+def test_spmv_poisson_closed_form(oracle):
+    """5-point stencil, x = 1: y = number of grid neighbours missing."""
+    import torch
+    from diagpu_amd.workloads import recon_poisson5
+    side = 8
+    R = recon_poisson5(side, seed=0, device="cpu")
+    n = side * side
+    y, _ = oracle.spmv_recon_ref64(n, n, R.offsets.numpy(), R.values.numpy(), np.ones(n, np.float32))
+    i, j = np.divmod(np.arange(n), side)
+    missing = (i == 0).astype(int) + (i == side - 1) + (j == 0) + (j == side - 1)
+    assert np.array_equal(y, missing.astype(np.float64))
+    assert torch.count_nonzero(R.values).item() == 5 * n - 4 * side
+
+
+def test_spmv_main_diagonal_and_out_of_range(oracle):
+    rng = np.random.default_rng(1)
+    n = 33
+    d = rng.standard_normal(n).astype(np.float32)
+    x = rng.standard_normal(n).astype(np.float32)
+    y = oracle.spmv_recon_f32(n, n, [0], d, x)
+    assert np.array_equal(y, d * x)
+    # offsets with |d| >= cols contribute nothing
+    y2 = oracle.spmv_recon_f32(n, n, [n, 0, -n - 5], np.concatenate([d, d, d]), x)
+    assert np.array_equal(y2, d * x)
+
+
+# --------------------------------------------------------- SpGEMM plan ----
+
+@pytest.mark.parametrize("seed", range(6))
+def test_c_structure_vs_brute_force(oracle, seed):
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(8, 60))
+    oa = rng.choice(np.arange(-n + 1, n), size=int(rng.integers(1, 8)), replace=False)
+    ob = rng.choice(np.arange(-n + 1, n), size=int(rng.integers(1, 8)), replace=False)
+    c_off, c_len, c_st, nnz = oracle.c_structure(n, oa, ob)
+    want = sorted({int(a + b) for a in oa for b in ob if abs(a + b) < n})
+    assert c_off.tolist() == want
+    assert c_len.tolist() == [n - abs(d) for d in want]
+    assert c_st.tolist() == np.concatenate([[0], np.cumsum(c_len)[:-1]]).tolist()
+    assert nnz == int(c_len.sum())
+    # the structural diagonal set of the dense product (random non-zero values)
+    A = hm_random_np(n, oa, rng)
+    B = hm_random_np(n, ob, rng)
+    P = hm_to_dense(n, A[0], A[2], A[3]) @ hm_to_dense(n, B[0], B[2], B[3])
+    r, c = np.nonzero(P)
+    assert sorted(set((c - r).tolist())) == want
+    lk = oracle.c_lookup(n, c_off)
+    for k, d in enumerate(want):
+        assert lk[d + n - 1] == k
+    assert int((lk >= 0).sum()) == len(want)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_pair_plan_and_numeric_vs_dense(oracle, seed):
+    rng = np.random.default_rng(100 + seed)
+    n = int(rng.integers(16, 90))
+    oa = rng.choice(np.arange(-n + 1, n), size=int(rng.integers(1, 10)), replace=False)
+    ob = rng.choice(np.arange(-n + 1, n), size=int(rng.integers(1, 10)), replace=False)
+    A = hm_random_np(n, oa, rng)
+    B = list(hm_random_np(n, ob, rng))
+    if seed % 2:   # B's order must not matter to the set, only to the pair order
+        perm = rng.permutation(len(B[0]))
+        B = [B[0][perm], B[1][perm], B[2][perm], B[3]]
+    c_off, c_len, c_st, nnz = oracle.c_structure(n, A[0], B[0])
+    ptr, pairs = oracle.pairs_only(n, A[0], A[1], A[2], B[0], B[1], B[2], c_off)
+    assert ptr[0] == 0 and np.all(np.diff(ptr) >= 1)          # every C diagonal has a pair
+    assert ptr[-1] == sum(1 for a in A[0] for b in B[0] if abs(int(a) + int(b)) < n)
+    # pairs of one C diagonal follow B's array order
+    b_index = {int(s): i for i, s in enumerate(B[2])}
+    for k in range(len(c_off)):
+        order = [b_index[int(g["bb"])] for g in pairs[ptr[k]:ptr[k + 1]]]
+        assert order == sorted(order)
+    dense = hm_to_dense(n, A[0], A[2], A[3]) @ hm_to_dense(n, B[0], B[2], B[3])
+    want = np.zeros(nnz)
+    for d, s, ln in zip(c_off, c_st, c_len):
+        sr, sc = (0, d) if d >= 0 else (-d, 0)
+        want[s:s + ln] = dense[sr + np.arange(ln), sc + np.arange(ln)]
+    got_pairs, ab = oracle.spgemm_pairs_f64(A[3], B[3], c_len, c_st, ptr, pairs, 0, len(c_off))
+    assert np.allclose(got_pairs, want, rtol=0, atol=1e-12)
+    got_gather, _ = oracle.spgemm_gather_f64(n, A, tuple(B), (c_off, c_len, c_st, nnz))
+    assert np.allclose(got_gather, want, rtol=0, atol=1e-12)
+    got_atomic = oracle.spgemm_hm_atomic_f64(n, A, tuple(B), c_len, c_st,
+                                             oracle.c_lookup(n, c_off), nnz)
+    assert np.allclose(got_atomic, want, rtol=0, atol=1e-12)
+    assert np.all(ab >= np.abs(got_pairs) - 1e-12)
+    # fp32 CPU baseline agrees within the summation bound
+    out = np.zeros(nnz, np.float32)
+    oracle.spgemm_pairs_omp_f32(A[3], B[3], c_len.astype(np.int32), c_st, ptr, pairs, 0,
+                                len(c_off), out)
+    assert np.all(np.abs(out - want) <= 1e-5 * ab + 1e-30)
+
+
+def test_gemm_diag_formula_vs_dense(oracle):
+    rng = np.random.default_rng(7)
+    n = 40
+    for oa, ob in [(list(range(-3, 4)), list(range(-3, 4))), ([-17, -2, 0, 5, 30], [-30, 1, 9])]:
+        DA = oracle.pack_diag_matrix(n, oa, 42)
+        DB = oracle.pack_diag_matrix(n, ob, 137)
+        Ad = np.zeros((n, n)); Bd = np.zeros((n, n))
+        for i, d in enumerate(oa):
+            for t in range(n):
+                if 0 <= t + d < n:
+                    Ad[t, t + d] = DA[i, t]
+        for j, d in enumerate(ob):
+            for t in range(n):
+                if 0 <= t + d < n:
+                    Bd[t, t + d] = DB[j, t]
+        P = Ad @ Bd
+        c_off, c_len, c_st, nnz = oracle.c_structure(n, oa, ob)
+        got, _ = oracle.gemm_diag_f64(n, DA, oa, DB, ob, oracle.c_lookup(n, c_off), c_st, nnz)
+        for d, s, ln in zip(c_off, c_st, c_len):
+            sr, sc = (0, d) if d >= 0 else (-d, 0)
+            assert np.allclose(got[s:s + ln], P[sr + np.arange(ln), sc + np.arange(ln)],
+                               rtol=0, atol=1e-12)
+
+
+def test_reference_generators(oracle):
+    offs, starts, lens, vals = oracle.make_banded(100, 3, 1234)
+    assert offs.tolist() == list(range(-3, 4))
+    assert lens.tolist() == [100 - abs(d) for d in offs]
+    assert starts.tolist() == np.concatenate([[0], np.cumsum(lens)[:-1]]).tolist()
+    assert vals.min() >= -1 and vals.max() < 1
+    assert np.array_equal(vals, oracle.make_banded(100, 3, 1234)[3])
+    assert not np.array_equal(vals, oracle.make_banded(100, 3, 5678)[3])
+    DA = oracle.pack_diag_matrix(50, [-4, 0, 7], 42)
+    assert np.all(DA[0, :4] == 0) and np.all(DA[2, 43:] == 0)
+    nz = DA[DA != 0]
+    assert nz.size == 46 + 50 + 43 and nz.min() >= 0.5 and nz.max() < 1.5
