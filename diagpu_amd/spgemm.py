@@ -1,0 +1,134 @@
+"""Host-side SpGEMM calls over device tensors: the symbolic plan
+(diagpu_spgemm_symbolic) and the numeric phase (diagpu_spgemm_numeric_f32)
+for HM operands, and gemm_diag on row-packed operands
+(diagpu_rowpacked_as_hm + the same two phases).
+
+torch tensors only carry device memory and the stream.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import torch
+
+from . import _lib
+from .spmv import _stream_handle
+
+GPAIR_BYTES = C.sizeof(_lib.GPair)
+GPAIR_DTYPE = np.dtype([("ab", "<u8"), ("bb", "<u8"), ("ash", "<i4"), ("bsh", "<i4"),
+                        ("al", "<i4"), ("bl", "<i4")])
+
+
+def _check_dev(t: torch.Tensor, dtype, name: str):
+    if not t.is_cuda or t.dtype != dtype or not t.is_contiguous():
+        raise TypeError(f"{name} must be a contiguous {dtype} device tensor")
+
+
+class SpgemmPlan:
+    """C = A * B for HM operands (objects with n, offsets, lengths, starts,
+    int32/int32/int64 device tensors).  Builds the C structure and pair plan
+    on construction (one stream sync); numeric() then fills C values."""
+
+    def __init__(self, A, B, stream=None, want_lookup: bool = False):
+        if A.n != B.n:
+            raise ValueError("A and B must have the same dimension")
+        for M, nm in ((A, "A"), (B, "B")):
+            _check_dev(M.offsets, torch.int32, f"{nm}.offsets")
+            _check_dev(M.lengths, torch.int32, f"{nm}.lengths")
+            _check_dev(M.starts, torch.int64, f"{nm}.starts")
+        self.A, self.B, self.n = A, B, A.n
+        self.stream = stream
+        dev = A.offsets.device
+        na, nb = A.offsets.numel(), B.offsets.numel()
+        self.c_cap = max(1, min(na * nb, 2 * self.n - 1))
+        self.p_cap = max(1, na * nb)
+        ws = C.c_size_t(0)
+        _lib.call("diagpu_spgemm_symbolic_workspace", self.n, na, nb, C.byref(ws))
+        self.workspace = torch.empty(ws.value, dtype=torch.uint8, device=dev)
+        self.C_off = torch.empty(self.c_cap, dtype=torch.int32, device=dev)
+        self.C_len = torch.empty(self.c_cap, dtype=torch.int32, device=dev)
+        self.C_starts = torch.empty(self.c_cap, dtype=torch.int64, device=dev)
+        self.ptr = torch.empty(self.c_cap + 1, dtype=torch.int64, device=dev)
+        self.pairs = torch.empty(self.p_cap * GPAIR_BYTES, dtype=torch.uint8, device=dev)
+        self.lookup = (torch.empty(2 * self.n - 1, dtype=torch.int32, device=dev)
+                       if want_lookup else None)
+        self.info = _lib.SpgemmInfo()
+        self.symbolic()
+
+    def symbolic(self) -> None:
+        A, B = self.A, self.B
+        _lib.call("diagpu_spgemm_symbolic", self.n,
+                  A.offsets.data_ptr(), A.lengths.data_ptr(), A.starts.data_ptr(),
+                  A.offsets.numel(),
+                  B.offsets.data_ptr(), B.lengths.data_ptr(), B.starts.data_ptr(),
+                  B.offsets.numel(),
+                  self.C_off.data_ptr(), self.C_len.data_ptr(), self.C_starts.data_ptr(),
+                  self.c_cap, self.ptr.data_ptr(), self.pairs.data_ptr(), self.p_cap,
+                  self.lookup.data_ptr() if self.lookup is not None else None,
+                  self.workspace.data_ptr(), self.workspace.numel(),
+                  C.byref(self.info), _stream_handle(self.stream))
+
+    # structure views (device tensors) --------------------------------------
+    def c_offsets(self) -> torch.Tensor:
+        return self.C_off[: self.info.c_ndiag]
+
+    def c_lengths(self) -> torch.Tensor:
+        return self.C_len[: self.info.c_ndiag]
+
+    def c_starts(self) -> torch.Tensor:
+        return self.C_starts[: self.info.c_ndiag]
+
+    def pair_ptr(self) -> torch.Tensor:
+        return self.ptr[: self.info.c_ndiag + 1]
+
+    def pairs_numpy(self) -> np.ndarray:
+        raw = self.pairs[: self.info.n_pairs * GPAIR_BYTES].cpu().numpy()
+        return raw.view(GPAIR_DTYPE)
+
+    # numeric ---------------------------------------------------------------
+    def numeric(self, A_vals: torch.Tensor, B_vals: torch.Tensor, C_vals: torch.Tensor) -> None:
+        _check_dev(A_vals, torch.float32, "A_vals")
+        _check_dev(B_vals, torch.float32, "B_vals")
+        _check_dev(C_vals, torch.float32, "C_vals")
+        if C_vals.numel() < self.info.c_nnz:
+            raise ValueError(f"C_vals has {C_vals.numel()} elements, needs {self.info.c_nnz}")
+        st = _lib.load().diagpu_spgemm_numeric_f32(
+            self.n, A_vals.data_ptr(), B_vals.data_ptr(), self.C_off.data_ptr(),
+            self.C_len.data_ptr(), self.C_starts.data_ptr(), self.info.c_ndiag,
+            self.ptr.data_ptr(), self.pairs.data_ptr(), self.info.max_pairs,
+            C_vals.data_ptr(), _stream_handle(self.stream))
+        if st:
+            _lib.check(st)
+
+    def multiply(self, A_vals: torch.Tensor, B_vals: torch.Tensor) -> torch.Tensor:
+        Cv = torch.empty(max(1, self.info.c_nnz), dtype=torch.float32, device=A_vals.device)
+        self.numeric(A_vals, B_vals, Cv)
+        return Cv[: self.info.c_nnz]
+
+
+class RowPacked:
+    """A P x n row-packed operand (gemm_diag layout) addressed as HM."""
+
+    def __init__(self, n: int, offsets: torch.Tensor, DA: torch.Tensor, stream=None):
+        _check_dev(offsets, torch.int32, "offsets")
+        _check_dev(DA, torch.float32, "DA")
+        if DA.numel() != offsets.numel() * n:
+            raise ValueError("DA must hold ndiag * n values")
+        self.n = n
+        self.offsets = offsets
+        self.values = DA
+        self.starts = torch.empty(offsets.numel(), dtype=torch.int64, device=DA.device)
+        self.lengths = torch.empty(offsets.numel(), dtype=torch.int32, device=DA.device)
+        _lib.call("diagpu_rowpacked_as_hm", n, offsets.data_ptr(), offsets.numel(),
+                  self.starts.data_ptr(), self.lengths.data_ptr(), _stream_handle(stream))
+
+
+def gemm_diag(n: int, off_A: torch.Tensor, DA: torch.Tensor, off_B: torch.Tensor,
+              DB: torch.Tensor, stream=None):
+    """C = A * B for row-packed DA, DB (gemm_diag/gemm_diag.cu:9-15); returns
+    (plan, C values in the compact C layout)."""
+    A = RowPacked(n, off_A, DA, stream)
+    B = RowPacked(n, off_B, DB, stream)
+    plan = SpgemmPlan(A, B, stream=stream, want_lookup=True)
+    return plan, plan.multiply(DA, DB)

@@ -65,3 +65,41 @@ def test_python_wrapper_rejects_bad_tensors():
     from diagpu_amd.spmv import recon_view
     with pytest.raises(TypeError):
         recon_view(torch.zeros(2, dtype=torch.int32), torch.zeros(8), 4, 4)
+
+
+def test_spgemm_argument_errors():
+    lib = _lib.load()
+    sz = C.c_size_t(0)
+    assert lib.diagpu_spgemm_symbolic_workspace(0, 1, 1, C.byref(sz)) == _lib.ERR_ARG
+    assert lib.diagpu_spgemm_symbolic_workspace(100, -1, 1, C.byref(sz)) == _lib.ERR_ARG
+    assert lib.diagpu_spgemm_symbolic_workspace(100, 3, 4, None) == _lib.ERR_ARG
+    assert lib.diagpu_spgemm_symbolic_workspace(1 << 20, 9, 7, C.byref(sz)) == _lib.OK
+    # A lookup of 2n-1 int32 plus two bitmaps and a word prefix dominate
+    assert sz.value >= 4 * (2 * (1 << 20) - 1) + 3 * 4 * ((2 * (1 << 20)) // 32)
+    fake = C.c_void_p(0x1000)
+    info = _lib.SpgemmInfo()
+    args = [100, fake, fake, fake, 3, fake, fake, fake, 2, fake, fake, fake, 6, fake, fake, 6,
+            None, fake, 1 << 20, C.byref(info), None]
+    bad = list(args); bad[19] = None
+    assert lib.diagpu_spgemm_symbolic(*bad) == _lib.ERR_ARG
+    bad = list(args); bad[0] = 0
+    assert lib.diagpu_spgemm_symbolic(*bad) == _lib.ERR_ARG
+    bad = list(args); bad[1] = None
+    assert lib.diagpu_spgemm_symbolic(*bad) == _lib.ERR_ARG
+    bad = list(args); bad[13] = None
+    assert lib.diagpu_spgemm_symbolic(*bad) == _lib.ERR_ARG
+    bad = list(args); bad[18] = 16
+    assert lib.diagpu_spgemm_symbolic(*bad) == _lib.ERR_CAPACITY
+    assert b"workspace" in lib.diagpu_last_error()
+    # numeric
+    assert lib.diagpu_spgemm_numeric_f32(0, fake, fake, fake, fake, fake, 1, fake, fake, 1,
+                                         fake, None) == _lib.ERR_ARG
+    assert lib.diagpu_spgemm_numeric_f32(10, fake, fake, fake, fake, fake, 0, fake, fake, 0,
+                                         fake, None) == _lib.OK      # no C diagonals: no-op
+    assert lib.diagpu_spgemm_numeric_f32(10, fake, fake, None, fake, fake, 3, fake, fake, 1,
+                                         fake, None) == _lib.ERR_ARG
+    assert lib.diagpu_spgemm_numeric_f32(10, fake, fake, fake, fake, fake, 50, fake, fake, 1,
+                                         fake, None) == _lib.ERR_ARG  # > 2n - 1 diagonals
+    assert lib.diagpu_rowpacked_as_hm(0, fake, 1, fake, fake, None) == _lib.ERR_ARG
+    assert lib.diagpu_rowpacked_as_hm(10, None, 1, fake, fake, None) == _lib.ERR_ARG
+    assert lib.diagpu_rowpacked_as_hm(10, None, 0, None, None, None) == _lib.OK

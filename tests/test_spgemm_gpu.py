@@ -1,0 +1,247 @@
+"""SpGEMM and gemm_diag parity on the GPU, through the C ABI.
+
+Integer outputs (C offsets, lengths, starts, lookup, pair_ptr, every GPair
+field, counts) must equal the oracle's restatement of the reference planners
+bit for bit.  Values: |C - C64| <= 1e-5 * sum |a * b| per element, C64 the
+oracle's fp64 result (1e-5 relative to the absolute term sum; any fp32
+summation of <= 166 products satisfies it).
+"""
+import numpy as np
+import pytest
+import torch
+
+from diagpu_amd import _lib, workloads
+from diagpu_amd.spgemm import SpgemmPlan, gemm_diag
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def host(M):
+    return (M.offsets.cpu().numpy(), M.lengths.cpu().numpy(), M.starts.cpu().numpy(),
+            M.values.cpu().numpy())
+
+
+def check_plan(oracle, plan, A, B):
+    n = A.n
+    a, b = host(A), host(B)
+    c_off, c_len, c_st, nnz = oracle.c_structure(n, a[0], b[0])
+    assert plan.info.c_ndiag == len(c_off)
+    assert plan.info.c_nnz == nnz
+    assert np.array_equal(plan.c_offsets().cpu().numpy(), c_off)
+    assert np.array_equal(plan.c_lengths().cpu().numpy(), c_len)
+    assert np.array_equal(plan.c_starts().cpu().numpy(), c_st)
+    ptr, pairs = oracle.pairs_only(n, a[0], a[1], a[2], b[0], b[1], b[2], c_off)
+    assert np.array_equal(plan.pair_ptr().cpu().numpy(), ptr)
+    assert plan.info.n_pairs == ptr[-1]
+    got = plan.pairs_numpy()
+    for f in ("ab", "bb", "ash", "bsh", "al", "bl"):
+        assert np.array_equal(got[f], pairs[f]), f
+    counts = np.diff(ptr)
+    assert plan.info.max_pairs == (counts.max() if len(counts) else 0)
+    # useful flops: 2 * sum over pairs of n - max(|da|, |db|, |dc|)
+    dc = np.repeat(c_off.astype(np.int64), counts)
+    b_of = {int(s): int(o) for s, o in zip(b[2], b[0])}
+    db = np.array([b_of[int(s)] for s in pairs["bb"]], np.int64)
+    da = dc - db
+    assert plan.info.useful_flops == int(2 * (n - np.maximum(np.maximum(abs(da), abs(db)),
+                                                               abs(dc))).sum())
+    if plan.lookup is not None:
+        assert np.array_equal(plan.lookup.cpu().numpy(), oracle.c_lookup(n, c_off))
+    return c_off, c_len, c_st, nnz, ptr, pairs
+
+
+def check_values(got, want, absum):
+    err = np.abs(got.astype(np.float64) - want)
+    bad = err > TOL * absum + 1e-300
+    assert not bad.any(), f"{int(bad.sum())} values out of bound, max err {err.max():.3e}"
+
+
+def rand_case(rng, n, na, nb, span):
+    oa = rng.choice(np.arange(-span, span + 1), size=na, replace=False)
+    ob = rng.choice(np.arange(-span, span + 1), size=nb, replace=False)
+    return oa, ob
+
+
+@pytest.mark.parametrize("seed,n,na,nb,span", [
+    (0, 16, 3, 3, 15), (1, 37, 5, 4, 36), (2, 257, 9, 7, 256), (3, 1000, 12, 30, 999),
+    (4, 3001, 40, 8, 2999), (5, 5000, 3, 60, 100), (6, 1031, 64, 64, 1030),
+])
+def test_random_products(dev, oracle, seed, n, na, nb, span):
+    rng = np.random.default_rng(seed)
+    oa, ob = rand_case(rng, n, na, nb, span)
+    A = workloads.hm_random(n, oa, seed=seed, device=dev)
+    B = workloads.hm_random(n, ob, seed=seed + 100, device=dev)
+    if seed % 2:   # B in non-ascending order: plan order must follow B's array order
+        perm = torch.as_tensor(rng.permutation(nb), device=dev)
+        B = workloads.HM(n, B.offsets[perm].contiguous(), B.lengths[perm].contiguous(),
+                         B.starts[perm].contiguous(), B.values)
+    plan = SpgemmPlan(A, B, want_lookup=True)
+    c_off, c_len, c_st, nnz, ptr, pairs = check_plan(oracle, plan, A, B)
+    Cv = plan.multiply(A.values, B.values)
+    C2 = plan.multiply(A.values, B.values)
+    torch.cuda.synchronize()
+    assert torch.equal(Cv, C2), "run-to-run results differ"
+    want, ab = oracle.spgemm_pairs_f64(A.values.cpu().numpy(), B.values.cpu().numpy(), c_len,
+                                       c_st, ptr, pairs, 0, len(c_off))
+    check_values(Cv.cpu().numpy(), want, ab)
+    if n <= 300:   # brute-force dense product
+        from test_oracle import hm_to_dense
+        a, b = host(A), host(B)
+        P = hm_to_dense(n, a[0], a[2], a[3]) @ hm_to_dense(n, b[0], b[2], b[3])
+        g = Cv.cpu().numpy()
+        for d, s, ln in zip(c_off, c_st, c_len):
+            sr, sc = (0, d) if d >= 0 else (-d, 0)
+            assert np.allclose(g[s:s + ln], P[sr + np.arange(ln), sc + np.arange(ln)],
+                               rtol=0, atol=1e-5)
+
+
+def test_reference_bench_operands(dev, oracle):
+    """make_banded(100000, 16, 1234 / 5678) of spmspm/bench_spmspm.cu:465-466,
+    values checked against the cpu_dia_spgemm loop (:376-408) in fp64."""
+    n, w = 100000, 16
+    A = workloads.hm_from_values(n, oracle.make_banded(n, w, 1234)[0],
+                                 torch.as_tensor(oracle.make_banded(n, w, 1234)[3], device=dev),
+                                 device=dev)
+    B = workloads.hm_from_values(n, oracle.make_banded(n, w, 5678)[0],
+                                 torch.as_tensor(oracle.make_banded(n, w, 5678)[3], device=dev),
+                                 device=dev)
+    plan = SpgemmPlan(A, B)
+    c_off, c_len, c_st, nnz, ptr, pairs = check_plan(oracle, plan, A, B)
+    assert len(c_off) == 4 * w + 1
+    Cv = plan.multiply(A.values, B.values).cpu().numpy()
+    want, ab = oracle.spgemm_gather_f64(n, host(A), host(B), (c_off, c_len, c_st, nnz))
+    check_values(Cv, want, ab)
+
+
+def test_config4_full_size(dev, oracle):
+    A, B = workloads.spgemm_config(4, seed=4, device=dev)
+    plan = SpgemmPlan(A, B)
+    c_off, c_len, c_st, nnz, ptr, pairs = check_plan(oracle, plan, A, B)
+    assert (len(c_off), int(ptr[-1]), nnz) == (47, 63, 48_985_826)
+    Cv = plan.multiply(A.values, B.values).cpu().numpy()
+    want, ab = oracle.spgemm_pairs_f64(A.values.cpu().numpy(), B.values.cpu().numpy(), c_len,
+                                       c_st, ptr, pairs, 0, len(c_off))
+    check_values(Cv, want, ab)
+
+
+def _row_sums_gpu(plan, Cv, n):
+    """C 1 on the device in fp64: each C diagonal adds into its rows."""
+    rs = torch.zeros(n, dtype=torch.float64, device=Cv.device)
+    offs = plan.c_offsets().cpu().tolist()
+    lens = plan.c_lengths().cpu().tolist()
+    sts = plan.c_starts().cpu().tolist()
+    for d, ln, s in zip(offs, lens, sts):
+        r0 = -d if d < 0 else 0
+        rs[r0:r0 + ln] += Cv[s:s + ln].double()
+    return rs.cpu().numpy()
+
+
+def _hm_matvec(n, M, v):
+    """(M v) and (|M| |v|) in fp64 for an HM matrix on the host."""
+    off, ln, st, val = M
+    y = np.zeros(n)
+    ya = np.zeros(n)
+    for d, l, s in zip(off, ln, st):
+        r0, c0 = (0, d) if d >= 0 else (-d, 0)
+        seg = val[s:s + l].astype(np.float64)
+        y[r0:r0 + l] += seg * v[c0:c0 + l]
+        ya[r0:r0 + l] += np.abs(seg) * np.abs(v[c0:c0 + l])
+    return y, ya
+
+
+def test_config5_full_size(dev, oracle):
+    """n = 262144, 128 x 128 random offsets: plan exact; values exact to the
+    bound on a sample of C diagonals; all of C through C 1 = A (B 1)."""
+    A, B = workloads.spgemm_config(5, seed=5, device=dev)
+    plan = SpgemmPlan(A, B)
+    c_off, c_len, c_st, nnz, ptr, pairs = check_plan(oracle, plan, A, B)
+    assert nnz > 2**31                       # int64 starts are required
+    Cv = plan.multiply(A.values, B.values)
+    torch.cuda.synchronize()
+    Av, Bv = A.values.cpu().numpy(), B.values.cpu().numpy()
+    rng = np.random.default_rng(0)
+    counts = np.diff(ptr)
+    ks = sorted({0, len(c_off) - 1, int(np.argmax(counts)), *rng.choice(len(c_off), 48).tolist()})
+    for k in ks:
+        want, ab = oracle.spgemm_pairs_f64(Av, Bv, c_len, c_st, ptr, pairs, k, k + 1)
+        got = Cv[int(c_st[k]):int(c_st[k]) + int(c_len[k])].cpu().numpy()
+        check_values(got, want, ab)
+    n = A.n
+    rs = _row_sums_gpu(plan, Cv, n)
+    b1, b1a = _hm_matvec(n, host(B), np.ones(n))
+    ab1, bound = _hm_matvec(n, host(A), b1)
+    _, bound = _hm_matvec(n, host(A), b1a)
+    assert np.all(np.abs(rs - ab1) <= TOL * bound + 1e-300)
+
+
+@pytest.mark.parametrize("n,offs_a,offs_b", [
+    (4096, list(range(-10, 11)), list(range(-10, 11))),          # gemm_diag.cu:467-486 defaults
+    (3000, [-700, -9, -2, 0, 1, 33, 512], [-1000, -5, 0, 3, 4, 900]),   # non-contiguous offsets
+    (1025, [-1024, 0, 1024], [-1, 1]),
+])
+def test_gemm_diag(dev, oracle, n, offs_a, offs_b):
+    DA = oracle.pack_diag_matrix(n, offs_a, 42)
+    DB = oracle.pack_diag_matrix(n, offs_b, 137)
+    oa = torch.tensor(offs_a, dtype=torch.int32, device=dev)
+    ob = torch.tensor(offs_b, dtype=torch.int32, device=dev)
+    plan, Cv = gemm_diag(n, oa, torch.as_tensor(DA, device=dev).reshape(-1), ob,
+                         torch.as_tensor(DB, device=dev).reshape(-1))
+    c_off, c_len, c_st, nnz = oracle.c_structure(n, offs_a, offs_b)
+    assert np.array_equal(plan.c_offsets().cpu().numpy(), c_off)
+    assert np.array_equal(plan.c_starts().cpu().numpy(), c_st)
+    lk = oracle.c_lookup(n, c_off)
+    assert np.array_equal(plan.lookup.cpu().numpy(), lk)
+    want, ab = oracle.gemm_diag_f64(n, DA, offs_a, DB, offs_b, lk, c_st, nnz)
+    got = Cv.cpu().numpy()
+    check_values(got, want, ab)
+    assert np.max(np.abs(got - want)) < 1e-1          # the reference's own bound (:544)
+
+
+def _hm_dev(dev, n, offs, lens=None):
+    offs = list(offs)
+    lens = lens or [n - abs(d) for d in offs]
+    st = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+    return workloads.HM(n, torch.tensor(offs, dtype=torch.int32, device=dev),
+                        torch.tensor(lens, dtype=torch.int32, device=dev),
+                        torch.tensor(st, device=dev),
+                        torch.zeros(max(1, sum(lens)), device=dev))
+
+
+@pytest.mark.parametrize("offs_a,offs_b,lens_a,status", [
+    ([0, 3, 3], [0, 1], None, _lib.ERR_DUPLICATE),
+    ([0, 1], [-2, -2], None, _lib.ERR_DUPLICATE),
+    ([0, 100], [1], None, _lib.ERR_OFFSET),          # |d| >= n
+    ([0, -5], [1], [100, 94], _lib.ERR_OFFSET),      # length != n - |d|
+])
+def test_invalid_operands(dev, offs_a, offs_b, lens_a, status):
+    n = 100
+    A = _hm_dev(dev, n, offs_a, lens_a)
+    B = _hm_dev(dev, n, offs_b)
+    with pytest.raises(_lib.DiagpuError) as ei:
+        SpgemmPlan(A, B)
+    assert ei.value.status == status
+
+
+def test_capacity_and_empty(dev):
+    n = 64
+    A = _hm_dev(dev, n, [-3, 0, 3])
+    B = _hm_dev(dev, n, [-1, 1])
+    plan = SpgemmPlan(A, B)
+    assert plan.info.c_ndiag == 6 and plan.info.n_pairs == 6
+    plan.p_cap = 5
+    with pytest.raises(_lib.DiagpuError) as ei:
+        plan.symbolic()
+    assert ei.value.status == _lib.ERR_CAPACITY
+    plan.p_cap, plan.c_cap = 6, 5
+    with pytest.raises(_lib.DiagpuError) as ei:
+        plan.symbolic()
+    assert ei.value.status == _lib.ERR_CAPACITY
+    E = _hm_dev(dev, n, [])
+    p2 = SpgemmPlan(A, E)
+    assert (p2.info.c_ndiag, p2.info.n_pairs, p2.info.c_nnz) == (0, 0, 0)
+    assert p2.pair_ptr().cpu().tolist() == [0]
+    # offsets whose sums all leave the matrix
+    F = _hm_dev(dev, n, [60, 63])
+    p3 = SpgemmPlan(F, _hm_dev(dev, n, [10, 20]))
+    assert p3.info.c_ndiag == 0
