@@ -12,8 +12,14 @@
 // Work decomposition.  An item is (row block rb, C diagonal k): the 1024
 // positions of diagonal k whose matrix rows fall in block rb (shifted by at
 // most 3 so the item's first C element is 16-byte aligned).  Each lane owns 4
-// consecutive positions: one aligned 128-bit store of C and, per plan entry,
-// one 128-bit load each of A and B (dword aligned).
+// consecutive positions: one aligned 128-bit streaming store of C and, per
+// plan entry, one 128-bit load each of A and B (dword aligned).  A workgroup
+// takes a batch of 16 consecutive C diagonals of one row block: their
+// metadata and plan entries (1.7 per diagonal on average) are resolved once
+// into LDS, then the flattened entry list is walked in chunks whose loads are
+// all in flight together, across C-diagonal boundaries.  The C stores are
+// non-temporal so the 10 GB output stream does not evict the operands from
+// L2.
 //
 // Row-space locality.  In row coordinates the entry (da, db) of C row i
 // reads A(i, i + da) and B(i + da, i + dc): every A diagonal at rows i, every
@@ -31,113 +37,180 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kTB = kBlock * 4;   // positions per item
-constexpr int kPairChunk = 4;     // plan entries whose loads are issued together
+constexpr int kBatch = 16;        // consecutive C diagonals per batch
 
 typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
 typedef float f4a __attribute__((ext_vector_type(4), aligned(16)));
 
 __device__ __forceinline__ f4u ld4(const float* p) { return *reinterpret_cast<const f4u*>(p); }
 
-struct PairVals {
-    f4u a, b;
-    uint32_t valid;   // bit e: position e of the quad has both operands in range
+// One C diagonal of the current batch, for the current row block.
+struct DiagRec {
+    int64_t P0;     // first position of the item (may lie outside [0, len))
+    int64_t cst;    // C_starts
+    int32_t len;    // C_len
+    int32_t pad0;
+    int64_t pad1;
 };
 
+// One plan entry of the current batch, resolved for the current row block.
+struct PairRec {
+    int64_t a_base;   // A index of position 0 (ab + ash)
+    int64_t b_base;   // B index of position 0 (bb + bsh)
+    int32_t plo, phi; // positions where both operands exist, within [0, len)
+    int32_t ci;       // C diagonal within the batch
+    int32_t cover;    // 1: covers the whole item, 0: part of it, -1: none of it
+};
+
+template <int PC>
 __global__ __launch_bounds__(kBlock) void k_gather(
-    int32_t n, const float* __restrict__ Av, const float* __restrict__ Bv,
+    const float* __restrict__ Av, const float* __restrict__ Bv,
     const int32_t* __restrict__ C_off, const int32_t* __restrict__ C_len,
     const int64_t* __restrict__ C_starts, int32_t nC, const int64_t* __restrict__ pair_ptr,
     const diagpu_gpair* __restrict__ pairs, float* __restrict__ Cv, int32_t NB,
     int32_t nb_per_xcd, int32_t wg_per_xcd)
 {
-    (void)n;
+    __shared__ DiagRec drec[kBatch];
+    __shared__ int64_t ptr_s[kBatch + 1];
+    __shared__ PairRec prec[kBlock];
+
     const int xcd = (int)(blockIdx.x % kNumXcd);
     const int l = (int)(blockIdx.x / kNumXcd);
     const int rb0 = xcd * nb_per_xcd;
     const int rb_end = (rb0 + nb_per_xcd) < NB ? (rb0 + nb_per_xcd) : NB;
     if (rb0 >= rb_end || nC <= 0) return;
+    const int nbat = (nC + kBatch - 1) / kBatch;
+    const int t = (int)threadIdx.x;
+    const int64_t p_lane = (int64_t)t * 4;
+    const int64_t nwork = (int64_t)(rb_end - rb0) * nbat;
 
-    // Item (rb, k) for j = l, l + L, l + 2L, ...: k advances by L mod nC.
-    int rb = rb0 + l / nC;
-    int k = l % nC;
-    const int lane4 = (int)threadIdx.x * 4;
+    for (int64_t j = l; j < nwork; j += wg_per_xcd) {
+        const int rb = rb0 + (int)(j / nbat);
+        const int kb = (int)(j % nbat) * kBatch;
+        const int gv = (nC - kb) < kBatch ? (nC - kb) : kBatch;
 
-    while (rb < rb_end) {
-        const int dc = C_off[k];
-        const int lenC = C_len[k];
-        const int64_t cst = C_starts[k];
-        const int mc = dc < 0 ? dc : 0;
-        const int delta = (int)((cst + mc) & 3);
-        const int64_t P0 = (int64_t)rb * kTB + mc - delta;
+        __syncthreads();   // previous batch done with drec/ptr_s/prec
+        if (t <= gv) ptr_s[t] = pair_ptr[kb + t];
+        if (t < gv) {
+            const int dc = C_off[kb + t];
+            const int64_t cst = C_starts[kb + t];
+            const int mc = dc < 0 ? dc : 0;
+            DiagRec d;
+            d.P0 = (int64_t)rb * kTB + mc - (int)((cst + mc) & 3);
+            d.cst = cst;
+            d.len = C_len[kb + t];
+            d.pad0 = 0;
+            d.pad1 = 0;
+            drec[t] = d;
+        }
+        __syncthreads();
 
-        if (P0 < lenC && P0 + kTB > 0) {
-            const int64_t g0 = pair_ptr[k], g1 = pair_ptr[k + 1];
-            const bool item_full = P0 >= 0 && P0 + kTB <= lenC;
-            const int64_t p = P0 + lane4;
-            float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
-
-            for (int64_t g = g0; g < g1; g += kPairChunk) {
-                diagpu_gpair gp[kPairChunk];
-#pragma unroll
-                for (int c = 0; c < kPairChunk; ++c)
-                    if (g + c < g1) gp[c] = pairs[g + c];
-                PairVals pv[kPairChunk];
-#pragma unroll
-                for (int c = 0; c < kPairChunk; ++c) {
-                    if (g + c >= g1) continue;
-                    const int ash = gp[c].ash, bsh = gp[c].bsh, al = gp[c].al, bl = gp[c].bl;
-                    const float* __restrict__ ap = Av + gp[c].ab + ash;
-                    const float* __restrict__ bp = Bv + gp[c].bb + bsh;
-                    const bool full = item_full && P0 + ash >= 0 && P0 + kTB + ash <= al &&
-                                      P0 + bsh >= 0 && P0 + kTB + bsh <= bl;
-                    if (full) {
-                        pv[c].a = ld4(ap + p);
-                        pv[c].b = ld4(bp + p);
-                        pv[c].valid = 0xF;
-                    } else {
-                        float a[4], b[4];
-                        uint32_t v = 0;
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const int64_t q = p + e;
-                            const bool ok = q >= 0 && q < lenC && q + ash >= 0 && q + ash < al &&
-                                            q + bsh >= 0 && q + bsh < bl;
-                            a[e] = ok ? ap[q] : 0.f;
-                            b[e] = ok ? bp[q] : 0.f;
-                            v |= ok ? (1u << e) : 0u;
-                        }
-                        pv[c].a = f4u{a[0], a[1], a[2], a[3]};
-                        pv[c].b = f4u{b[0], b[1], b[2], b[3]};
-                        pv[c].valid = v;
-                    }
-                }
-#pragma unroll
-                for (int c = 0; c < kPairChunk; ++c) {
-                    if (g + c >= g1) continue;
-                    const uint32_t v = pv[c].valid;
-                    acc0 = (v & 1) ? __builtin_fmaf(pv[c].a.x, pv[c].b.x, acc0) : acc0;
-                    acc1 = (v & 2) ? __builtin_fmaf(pv[c].a.y, pv[c].b.y, acc1) : acc1;
-                    acc2 = (v & 4) ? __builtin_fmaf(pv[c].a.z, pv[c].b.z, acc2) : acc2;
-                    acc3 = (v & 8) ? __builtin_fmaf(pv[c].a.w, pv[c].b.w, acc3) : acc3;
-                }
-            }
-
-            float* __restrict__ cp = Cv + cst;
-            if (item_full) {
-                *reinterpret_cast<f4a*>(cp + p) = f4a{acc0, acc1, acc2, acc3};
-            } else {
+        const int64_t gb = ptr_s[0], ge = ptr_s[gv];
+        float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+        int cur = -1;
+        auto flush = [&](int ci) {
+            const DiagRec d = drec[ci];
+            const int64_t p = d.P0 + p_lane;
+            float* __restrict__ cp = Cv + d.cst;
+            if (d.P0 >= 0 && d.P0 + kTB <= d.len) {
+                __builtin_nontemporal_store(f4a{acc0, acc1, acc2, acc3}, reinterpret_cast<f4a*>(cp + p));
+            } else if (d.P0 < d.len && d.P0 + kTB > 0) {
                 const float r[4] = {acc0, acc1, acc2, acc3};
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    if (p + e >= 0 && p + e < lenC) cp[p + e] = r[e];
+                    if (p + e >= 0 && p + e < d.len) cp[p + e] = r[e];
+            }
+        };
+
+        for (int64_t gq = gb; gq < ge; gq += kBlock) {
+            const int cnt = (ge - gq) < kBlock ? (int)(ge - gq) : kBlock;
+            __syncthreads();
+            if (t < cnt) {
+                const diagpu_gpair g = pairs[gq + t];
+                int ci = 0;
+                for (int c = 1; c < gv; ++c) ci += (ptr_s[c] <= gq + t) ? 1 : 0;
+                const DiagRec d = drec[ci];
+                PairRec r;
+                r.a_base = (int64_t)g.ab + g.ash;
+                r.b_base = (int64_t)g.bb + g.bsh;
+                int lo = 0, hi = d.len;
+                lo = -g.ash > lo ? -g.ash : lo;
+                lo = -g.bsh > lo ? -g.bsh : lo;
+                hi = g.al - g.ash < hi ? g.al - g.ash : hi;
+                hi = g.bl - g.bsh < hi ? g.bl - g.bsh : hi;
+                r.plo = lo;
+                r.phi = hi;
+                r.ci = ci;
+                r.cover = (d.P0 >= lo && d.P0 + kTB <= hi) ? 1
+                          : ((d.P0 + kTB > lo && d.P0 < hi) ? 0 : -1);
+                prec[t] = r;
+            }
+            __syncthreads();
+
+            for (int s0 = 0; s0 < cnt; s0 += PC) {
+                // A chunk in which no entry covers only part of the item takes
+                // the straight-line path: all 2*PC quad loads are issued before
+                // the first FMA (a masked element path in the same block would
+                // make the compiler drain the loads at its merge point).
+                bool fast = true;
+#pragma unroll
+                for (int c = 0; c < PC; ++c)
+                    if (s0 + c < cnt && prec[s0 + c].cover == 0) fast = false;
+                if (fast) {
+                    f4u a[PC], b[PC];
+#pragma unroll
+                    for (int c = 0; c < PC; ++c) {
+                        if (s0 + c < cnt && prec[s0 + c].cover > 0) {
+                            const PairRec r = prec[s0 + c];
+                            const int64_t p = drec[r.ci].P0 + p_lane;
+                            a[c] = ld4(Av + r.a_base + p);
+                            b[c] = ld4(Bv + r.b_base + p);
+                        }
+                    }
+#pragma unroll
+                    for (int c = 0; c < PC; ++c) {
+                        if (s0 + c >= cnt) continue;
+                        const PairRec r = prec[s0 + c];
+                        if (r.ci != cur) {
+                            if (cur >= 0) flush(cur);
+                            acc0 = acc1 = acc2 = acc3 = 0.f;
+                            cur = r.ci;
+                        }
+                        if (r.cover > 0) {
+                            acc0 = __builtin_fmaf(a[c].x, b[c].x, acc0);
+                            acc1 = __builtin_fmaf(a[c].y, b[c].y, acc1);
+                            acc2 = __builtin_fmaf(a[c].z, b[c].z, acc2);
+                            acc3 = __builtin_fmaf(a[c].w, b[c].w, acc3);
+                        }
+                    }
+                } else {
+                    for (int c = 0; c < PC && s0 + c < cnt; ++c) {
+                        const PairRec r = prec[s0 + c];
+                        if (r.ci != cur) {
+                            if (cur >= 0) flush(cur);
+                            acc0 = acc1 = acc2 = acc3 = 0.f;
+                            cur = r.ci;
+                        }
+                        if (r.cover < 0) continue;
+                        const int64_t p = drec[r.ci].P0 + p_lane;
+                        float av[4], bv[4];
+                        bool ok[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int64_t x = p + e;
+                            ok[e] = x >= r.plo && x < r.phi;
+                            av[e] = ok[e] ? Av[r.a_base + x] : 0.f;
+                            bv[e] = ok[e] ? Bv[r.b_base + x] : 0.f;
+                        }
+                        acc0 = ok[0] ? __builtin_fmaf(av[0], bv[0], acc0) : acc0;
+                        acc1 = ok[1] ? __builtin_fmaf(av[1], bv[1], acc1) : acc1;
+                        acc2 = ok[2] ? __builtin_fmaf(av[2], bv[2], acc2) : acc2;
+                        acc3 = ok[3] ? __builtin_fmaf(av[3], bv[3], acc3) : acc3;
+                    }
+                }
             }
         }
-
-        k += wg_per_xcd;
-        while (k >= nC) {
-            k -= nC;
-            ++rb;
-        }
+        if (cur >= 0) flush(cur);
     }
 }
 
@@ -166,13 +239,21 @@ DIAGPU_API int diagpu_spgemm_numeric_f32(
 
     const int32_t NB = (int32_t)ceil_div<int64_t>((int64_t)n + 3, kTB);
     const int32_t nb_per_xcd = ceil_div<int32_t>(NB, kNumXcd);
-    const int64_t items_per_xcd = (int64_t)nb_per_xcd * c_ndiag;
-    int64_t wg = (int64_t)(cu_count() / kNumXcd) * 4;       // 4 workgroups per CU
-    if (wg > items_per_xcd) wg = items_per_xcd;
+    // Many C diagonals (wide operands): 4-entry chunks, 4 workgroups per CU;
+    // few: 8-entry chunks and 8 workgroups per CU for more loads in flight.
+    const bool wide = c_ndiag >= 1024;
+    const int64_t batches_per_xcd = (int64_t)nb_per_xcd * ceil_div<int64_t>(c_ndiag, kBatch);
+    int64_t wg = (int64_t)(cu_count() / kNumXcd) * (wide ? 4 : 8);
+    if (wg > batches_per_xcd) wg = batches_per_xcd;
     if (wg < 1) wg = 1;
-    hipLaunchKernelGGL(k_gather, dim3((unsigned)(wg * kNumXcd)), dim3(kBlock), 0,
-                       as_stream(stream), n, A_vals, B_vals, C_off, C_len, C_starts,
-                       (int32_t)c_ndiag, pair_ptr, pairs, C_vals, NB, nb_per_xcd, (int32_t)wg);
+    if (wide)
+        hipLaunchKernelGGL(k_gather<4>, dim3((unsigned)(wg * kNumXcd)), dim3(kBlock), 0,
+                           as_stream(stream), A_vals, B_vals, C_off, C_len, C_starts,
+                           (int32_t)c_ndiag, pair_ptr, pairs, C_vals, NB, nb_per_xcd, (int32_t)wg);
+    else
+        hipLaunchKernelGGL(k_gather<8>, dim3((unsigned)(wg * kNumXcd)), dim3(kBlock), 0,
+                           as_stream(stream), A_vals, B_vals, C_off, C_len, C_starts,
+                           (int32_t)c_ndiag, pair_ptr, pairs, C_vals, NB, nb_per_xcd, (int32_t)wg);
     return check_launch(fn);
 }
 

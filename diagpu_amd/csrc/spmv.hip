@@ -14,10 +14,11 @@
 // Recon[k][r+d_k .. r+d_k+3] and x[r+d_k .. r+d_k+3]: both are contiguous
 // quads at the same column, so one 128-bit load each (dword-aligned: gfx950
 // serves unaligned global loads), and the 64 lanes of a wave cover 1 KiB of
-// each stream.  Diagonals are processed in chunks of 8 whose 16 loads are all
-// issued before the first FMA, so a lane keeps 16 quads in flight.  The
-// diagonal offsets are wave-uniform and come in through the scalar cache.
-// Tiles whose rows and columns are all in range (every tile of a large
+// each stream.  Diagonals are processed in chunks of 4 whose 8 loads are all
+// issued before the first FMA (a larger chunk costs more VGPRs than its
+// extra loads in flight buy back in occupancy).  Value loads and the y store
+// are non-temporal: each value is used once, while x stays in L2 for the
+// tiles that re-read it.  The diagonal offsets are wave-uniform.  Tiles whose rows and columns are all in range (every tile of a large
 // matrix except the first and last few) run without per-element bounds
 // checks; the others take a checked path.
 //
@@ -35,7 +36,7 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kRowsPerLane = 4;
 constexpr int kTile = kBlock * kRowsPerLane;   // rows per workgroup
-constexpr int kChunk = 8;                       // diagonals per load batch
+constexpr int kChunk = 4;                       // diagonals per load batch
 
 template <typename T> struct QuadOf;
 template <> struct QuadOf<float> {
@@ -51,10 +52,18 @@ __device__ __forceinline__ typename QuadOf<T>::type load_quad(const T* p)
     return *reinterpret_cast<const typename QuadOf<T>::type*>(p);
 }
 
+// Streaming (non-temporal) load: the value stream is read once, so it should
+// not displace x, which neighbouring tiles re-read from L2.
 template <typename T>
-__device__ __forceinline__ void store_quad(T* p, typename QuadOf<T>::type v)
+__device__ __forceinline__ typename QuadOf<T>::type load_quad_stream(const T* p)
 {
-    *reinterpret_cast<typename QuadOf<T>::type*>(p) = v;
+    return __builtin_nontemporal_load(reinterpret_cast<const typename QuadOf<T>::type*>(p));
+}
+
+template <typename T>
+__device__ __forceinline__ void store_quad_stream(T* p, typename QuadOf<T>::type v)
+{
+    __builtin_nontemporal_store(v, reinterpret_cast<typename QuadOf<T>::type*>(p));
 }
 
 __device__ __forceinline__ float fma_(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
@@ -122,7 +131,7 @@ __global__ __launch_bounds__(kBlock) void spmv_recon_kernel(
 #pragma unroll
                 for (int j = 0; j < kChunk; ++j) {
                     if (k0 + j < gn) {
-                        a[j] = load_quad<T>(vg + (int64_t)(k0 + j) * cols + d[j]);
+                        a[j] = load_quad_stream<T>(vg + (int64_t)(k0 + j) * cols + d[j]);
                         b[j] = load_quad<T>(xr + d[j]);
                     }
                 }
@@ -137,7 +146,7 @@ __global__ __launch_bounds__(kBlock) void spmv_recon_kernel(
                 }
             }
         }
-        store_quad<T>(y + r, acc);
+        store_quad_stream<T>(y + r, acc);
         return;
     }
 
