@@ -1,0 +1,125 @@
+// SpMV host API of spmv/src/dia_reconstruct.cuh, over libdiagpu.
+//
+// Same type names, members and semantics as the reference header, so code
+// written against it compiles unchanged with hipcc after swapping the
+// include: DiaMatrix, ReconMatrix, build_recon, ReconView and
+// launch_tc_spmv_regdirect.  The launcher runs the gfx950 FP32 kernel
+// (diagpu_spmv_recon_f32) instead of the TF32 MMA; results are the exact-FP32
+// sum, i.e. at least as accurate.  Failures throw diagpu::Error (the
+// reference returned void and left errors to cudaGetLastError).
+#pragma once
+
+#include <algorithm>
+#include <cstdint>
+#include <functional>
+#include <type_traits>
+#include <vector>
+
+#include "common.hpp"
+
+// Host-side compact DIA matrix (spmv/src/dia_reconstruct.cuh:52-59).
+struct DiaMatrix {
+    int                rows;
+    int                cols;
+    std::vector<int>   offsets;
+    std::vector<int>   diag_starts;
+    std::vector<int>   diag_lengths;
+    std::vector<float> values;
+};
+
+// Host-side K x cols Recon matrix (:64-70): row k holds diagonal
+// diag_offsets[k] at columns [max(d,0), max(d,0) + len), offsets descending.
+struct ReconMatrix {
+    int                rows;
+    int                cols;
+    int                num_diags;
+    std::vector<int>   diag_offsets;
+    std::vector<float> values;
+};
+
+// build_recon (:77-107): offsets sorted descending; row k receives the values
+// of the first input diagonal whose offset equals d_k.
+inline ReconMatrix build_recon(const DiaMatrix& H)
+{
+    ReconMatrix R;
+    R.rows = H.rows;
+    R.cols = H.cols;
+    R.num_diags = static_cast<int>(H.offsets.size());
+    R.diag_offsets = H.offsets;
+    std::sort(R.diag_offsets.begin(), R.diag_offsets.end(), std::greater<int>());
+    R.values.assign(static_cast<size_t>(R.num_diags) * static_cast<size_t>(R.cols), 0.0f);
+    for (int k = 0; k < R.num_diags; ++k) {
+        const int d = R.diag_offsets[k];
+        const auto it = std::find(H.offsets.begin(), H.offsets.end(), d);
+        const size_t di = static_cast<size_t>(it - H.offsets.begin());
+        const int first_col = d > 0 ? d : 0;
+        const int len = H.diag_lengths[di];
+        const float* src = H.values.data() + H.diag_starts[di];
+        std::copy(src, src + len,
+                  R.values.begin() + static_cast<std::ptrdiff_t>(k) * R.cols + first_col);
+    }
+    return R;
+}
+
+// Non-owning device view (:112-118).  Layout-identical to the C ABI's
+// diagpu_recon_view_f32.
+struct ReconView {
+    int          rows;
+    int          cols;
+    int          num_diags;
+    const int*   diag_offsets;   // device [num_diags]
+    const float* values;         // device [num_diags * cols]
+};
+static_assert(sizeof(ReconView) == sizeof(diagpu_recon_view_f32) &&
+                  offsetof(ReconView, diag_offsets) == offsetof(diagpu_recon_view_f32, diag_offsets) &&
+                  offsetof(ReconView, values) == offsetof(diagpu_recon_view_f32, values),
+              "ReconView must match diagpu_recon_view_f32");
+
+// y = H x on `stream` (:139-144; tc_spmv_regdirect_kernel.cu:135-147): y is
+// overwritten, rows == 0 is a no-op, asynchronous, allocates nothing.
+inline void launch_tc_spmv_regdirect(ReconView R, const float* d_x, int x_size, float* d_y,
+                                     hipStream_t stream = 0)
+{
+    diagpu::check(diagpu_spmv_recon_f32(reinterpret_cast<const diagpu_recon_view_f32*>(&R), d_x,
+                                        x_size, d_y, stream));
+}
+
+namespace diagpu {
+
+// The same SpMV under its own name, and the fp64 variant.
+inline void launch_dia_spmv(ReconView R, const float* d_x, int64_t x_size, float* d_y,
+                            hipStream_t stream = 0)
+{
+    check(diagpu_spmv_recon_f32(reinterpret_cast<const diagpu_recon_view_f32*>(&R), d_x, x_size,
+                                d_y, stream));
+}
+
+struct ReconViewF64 {
+    int           rows;
+    int           cols;
+    int           num_diags;
+    const int*    diag_offsets;
+    const double* values;
+};
+
+inline void launch_dia_spmv(ReconViewF64 R, const double* d_x, int64_t x_size, double* d_y,
+                            hipStream_t stream = 0)
+{
+    check(diagpu_spmv_recon_f64(reinterpret_cast<const diagpu_recon_view_f64*>(&R), d_x, x_size,
+                                d_y, stream));
+}
+
+// Owning device copy of a ReconMatrix with its view.
+struct DeviceRecon {
+    DeviceArray<int> offsets;
+    DeviceArray<float> values;
+    ReconView view{};
+
+    explicit DeviceRecon(const ReconMatrix& R)
+        : offsets(R.diag_offsets), values(R.values)
+    {
+        view = ReconView{R.rows, R.cols, R.num_diags, offsets.data(), values.data()};
+    }
+};
+
+}  // namespace diagpu

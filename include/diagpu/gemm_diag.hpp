@@ -1,0 +1,80 @@
+// gemm_diag (gemm_diag/gemm_diag.cu) over libdiagpu: row-packed operands,
+// compact C.
+//
+//   C[k][t] = sum_{i + j = k} DA[i][t] * DB[j][t + d_i]        (:9-15)
+//
+// DA / DB are P x n / Q x n row-packed arrays (DA[i][t] = A[t, t + d_i], zero
+// elsewhere; pack_diag_matrix, :362-382).  C uses the compact layout of
+// build_c_layout (:388-423), with int64 offsets.  The product is exact for
+// any offset sets (the reference kernel's 7-entry k-map per 4x4 tile drops
+// terms for non-contiguous offsets); C is overwritten, so no memset first.
+#pragma once
+
+#include <cstdint>
+#include <vector>
+
+#include "common.hpp"
+#include "spgemm.hpp"
+
+namespace diagpu {
+
+// build_c_layout (gemm_diag.cu:388-423) with 64-bit C offsets.
+struct CLayout {
+    std::vector<int64_t> C_offsets;   // start of each C diagonal
+    std::vector<int> C_lens;
+    std::vector<int> k_to_idx;        // 2n - 1 entries
+    std::vector<int> k_list;          // C diagonal offsets, ascending
+    int64_t total_c = 0;
+    int num_k = 0;
+};
+
+inline CLayout build_c_layout(int n, const std::vector<int>& off_A, const std::vector<int>& off_B)
+{
+    std::vector<int> la, lb;
+    for (int d : off_A) la.push_back(n - std::abs(d));
+    for (int d : off_B) lb.push_back(n - std::abs(d));
+    const auto r = run_symbolic(n, off_A, la, hm_starts(n, off_A), off_B, lb, hm_starts(n, off_B), true);
+    CLayout L;
+    L.C_offsets = r.C_starts;
+    L.C_lens = r.C_len;
+    L.k_to_idx = r.lookup;
+    L.k_list = r.C_off;
+    L.total_c = r.info.c_nnz;
+    L.num_k = static_cast<int>(r.info.c_ndiag);
+    return L;
+}
+
+// Device gemm_diag: row-packed DA (P x n) and DB (Q x n) with device offsets.
+// Builds the HM addressing of both operands and the plan at construction;
+// run() computes C (info().c_nnz values) on `stream`.
+class GemmDiag {
+public:
+    GemmDiag(int n, const int* d_off_A, int P, const int* d_off_B, int Q, hipStream_t stream = 0)
+        : n_(n), sa_(P), la_(P), sb_(Q), lb_(Q)
+    {
+        check(diagpu_rowpacked_as_hm(n, d_off_A, P, sa_.data(), la_.data(), stream));
+        check(diagpu_rowpacked_as_hm(n, d_off_B, Q, sb_.data(), lb_.data(), stream));
+        plan_ = new SpgemmPlan(n, d_off_A, la_.data(), sa_.data(), P, d_off_B, lb_.data(), sb_.data(),
+                               Q, true, stream);
+    }
+    GemmDiag(const GemmDiag&) = delete;
+    GemmDiag& operator=(const GemmDiag&) = delete;
+    ~GemmDiag() { delete plan_; }
+
+    void run(const float* d_DA, const float* d_DB, float* d_C, hipStream_t stream = 0) const
+    {
+        plan_->numeric(d_DA, d_DB, d_C, stream);
+    }
+    const SpgemmPlan& plan() const { return *plan_; }
+    const diagpu_spgemm_info& info() const { return plan_->info(); }
+
+private:
+    int n_;
+    DeviceArray<int64_t> sa_;
+    DeviceArray<int> la_;
+    DeviceArray<int64_t> sb_;
+    DeviceArray<int> lb_;
+    SpgemmPlan* plan_ = nullptr;
+};
+
+}  // namespace diagpu

@@ -1,0 +1,317 @@
+// DIA x DIA SpGEMM host API of spmspm/paper_hm.cuh and spmspm/gather_flat.cuh,
+// over libdiagpu.
+//
+// HMMatrix, dense_to_hm, hm_to_dense, compute_c_hm_structure,
+// build_c_diag_lookup, GPair, PairPlan, build_pairs_only, FlatPlan and
+// build_flat_plan keep the reference names and meanings.  Two deliberate
+// differences: element starts and totals are int64 (the reference's int
+// overflows once C exceeds 2^31 values), and the integer planners run as the
+// GPU symbolic phase (diagpu_spgemm_symbolic), whose output is bit-identical
+// to the reference's host loops.  diagpu::SpgemmPlan keeps the plan on the
+// device for the numeric phase; spgemm_hm() is a one-call host convenience.
+#pragma once
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <stdexcept>
+#include <vector>
+
+#include "common.hpp"
+
+// HM (Hossain-Mahmud) diagonal storage (spmspm/paper_hm.cuh:18-37): diagonal d
+// has length n - |d|; element (i, j) sits at position min(i, j).
+struct HMMatrix {
+    int                  n = 0;
+    int                  num_diags = 0;
+    std::vector<int>     diag_offsets;
+    std::vector<int64_t> diag_starts;
+    std::vector<int>     diag_lengths;
+    std::vector<float>   values;
+    int64_t              total_nz = 0;
+};
+
+// dense_to_hm (:41-65): the given offsets, in the given order.
+inline HMMatrix dense_to_hm(const float* dense, int n, const std::vector<int>& offsets)
+{
+    HMMatrix hm;
+    hm.n = n;
+    hm.num_diags = static_cast<int>(offsets.size());
+    hm.diag_offsets = offsets;
+    int64_t off = 0;
+    for (int d : offsets) {
+        const int len = n - std::abs(d);
+        const int sr = d >= 0 ? 0 : -d, sc = d >= 0 ? d : 0;
+        hm.diag_starts.push_back(off);
+        hm.diag_lengths.push_back(len);
+        for (int p = 0; p < len; ++p)
+            hm.values.push_back(dense[static_cast<size_t>(sr + p) * n + (sc + p)]);
+        off += len;
+    }
+    hm.total_nz = off;
+    return hm;
+}
+
+// hm_to_dense (:68-83).
+inline void hm_to_dense(const HMMatrix& hm, float* dense)
+{
+    const int n = hm.n;
+    std::memset(dense, 0, sizeof(float) * static_cast<size_t>(n) * n);
+    for (int i = 0; i < hm.num_diags; ++i) {
+        const int d = hm.diag_offsets[i];
+        const int sr = d >= 0 ? 0 : -d, sc = d >= 0 ? d : 0;
+        for (int p = 0; p < hm.diag_lengths[i]; ++p)
+            dense[static_cast<size_t>(sr + p) * n + (sc + p)] = hm.values[hm.diag_starts[i] + p];
+    }
+}
+
+// One pair-plan entry (spmspm/gather_flat.cuh:21); layout of diagpu_gpair.
+struct GPair {
+    size_t ab, bb;
+    int ash, bsh, al, bl;
+};
+static_assert(sizeof(GPair) == sizeof(diagpu_gpair), "GPair must match diagpu_gpair");
+
+// Pair plan (gather_flat.cuh:231): pairPtr has one entry per C diagonal + 1.
+struct PairPlan {
+    std::vector<int64_t> pairPtr;
+    std::vector<GPair> pairs;
+};
+
+// Pair plan plus the flat tile list of gather_flat (:264): tiles (k, ts)
+// every POS positions of each C diagonal.
+struct FlatPlan {
+    std::vector<int64_t> pairPtr;
+    std::vector<GPair> pairs;
+    std::vector<int2> tiles;
+    int64_t nTiles = 0;
+};
+
+namespace diagpu {
+
+// Everything the GPU symbolic phase produces, on the host.
+struct SymbolicResult {
+    std::vector<int> C_off, C_len;
+    std::vector<int64_t> C_starts, pair_ptr;
+    std::vector<GPair> pairs;
+    std::vector<int> lookup;
+    diagpu_spgemm_info info{};
+};
+
+// Run diagpu_spgemm_symbolic on host operand descriptions and bring every
+// output back to the host (one stream sync).
+inline SymbolicResult run_symbolic(int n, const std::vector<int>& A_off, const std::vector<int>& A_len,
+                                   const std::vector<int64_t>& A_starts, const std::vector<int>& B_off,
+                                   const std::vector<int>& B_len, const std::vector<int64_t>& B_starts,
+                                   bool want_lookup)
+{
+    const int na = static_cast<int>(A_off.size()), nb = static_cast<int>(B_off.size());
+    const int64_t ccap = std::max<int64_t>(1, std::min<int64_t>(int64_t(na) * nb, 2 * int64_t(n) - 1));
+    const int64_t pcap = std::max<int64_t>(1, int64_t(na) * nb);
+    DeviceArray<int> dAo(A_off), dAl(A_len), dBo(B_off), dBl(B_len);
+    DeviceArray<int64_t> dAs(A_starts), dBs(B_starts);
+    DeviceArray<int> dCo(ccap), dCl(ccap);
+    DeviceArray<int64_t> dCs(ccap), dPtr(ccap + 1);
+    DeviceArray<diagpu_gpair> dPairs(pcap);
+    DeviceArray<int> dLk(want_lookup ? static_cast<size_t>(2 * int64_t(n) - 1) : 0);
+    size_t ws_bytes = 0;
+    check(diagpu_spgemm_symbolic_workspace(n, na, nb, &ws_bytes));
+    DeviceArray<char> ws(ws_bytes);
+    SymbolicResult r;
+    check(diagpu_spgemm_symbolic(n, dAo.data(), dAl.data(), dAs.data(), na, dBo.data(), dBl.data(),
+                                 dBs.data(), nb, dCo.data(), dCl.data(), dCs.data(), ccap,
+                                 dPtr.data(), dPairs.data(), pcap,
+                                 want_lookup ? dLk.data() : nullptr, ws.data(), ws_bytes, &r.info,
+                                 nullptr));
+    const size_t nc = static_cast<size_t>(r.info.c_ndiag);
+    r.C_off = dCo.download(nc);
+    r.C_len = dCl.download(nc);
+    r.C_starts = dCs.download(nc);
+    r.pair_ptr = dPtr.download(nc + 1);
+    const auto gp = dPairs.download(static_cast<size_t>(r.info.n_pairs));
+    r.pairs.resize(gp.size());
+    if (!gp.empty()) std::memcpy(r.pairs.data(), gp.data(), gp.size() * sizeof(GPair));
+    if (want_lookup) r.lookup = dLk.download();
+    return r;
+}
+
+inline std::vector<int64_t> hm_starts(int n, const std::vector<int>& offsets)
+{
+    std::vector<int64_t> s;
+    int64_t o = 0;
+    for (int d : offsets) { s.push_back(o); o += n - std::abs(d); }
+    return s;
+}
+
+}  // namespace diagpu
+
+// compute_c_hm_structure (spmspm/paper_hm.cuh:87-117): every da + db inside
+// the matrix, ascending, lengths n - |d|, starts the prefix sums, values zero.
+inline HMMatrix compute_c_hm_structure(const HMMatrix& A, const HMMatrix& B, int n)
+{
+    const auto r = diagpu::run_symbolic(n, A.diag_offsets, A.diag_lengths, A.diag_starts,
+                                        B.diag_offsets, B.diag_lengths, B.diag_starts, false);
+    HMMatrix C;
+    C.n = n;
+    C.num_diags = static_cast<int>(r.C_off.size());
+    C.diag_offsets = r.C_off;
+    C.diag_lengths = r.C_len;
+    C.diag_starts = r.C_starts;
+    C.total_nz = r.info.c_nnz;
+    C.values.assign(static_cast<size_t>(C.total_nz), 0.0f);
+    return C;
+}
+
+// build_c_diag_lookup (:121-130): lookup[d + n - 1] = C index, -1 elsewhere.
+inline std::vector<int> build_c_diag_lookup(const HMMatrix& C, int n)
+{
+    std::vector<int> lookup(static_cast<size_t>(2 * int64_t(n) - 1), -1);
+    for (int i = 0; i < C.num_diags; ++i) lookup[C.diag_offsets[i] + (n - 1)] = i;
+    return lookup;
+}
+
+// build_pairs_only (spmspm/gather_flat.cuh:231-255) for the requested C
+// offsets (each |dc| < n): per C diagonal, per B diagonal in B's order, the A
+// diagonal with da = dc - db found through Alookup.
+inline PairPlan build_pairs_only(int n, const std::vector<int>& A_len,
+                                 const std::vector<size_t>& A_starts, const std::vector<int>& B_off,
+                                 const std::vector<int>& B_len, const std::vector<size_t>& B_starts,
+                                 const std::vector<int>& Alookup, const std::vector<int>& C_off)
+{
+    // The A offsets are the positions of the lookup's entries.
+    std::vector<int> A_off(A_len.size(), 0);
+    std::vector<char> seen(A_len.size(), 0);
+    for (int64_t i = 0; i < int64_t(Alookup.size()); ++i) {
+        const int ai = Alookup[static_cast<size_t>(i)];
+        if (ai >= 0 && ai < int(A_off.size())) { A_off[ai] = int(i - (n - 1)); seen[ai] = 1; }
+    }
+    std::vector<int> A_off_used, A_len_used;
+    std::vector<int64_t> A_st_used;
+    for (size_t a = 0; a < A_off.size(); ++a)
+        if (seen[a]) {
+            A_off_used.push_back(A_off[a]);
+            A_len_used.push_back(A_len[a]);
+            A_st_used.push_back(static_cast<int64_t>(A_starts[a]));
+        }
+    const std::vector<int64_t> B_st(B_starts.begin(), B_starts.end());
+    const auto r = diagpu::run_symbolic(n, A_off_used, A_len_used, A_st_used, B_off, B_len, B_st, true);
+    PairPlan pp;
+    pp.pairPtr.assign(C_off.size() + 1, 0);
+    for (size_t k = 0; k < C_off.size(); ++k) {
+        const int dc = C_off[k];
+        if (dc <= -n || dc >= n) throw std::invalid_argument("build_pairs_only: |C offset| >= n");
+        pp.pairPtr[k] = static_cast<int64_t>(pp.pairs.size());
+        const int ci = r.lookup[static_cast<size_t>(dc + (n - 1))];
+        if (ci < 0) continue;
+        pp.pairs.insert(pp.pairs.end(), r.pairs.begin() + r.pair_ptr[ci],
+                        r.pairs.begin() + r.pair_ptr[ci + 1]);
+    }
+    pp.pairPtr[C_off.size()] = static_cast<int64_t>(pp.pairs.size());
+    return pp;
+}
+
+// build_flat_plan (gather_flat.cuh:264-292): the pair plan plus tiles.
+inline FlatPlan build_flat_plan(int n, const std::vector<int>& A_off, const std::vector<int>& A_len,
+                                const std::vector<size_t>& A_starts, const std::vector<int>& B_off,
+                                const std::vector<int>& B_len, const std::vector<size_t>& B_starts,
+                                const std::vector<int>& Alookup, const std::vector<int>& C_off,
+                                const std::vector<int>& C_len, int POS)
+{
+    (void)A_off;
+    PairPlan pp = build_pairs_only(n, A_len, A_starts, B_off, B_len, B_starts, Alookup, C_off);
+    FlatPlan fp;
+    fp.pairPtr = std::move(pp.pairPtr);
+    fp.pairs = std::move(pp.pairs);
+    for (size_t k = 0; k < C_off.size(); ++k)
+        for (int ts = 0; ts < C_len[k]; ts += POS) fp.tiles.push_back(make_int2(int(k), ts));
+    fp.nTiles = static_cast<int64_t>(fp.tiles.size());
+    return fp;
+}
+
+namespace diagpu {
+
+// Device-resident C = A * B for HM operands whose offsets, lengths and starts
+// are device arrays: the plan is built once (symbolic), numeric() may run
+// many times on new values with the same structure.
+class SpgemmPlan {
+public:
+    SpgemmPlan(int n, const int* dA_off, const int* dA_len, const int64_t* dA_starts, int a_ndiag,
+               const int* dB_off, const int* dB_len, const int64_t* dB_starts, int b_ndiag,
+               bool want_lookup = false, hipStream_t stream = 0)
+        : n_(n)
+    {
+        const int64_t ccap = std::max<int64_t>(1, std::min<int64_t>(int64_t(a_ndiag) * b_ndiag, 2 * int64_t(n) - 1));
+        const int64_t pcap = std::max<int64_t>(1, int64_t(a_ndiag) * b_ndiag);
+        C_off_.resize(ccap);
+        C_len_.resize(ccap);
+        C_starts_.resize(ccap);
+        ptr_.resize(ccap + 1);
+        pairs_.resize(pcap);
+        if (want_lookup) lookup_.resize(static_cast<size_t>(2 * int64_t(n) - 1));
+        size_t ws_bytes = 0;
+        check(diagpu_spgemm_symbolic_workspace(n, a_ndiag, b_ndiag, &ws_bytes));
+        DeviceArray<char> ws(ws_bytes);
+        check(diagpu_spgemm_symbolic(n, dA_off, dA_len, dA_starts, a_ndiag, dB_off, dB_len, dB_starts,
+                                     b_ndiag, C_off_.data(), C_len_.data(), C_starts_.data(), ccap,
+                                     ptr_.data(), pairs_.data(), pcap,
+                                     want_lookup ? lookup_.data() : nullptr, ws.data(), ws_bytes,
+                                     &info_, stream));
+    }
+
+    // C_vals (device, info().c_nnz values) = A * B; asynchronous on `stream`.
+    void numeric(const float* dA_vals, const float* dB_vals, float* dC_vals, hipStream_t stream = 0) const
+    {
+        check(diagpu_spgemm_numeric_f32(n_, dA_vals, dB_vals, C_off_.data(), C_len_.data(),
+                                        C_starts_.data(), info_.c_ndiag, ptr_.data(), pairs_.data(),
+                                        info_.max_pairs, dC_vals, stream));
+    }
+
+    const diagpu_spgemm_info& info() const { return info_; }
+    const int* c_offsets() const { return C_off_.data(); }
+    const int* c_lengths() const { return C_len_.data(); }
+    const int64_t* c_starts() const { return C_starts_.data(); }
+    const int64_t* pair_ptr() const { return ptr_.data(); }
+    const diagpu_gpair* pairs() const { return pairs_.data(); }
+    const int* c_lookup() const { return lookup_.size() ? lookup_.data() : nullptr; }
+
+private:
+    int n_;
+    DeviceArray<int> C_off_, C_len_, lookup_;
+    DeviceArray<int64_t> C_starts_, ptr_;
+    DeviceArray<diagpu_gpair> pairs_;
+    diagpu_spgemm_info info_{};
+};
+
+}  // namespace diagpu
+
+// C = A * B for host HM matrices (upload, symbolic + numeric on the GPU,
+// download): compute_c_hm_structure's C with its values filled.
+inline HMMatrix spgemm_hm(const HMMatrix& A, const HMMatrix& B)
+{
+    using namespace diagpu;
+    const int n = A.n;
+    DeviceArray<int> ao(A.diag_offsets), al(A.diag_lengths), bo(B.diag_offsets), bl(B.diag_lengths);
+    DeviceArray<int64_t> as(A.diag_starts), bs(B.diag_starts);
+    DeviceArray<float> av(A.values), bv(B.values);
+    SpgemmPlan plan(n, ao.data(), al.data(), as.data(), A.num_diags, bo.data(), bl.data(), bs.data(),
+                    B.num_diags);
+    const auto& inf = plan.info();
+    DeviceArray<float> cv(static_cast<size_t>(inf.c_nnz));
+    plan.numeric(av.data(), bv.data(), cv.data());
+    check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    HMMatrix C;
+    C.n = n;
+    C.num_diags = static_cast<int>(inf.c_ndiag);
+    C.diag_offsets.resize(C.num_diags);
+    C.diag_lengths.resize(C.num_diags);
+    C.diag_starts.resize(C.num_diags);
+    if (C.num_diags) {
+        check_hip(hipMemcpy(C.diag_offsets.data(), plan.c_offsets(), sizeof(int) * C.num_diags, hipMemcpyDeviceToHost), "hipMemcpy");
+        check_hip(hipMemcpy(C.diag_lengths.data(), plan.c_lengths(), sizeof(int) * C.num_diags, hipMemcpyDeviceToHost), "hipMemcpy");
+        check_hip(hipMemcpy(C.diag_starts.data(), plan.c_starts(), sizeof(int64_t) * C.num_diags, hipMemcpyDeviceToHost), "hipMemcpy");
+    }
+    C.total_nz = inf.c_nnz;
+    C.values = cv.download();
+    return C;
+}

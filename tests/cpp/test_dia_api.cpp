@@ -1,0 +1,282 @@
+// GPU test of the C++ drop-in headers (include/diagpu/*.hpp), written the way
+// the reference's own tests are (spmv/test/test_tc_spmv.cu,
+// spmv/test/test_reconstruct.cpp): build inputs on the host, run through the
+// reference-named API, compare, print one line per case, exit status = pass.
+//
+// Integer outputs (Recon layout, C structure, lookup, pair plan) are compared
+// bit for bit with the CPU oracle (oracle/liboracle.so, test infrastructure);
+// values against an fp64 reference with |err| <= 1e-5 * sum |terms|.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <random>
+#include <vector>
+
+#include "diagpu/dia.hpp"
+
+extern "C" {
+void orc_build_recon_f32(int rows, int cols, int K, const int* offsets, const int64_t* starts,
+                         const int* lengths, const float* values, int* r_offsets, float* r_values);
+int orc_c_structure(int n, const int* A_off, int nA, const int* B_off, int nB, int* C_off,
+                    int* C_len, int64_t* C_starts, int64_t* nnz);
+void orc_c_lookup(int n, const int* C_off, int nC, int* lookup);
+int64_t orc_pairs_only(int n, const int* A_off, int nA, const int* A_len, const int64_t* A_starts,
+                       const int* B_off, int nB, const int* B_len, const int64_t* B_starts,
+                       const int* C_off, int nC, int64_t* pair_ptr, void* pairs);
+void orc_spgemm_pairs_f64(const float* A_vals, const float* B_vals, const int* C_len,
+                          const int64_t* C_starts, const int64_t* pair_ptr, const void* pairs,
+                          int kbeg, int kend, double* out, double* abs_out);
+void orc_gemm_diag_f64(int n, const float* DA, const int* off_A, int P, const float* DB,
+                       const int* off_B, int Q, const int* C_lookup, const int64_t* C_starts,
+                       double* out, double* abs_out);
+}
+
+static bool g_all = true;
+
+static void report(const char* name, bool ok, const char* detail = "")
+{
+    std::printf("  %-40s %s %s\n", name, ok ? "[OK]" : "[FAIL]", detail);
+    g_all &= ok;
+}
+
+// dense_to_dia of the reference tests (test_tc_spmv.cu:39-62).
+static DiaMatrix dense_to_dia(const float* H, int rows, int cols)
+{
+    DiaMatrix D;
+    D.rows = rows;
+    D.cols = cols;
+    for (int d = -(rows - 1); d <= cols - 1; ++d) {
+        const int sr = d >= 0 ? 0 : -d, sc = d >= 0 ? d : 0;
+        const int len = std::min(rows - sr, cols - sc);
+        if (len <= 0) continue;
+        bool nz = false;
+        for (int j = 0; j < len; ++j) nz |= H[(size_t)(sr + j) * cols + (sc + j)] != 0.0f;
+        if (!nz) continue;
+        D.offsets.push_back(d);
+        D.diag_starts.push_back((int)D.values.size());
+        D.diag_lengths.push_back(len);
+        for (int j = 0; j < len; ++j) D.values.push_back(H[(size_t)(sr + j) * cols + (sc + j)]);
+    }
+    return D;
+}
+
+static std::vector<float> gpu_spmv(const ReconMatrix& R, const std::vector<float>& x)
+{
+    diagpu::DeviceRecon dR(R);
+    diagpu::DeviceArray<float> dx(x), dy(R.rows);
+    launch_tc_spmv_regdirect(dR.view, dx.data(), (int)x.size(), dy.data(), 0);
+    diagpu::check_hip(hipDeviceSynchronize(), "sync");
+    return dy.download();
+}
+
+static void test_known_answer()
+{
+    // spmv/test/test_reconstruct.cpp:185-194
+    const float H[25] = {1, 2, 3, 0, 0, 4, 5, 6, 7, 0, 8, 9, 8, 7, 6, 0, 5, 4, 3, 2, 0, 0, 1, 2, 3};
+    const std::vector<float> x = {1, 2, 3, 4, 5};
+    const DiaMatrix D = dense_to_dia(H, 5, 5);
+    const ReconMatrix R = build_recon(D);
+    const std::vector<int> want_off = {2, 1, 0, -1, -2};
+    const std::vector<float> want_rows = {0, 0, 3, 7, 6, 0, 2, 6, 7, 2, 1, 5, 8, 3, 3,
+                                          4, 9, 4, 2, 0, 8, 5, 1, 0, 0};
+    report("5x5 build_recon", R.diag_offsets == want_off && R.values == want_rows);
+    const auto y = gpu_spmv(R, x);
+    report("5x5 launch_tc_spmv_regdirect", y == std::vector<float>({14, 60, 108, 44, 26}));
+}
+
+static void test_tc_case(const char* name, int N, const std::vector<int>& offsets)
+{
+    // inputs exactly as spmv/test/test_tc_spmv.cu:86-98
+    std::vector<float> H((size_t)N * N, 0.0f);
+    unsigned seed = 0x1234567u + (unsigned)N;
+    auto rng = [&]() {
+        seed = seed * 1664525u + 1013904223u;
+        return (float)((seed >> 8) & 0xFFFF) / 65536.0f * 2.0f - 1.0f;
+    };
+    for (int r = 0; r < N; ++r)
+        for (int d : offsets) {
+            const int c = r + d;
+            if (c >= 0 && c < N) H[(size_t)r * N + c] = rng();
+        }
+    std::vector<float> x(N);
+    for (int i = 0; i < N; ++i) x[i] = rng();
+    const DiaMatrix D = dense_to_dia(H.data(), N, N);
+    const ReconMatrix R = build_recon(D);
+    // Recon layout bit-exact with the oracle's build_recon
+    std::vector<int64_t> st(D.diag_starts.begin(), D.diag_starts.end());
+    std::vector<int> o_off(R.num_diags);
+    std::vector<float> o_val((size_t)R.num_diags * N);
+    orc_build_recon_f32(N, N, R.num_diags, D.offsets.data(), st.data(), D.diag_lengths.data(),
+                        D.values.data(), o_off.data(), o_val.data());
+    const bool layout_ok = o_off == R.diag_offsets && o_val == R.values;
+    const auto y = gpu_spmv(R, x);
+    bool ok = true;
+    double worst = 0;
+    for (int r = 0; r < N; ++r) {
+        double s = 0, a = 0;
+        for (int c = 0; c < N; ++c) {
+            const double t = (double)H[(size_t)r * N + c] * x[c];
+            s += t;
+            a += std::fabs(t);
+        }
+        const double err = std::fabs(y[r] - s);
+        worst = std::max(worst, err / (a + 1e-300));
+        ok &= err <= 1e-5 * a + 1e-300;
+    }
+    char buf[96];
+    std::snprintf(buf, sizeof buf, "N=%d diags=%d worst err/sum|t|=%.1e", N, R.num_diags, worst);
+    report(name, layout_ok && ok, buf);
+}
+
+static void test_spmv_f64()
+{
+    const int n = 4099;
+    std::mt19937 g(3);
+    std::vector<int> offs = {700, 3, 0, -1, -2000};
+    std::vector<double> vals((size_t)offs.size() * n), x(n);
+    for (auto& v : vals) v = (double)(g() % 20001) / 10000.0 - 1.0;
+    for (auto& v : x) v = (double)(g() % 20001) / 10000.0 - 1.0;
+    diagpu::DeviceArray<int> doff(offs);
+    diagpu::DeviceArray<double> dv(vals), dx(x), dy(n);
+    diagpu::launch_dia_spmv(diagpu::ReconViewF64{n, n, (int)offs.size(), doff.data(), dv.data()},
+                            dx.data(), n, dy.data());
+    diagpu::check_hip(hipDeviceSynchronize(), "sync");
+    const auto y = dy.download();
+    bool ok = true;
+    for (int r = 0; r < n; ++r) {
+        long double s = 0, a = 0;
+        for (size_t k = 0; k < offs.size(); ++k) {
+            const long c = (long)r + offs[k];
+            if (c >= 0 && c < n) {
+                const long double t = (long double)vals[k * n + c] * x[c];
+                s += t;
+                a += std::fabs((double)t);
+            }
+        }
+        ok &= std::fabs((double)(y[r] - s)) <= 1e-13 * (double)a + 1e-300;
+    }
+    report("fp64 launch_dia_spmv", ok);
+}
+
+static HMMatrix random_hm(int n, std::vector<int> offs, unsigned seed)
+{
+    std::mt19937 g(seed);
+    std::vector<float> dense((size_t)n * n, 0.0f);
+    for (int d : offs)
+        for (int p = 0; p < n - std::abs(d); ++p) {
+            const int r = d >= 0 ? p : p - d, c = d >= 0 ? p + d : p;
+            dense[(size_t)r * n + c] = (float)(g() % 65536) / 32768.0f - 1.0f;
+        }
+    return dense_to_hm(dense.data(), n, offs);
+}
+
+static void test_spgemm(const char* name, int n, std::vector<int> oa, std::vector<int> ob)
+{
+    const HMMatrix A = random_hm(n, oa, 11), B = random_hm(n, ob, 12);
+    const HMMatrix Cs = compute_c_hm_structure(A, B, n);
+    const int cap = (int)std::min<int64_t>((int64_t)oa.size() * ob.size(), 2 * n - 1);
+    std::vector<int> c_off(cap), c_len(cap);
+    std::vector<int64_t> c_st(cap);
+    int64_t nnz = 0;
+    const int nc = orc_c_structure(n, oa.data(), (int)oa.size(), ob.data(), (int)ob.size(),
+                                   c_off.data(), c_len.data(), c_st.data(), &nnz);
+    c_off.resize(nc); c_len.resize(nc); c_st.resize(nc);
+    report((std::string(name) + " compute_c_hm_structure").c_str(),
+           Cs.diag_offsets == c_off && Cs.diag_lengths == c_len && Cs.diag_starts == c_st &&
+               Cs.total_nz == nnz);
+    std::vector<int> lk(2 * n - 1);
+    orc_c_lookup(n, c_off.data(), nc, lk.data());
+    report((std::string(name) + " build_c_diag_lookup").c_str(), build_c_diag_lookup(Cs, n) == lk);
+    // pair plan, reference signature: Alookup built as the bench builds it
+    std::vector<int> Alookup(2 * n - 1, -1);
+    for (size_t i = 0; i < oa.size(); ++i) Alookup[oa[i] + (n - 1)] = (int)i;
+    std::vector<size_t> as(A.diag_starts.begin(), A.diag_starts.end());
+    std::vector<size_t> bs(B.diag_starts.begin(), B.diag_starts.end());
+    const PairPlan pp = build_pairs_only(n, A.diag_lengths, as, B.diag_offsets, B.diag_lengths, bs,
+                                         Alookup, c_off);
+    std::vector<int64_t> o_ptr(nc + 1);
+    const int64_t np = orc_pairs_only(n, oa.data(), (int)oa.size(), A.diag_lengths.data(),
+                                      A.diag_starts.data(), ob.data(), (int)ob.size(),
+                                      B.diag_lengths.data(), B.diag_starts.data(), c_off.data(), nc,
+                                      o_ptr.data(), nullptr);
+    std::vector<GPair> o_pairs(np);
+    orc_pairs_only(n, oa.data(), (int)oa.size(), A.diag_lengths.data(), A.diag_starts.data(),
+                   ob.data(), (int)ob.size(), B.diag_lengths.data(), B.diag_starts.data(),
+                   c_off.data(), nc, o_ptr.data(), o_pairs.data());
+    const bool plan_ok = pp.pairPtr == o_ptr && pp.pairs.size() == o_pairs.size() &&
+                         std::memcmp(pp.pairs.data(), o_pairs.data(), np * sizeof(GPair)) == 0;
+    report((std::string(name) + " build_pairs_only").c_str(), plan_ok);
+    const FlatPlan fp = build_flat_plan(n, oa, A.diag_lengths, as, B.diag_offsets, B.diag_lengths,
+                                        bs, Alookup, c_off, c_len, 512);
+    int64_t tiles = 0;
+    for (int k = 0; k < nc; ++k) tiles += (c_len[k] + 511) / 512;
+    report((std::string(name) + " build_flat_plan").c_str(),
+           fp.pairPtr == o_ptr && fp.nTiles == tiles);
+    // values
+    const HMMatrix C = spgemm_hm(A, B);
+    std::vector<double> want(nnz), absum(nnz);
+    orc_spgemm_pairs_f64(A.values.data(), B.values.data(), c_len.data(), c_st.data(), o_ptr.data(),
+                         o_pairs.data(), 0, nc, want.data(), absum.data());
+    bool ok = C.diag_offsets == c_off && (int64_t)C.values.size() == nnz;
+    for (int64_t i = 0; ok && i < nnz; ++i)
+        ok &= std::fabs(C.values[i] - want[i]) <= 1e-5 * absum[i] + 1e-300;
+    report((std::string(name) + " spgemm_hm values").c_str(), ok);
+}
+
+static void test_gemm_diag(const char* name, int n, std::vector<int> oa, std::vector<int> ob)
+{
+    std::mt19937 g(42);
+    auto pack = [&](const std::vector<int>& offs) {
+        std::vector<float> D(offs.size() * (size_t)n, 0.0f);
+        for (size_t i = 0; i < offs.size(); ++i) {
+            const int sr = offs[i] >= 0 ? 0 : -offs[i];
+            for (int p = 0; p < n - std::abs(offs[i]); ++p)
+                D[i * n + sr + p] = 0.5f + (float)(g() % 65536) / 65536.0f;
+        }
+        return D;
+    };
+    const auto DA = pack(oa), DB = pack(ob);
+    const diagpu::CLayout L = diagpu::build_c_layout(n, oa, ob);
+    std::vector<int> lk(2 * n - 1);
+    orc_c_lookup(n, L.k_list.data(), L.num_k, lk.data());
+    report((std::string(name) + " build_c_layout").c_str(), L.k_to_idx == lk);
+    diagpu::DeviceArray<int> doa(oa), dob(ob);
+    diagpu::DeviceArray<float> dA(DA), dB(DB);
+    diagpu::GemmDiag gd(n, doa.data(), (int)oa.size(), dob.data(), (int)ob.size());
+    diagpu::DeviceArray<float> dC((size_t)gd.info().c_nnz);
+    gd.run(dA.data(), dB.data(), dC.data());
+    diagpu::check_hip(hipDeviceSynchronize(), "sync");
+    const auto C = dC.download();
+    std::vector<double> want(L.total_c, 0.0), absum(L.total_c, 0.0);
+    orc_gemm_diag_f64(n, DA.data(), oa.data(), (int)oa.size(), DB.data(), ob.data(), (int)ob.size(),
+                      lk.data(), L.C_offsets.data(), want.data(), absum.data());
+    bool ok = gd.info().c_nnz == L.total_c;
+    for (int64_t i = 0; ok && i < L.total_c; ++i)
+        ok &= std::fabs(C[i] - want[i]) <= 1e-5 * absum[i] + 1e-300;
+    report((std::string(name) + " GemmDiag values").c_str(), ok);
+}
+
+int main()
+{
+    std::printf("C++ drop-in API on the GPU\n");
+    try {
+        test_known_answer();
+        test_tc_case("tridiagonal", 48, {-1, 0, 1});
+        test_tc_case("tridiag ragged", 37, {-1, 0, 1});
+        test_tc_case("pentadiagonal", 64, {-2, -1, 0, 1, 2});
+        test_tc_case("9-diag wide band", 80, {-9, -5, -2, -1, 0, 1, 2, 5, 9});
+        test_tc_case("asymmetric band", 71, {-3, 0, 2, 4, 7});
+        test_tc_case("main diagonal", 16, {0});
+        test_tc_case("wide band 3000", 3000, {-1500, -7, 0, 9, 2048});
+        test_spmv_f64();
+        test_spgemm("band", 300, {-4, -3, -2, -1, 0, 1, 2, 3, 4}, {-16, -1, 0, 1, 16});
+        test_spgemm("scattered", 2000, {-1900, -77, 0, 5, 640}, {-3, -2, 300, 1999, 1});
+        test_gemm_diag("gemm_diag band", 512, {-3, -2, -1, 0, 1, 2, 3}, {-3, -2, -1, 0, 1, 2, 3});
+        test_gemm_diag("gemm_diag scattered", 700, {-300, -9, 0, 33}, {-600, -1, 2, 5, 450});
+    } catch (const std::exception& e) {
+        std::printf("  exception: %s\n", e.what());
+        g_all = false;
+    }
+    std::printf("\n%s\n", g_all ? "ALL TESTS PASSED" : "SOME TESTS FAILED");
+    return g_all ? 0 : 1;
+}
