@@ -69,13 +69,14 @@ __device__ __forceinline__ void store_quad_stream(T* p, typename QuadOf<T>::type
 __device__ __forceinline__ float fma_(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
 __device__ __forceinline__ double fma_(double a, double b, double c) { return __builtin_fma(a, b, c); }
 
-// min and max of the diagonal offsets, uniform across the wave.
-__device__ __forceinline__ void offset_range(const int32_t* __restrict__ offs, int K,
+// min and max of the diagonal offsets, uniform across the wave.  `first` is
+// offs[lane] (lane < K), loaded once and reused by the main loop.
+__device__ __forceinline__ void offset_range(const int32_t* __restrict__ offs, int K, int first,
                                              int& dmin, int& dmax)
 {
     const int lane = threadIdx.x & 63;
-    int lo = INT_MAX, hi = INT_MIN;
-    for (int k = lane; k < K; k += 64) {
+    int lo = lane < K ? first : INT_MAX, hi = lane < K ? first : INT_MIN;
+    for (int k = lane + 64; k < K; k += 64) {
         const int d = offs[k];
         lo = d < lo ? d : lo;
         hi = d > hi ? d : hi;
@@ -103,8 +104,12 @@ __global__ __launch_bounds__(kBlock) void spmv_recon_kernel(
     const int64_t r0 = (int64_t)tile * kTile;
     const int64_t r = r0 + (int64_t)threadIdx.x * kRowsPerLane;
 
+    // One vector load of the first 64 offsets serves the range test and the
+    // first group of the main loop (one dependent round trip per tile).
+    const int lane = threadIdx.x & 63;
+    const int first = lane < K ? offs[lane] : 0;
     int dmin = 0, dmax = 0;
-    offset_range(offs, K, dmin, dmax);
+    offset_range(offs, K, first, dmin, dmax);
     const bool interior = (r0 + kTile <= rows) &&
                           (K == 0 || (r0 + dmin >= 0 && r0 + kTile + (int64_t)dmax <= lim));
 
@@ -112,12 +117,11 @@ __global__ __launch_bounds__(kBlock) void spmv_recon_kernel(
         Quad acc = {0, 0, 0, 0};
         const T* __restrict__ vr = vals + r;
         const T* __restrict__ xr = x + r;
-        const int lane = threadIdx.x & 63;
         // Offsets travel 64 at a time as one vector load (lane l holds
         // offset g0 + l) and are broadcast with readlane, so the loads of a
         // chunk issue back to back without a scalar-load wait per diagonal.
         for (int g0 = 0; g0 < K; g0 += 64) {
-            const int dl = (g0 + lane < K) ? offs[g0 + lane] : 0;
+            const int dl = g0 == 0 ? first : ((g0 + lane < K) ? offs[g0 + lane] : 0);
             const int gn = (K - g0) < 64 ? (K - g0) : 64;
             const T* __restrict__ vg = vr + (int64_t)g0 * cols;
             for (int k0 = 0; k0 < gn; k0 += kChunk) {
