@@ -86,6 +86,11 @@ def build_cpp_tests() -> None:
     cc = hipcc()
     for src in sorted(src_dir.glob("*.cpp")):
         exe = out_dir / src.stem
+        if src.stem.endswith("_cpu"):      # host-only: plain g++, no HIP
+            _run(["g++", "-O2", "-std=c++17", "-Wall", f"-I{ROOT / 'include'}", str(src),
+                  f"-L{ROOT / 'oracle'}", "-loracle", "-Wl,-rpath,$ORIGIN/../../../oracle",
+                  "-o", str(exe)])
+            continue
         # tests/cpp/bin/<exe>: the library and the oracle sit three levels up
         _run([cc, "-O2", "-std=c++17", "-Wall", f"-I{ROOT / 'include'}", str(src),
               f"-L{PKG}", "-ldiagpu", f"-L{ROOT / 'oracle'}", "-loracle",
