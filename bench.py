@@ -46,7 +46,7 @@ def parse_args(argv=None):
     ap.add_argument("--no-extras", dest="extras", action="store_false")
     ap.add_argument("--only", default="",
                     help="profiling aid: run just one workload (spmv2, spmv2d, spmv1, spmv3, "
-                         "spgemm4, spgemm5, copy) and print its line")
+                         "spgemm4, spgemm5, taylor, copy) and print its line")
     return ap.parse_args(argv)
 
 
@@ -207,6 +207,35 @@ def time_spgemm(cfg: int, seed: int, reps: int):
     }
 
 
+def time_taylor(order: int = 6, t: float = 0.05):
+    """Taylor chain exp(tH) ~ sum_k (tH)^k/k! on the 7-point stencil of SpGEMM
+    config 4 (n = 2^20): one warm-up chain, then one timed chain whose phases
+    are stream-synchronised (the plan of every product is built on the device)."""
+    import torch
+    from diagpu_amd import chain, workloads
+    H = workloads.hm_stencil7(128, 128, 64, device="cuda")
+    chain.taylor_expm(H, t, order)
+    torch.cuda.synchronize()
+    st = chain.ChainStats()
+    t0 = time.perf_counter()
+    S = chain.taylor_expm(H, t, order, st)
+    torch.cuda.synchronize()
+    total = time.perf_counter() - t0
+    steps = [{"k": k + 2, "C_diags": st.c_ndiag[k], "pairs": st.n_pairs[k],
+              "symbolic_ms": round(st.symbolic[k] * 1e3, 3),
+              "numeric_ms": round(st.numeric[k] * 1e3, 3),
+              "GFLOPs": round(st.useful_flops[k] / (st.numeric[k] * 1e9), 1)}
+             for k in range(len(st.numeric))]
+    flops = sum(st.useful_flops)
+    return {"workload": "taylor_expm_stencil7_cfg4", "n": H.n, "order": order, "t": t,
+            "S_diags": S.ndiag, "S_nnz": S.nnz, "total_ms": round(total * 1e3, 3),
+            "symbolic_ms": round(sum(st.symbolic) * 1e3, 3),
+            "numeric_ms": round(sum(st.numeric) * 1e3, 3),
+            "axpby_ms": round(sum(st.axpby) * 1e3, 3),
+            "numeric_GFLOPs": round(flops / (sum(st.numeric) * 1e9), 1),
+            "steps": steps}
+
+
 def copy_calibration(steps: int):
     """A plain device copy of known size, for scaling rocprof FETCH/WRITE counters."""
     import torch
@@ -253,6 +282,8 @@ def main(argv=None) -> int:
             print(json.dumps(spmv_record(cfg, dt, res)), flush=True)
         elif w.startswith("spgemm"):
             print(json.dumps(time_spgemm(int(w[6]), args.seed, args.steps)), flush=True)
+        elif w == "taylor":
+            print(json.dumps(time_taylor()), flush=True)
         else:
             raise SystemExit(f"unknown --only {w}")
         return 0
@@ -293,6 +324,13 @@ def main(argv=None) -> int:
                 torch.cuda.empty_cache()
             except Exception as e:
                 extras[f"spgemm_cfg{cfg}"] = {"error": repr(e)}
+        try:
+            rec = time_taylor()
+            extras["taylor_chain"] = rec
+            log(f"extra taylor chain: {rec['total_ms']} ms, numeric {rec['numeric_GFLOPs']} GFLOP/s")
+            torch.cuda.empty_cache()
+        except Exception as e:
+            extras["taylor_chain"] = {"error": repr(e)}
 
     traffic = load_traffic("spmv_cfg2_f32")
     line = {

@@ -1,0 +1,202 @@
+"""Matrix-power chain and truncated Taylor series on HM matrices: the caller
+of the SpGEMM hot path that the reference describes but does not ship
+(spmspm/gather_flat.cuh:13-14 "recurs each step of a matrix-power chain where
+A grows"; :110-117 "fully on-device plan build").
+
+Every product builds its C structure and pair plan on the GPU
+(diagpu_spgemm_symbolic; one stream sync returns the counts) and fills C with
+diagpu_spgemm_numeric_f32.  Sums and scalings use diagpu_dia_axpby_f32 over
+the union of the operands' diagonals; the union itself is a merge of two
+short sorted offset lists on the host.
+
+torch tensors only carry device memory; all arithmetic is in libdiagpu.
+"""
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from . import _lib
+from .spgemm import SpgemmPlan, _check_dev
+from .spmv import _stream_handle
+from .workloads import HM, hm_layout
+
+
+def hm_structure(n: int, offsets, device) -> HM:
+    """An HM matrix with the given (ascending, distinct) offsets and
+    uninitialised values."""
+    offs, lens, starts = hm_layout(n, offsets)
+    if len(offs) != len(list(offsets)):
+        raise ValueError("offsets must be distinct")
+    if offs and (offs[0] <= -n or offs[-1] >= n):
+        raise ValueError(f"offsets must satisfy |d| < n = {n}")
+    return HM(n, torch.tensor(offs, dtype=torch.int32, device=device),
+              torch.tensor(lens, dtype=torch.int32, device=device),
+              torch.tensor(starts, dtype=torch.int64, device=device),
+              torch.empty(max(1, int(sum(lens))), dtype=torch.float32, device=device)[: int(sum(lens))])
+
+
+def identity(n: int, device) -> HM:
+    I = hm_structure(n, [0], device)
+    I.values.fill_(1.0)
+    return I
+
+
+def _host_offsets(M: HM) -> list[int]:
+    return M.offsets.cpu().tolist()
+
+
+def axpby(alpha: float, X: HM, beta: float, Y: HM | None, stream=None) -> HM:
+    """Z = alpha * X + beta * Y on the union of the two diagonal sets."""
+    if Y is not None and Y.n != X.n:
+        raise ValueError("X and Y must have the same dimension")
+    ox = _host_offsets(X)
+    oy = _host_offsets(Y) if Y is not None else []
+    for offs, nm in ((ox, "X"), (oy, "Y")):
+        if any(b <= a for a, b in zip(offs, offs[1:])):
+            raise ValueError(f"{nm} offsets must be ascending and distinct")
+    Z = hm_structure(X.n, sorted(set(ox) | set(oy)), X.values.device)
+    for M, nm in ((X, "X"), (Y, "Y")):
+        if M is not None:
+            _check_dev(M.values, torch.float32, f"{nm}.values")
+    ny = Y.ndiag if Y is not None else 0
+    _lib.call("diagpu_dia_axpby_f32", X.n,
+              X.offsets.data_ptr(), X.starts.data_ptr(), X.ndiag, X.values.data_ptr(), float(alpha),
+              Y.offsets.data_ptr() if ny else None, Y.starts.data_ptr() if ny else None, ny,
+              Y.values.data_ptr() if ny else None, float(beta),
+              Z.offsets.data_ptr(), Z.starts.data_ptr(), Z.ndiag, Z.values.data_ptr(),
+              _stream_handle(stream))
+    return Z
+
+
+@dataclass
+class ChainStats:
+    """Wall-clock split of a chain (seconds, stream-synchronised per phase)."""
+    symbolic: list[float] = field(default_factory=list)
+    numeric: list[float] = field(default_factory=list)
+    axpby: list[float] = field(default_factory=list)
+    c_ndiag: list[int] = field(default_factory=list)
+    n_pairs: list[int] = field(default_factory=list)
+    useful_flops: list[int] = field(default_factory=list)
+
+
+def _timed(stats_list, fn, *args, **kw):
+    if stats_list is None:
+        return fn(*args, **kw)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = fn(*args, **kw)
+    torch.cuda.synchronize()
+    stats_list.append(time.perf_counter() - t0)
+    return out
+
+
+def multiply(A: HM, B: HM, stats: ChainStats | None = None) -> HM:
+    """C = A * B with its plan built on the device for this product (torch's
+    current stream; one sync for the symbolic counts)."""
+    if stats is not None:
+        torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    plan = SpgemmPlan(A, B)
+    inf = plan.info
+    C = HM(A.n, plan.c_offsets().clone(), plan.c_lengths().clone(), plan.c_starts().clone(),
+           torch.empty(max(1, inf.c_nnz), dtype=torch.float32, device=A.values.device)[: inf.c_nnz])
+    if stats is not None:
+        torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    if inf.c_ndiag:
+        plan.numeric(A.values, B.values, C.values)
+    if stats is not None:
+        torch.cuda.synchronize()
+        stats.symbolic.append(t1 - t0)
+        stats.numeric.append(time.perf_counter() - t1)
+        stats.c_ndiag.append(inf.c_ndiag)
+        stats.n_pairs.append(inf.n_pairs)
+        stats.useful_flops.append(inf.useful_flops)
+    return C
+
+
+def power(H: HM, k: int, stats: ChainStats | None = None) -> HM:
+    """H^k (k >= 1) by the chain P_j = P_{j-1} * H."""
+    if k < 1:
+        raise ValueError("k must be >= 1")
+    P = H
+    for _ in range(k - 1):
+        P = multiply(P, H, stats)
+    return P
+
+
+def add_identity(S: HM, sigma: float = 1.0, stream=None) -> HM:
+    """S + sigma I: in place when S holds the main diagonal, else a new
+    matrix on the union of the diagonal sets."""
+    offs = _host_offsets(S)
+    if 0 not in offs:
+        return axpby(1.0, S, sigma, identity(S.n, S.values.device), stream)
+    i = offs.index(0)
+    I = identity(S.n, S.values.device)
+    o4, s8 = S.offsets.element_size(), S.starts.element_size()
+    # X = Z = S's main diagonal alone (one offset, its start), Y = I
+    _lib.call("diagpu_dia_axpby_f32", S.n,
+              S.offsets.data_ptr() + i * o4, S.starts.data_ptr() + i * s8, 1,
+              S.values.data_ptr(), 1.0,
+              I.offsets.data_ptr(), I.starts.data_ptr(), 1, I.values.data_ptr(), float(sigma),
+              S.offsets.data_ptr() + i * o4, S.starts.data_ptr() + i * s8, 1,
+              S.values.data_ptr(), _stream_handle(stream))
+    return S
+
+
+def taylor_expm(H: HM, t: float, order: int, stats: ChainStats | None = None) -> HM:
+    """S = sum_{k=0..order} (t H)^k / k! in Horner form,
+
+        S_order = I + (t/order) H,   S_j = I + S_{j+1} * ((t/j) H),   S = S_1,
+
+    so each step is one device-planned SpGEMM, the wide S_{j+1} times the
+    narrow (t/j) H (S_{j+1} is a polynomial in H, so the two commute; this
+    order is the faster one for the numeric kernel), and an in-place add of I
+    to the product's main diagonal (a full union pass only when the product
+    lacks that diagonal)."""
+    if order < 0:
+        raise ValueError("order must be >= 0")
+    dev = H.values.device
+    if order == 0:
+        return identity(H.n, dev)
+    ax = stats.axpby if stats else None
+    S = _timed(ax, axpby, t / order, H, 1.0, identity(H.n, dev))
+    for j in range(order - 1, 0, -1):
+        Hj = _timed(ax, axpby, t / j, H, 0.0, None)
+        S = multiply(S, Hj, stats)
+        S = _timed(ax, add_identity, S)
+    return S
+
+
+# ---- host helpers for tests and examples ----------------------------------
+
+def hm_to_dense(M: HM) -> np.ndarray:
+    """Dense float64 copy of a small HM matrix."""
+    n = M.n
+    offs = _host_offsets(M)
+    starts = M.starts.cpu().numpy()
+    vals = M.values.cpu().numpy().astype(np.float64)
+    D = np.zeros((n, n))
+    for d, s in zip(offs, starts):
+        ln = n - abs(d)
+        r = np.arange(ln) + max(-d, 0)
+        D[r, r + d] = vals[s: s + ln]
+    return D
+
+
+def hm_matvec64(M: HM, x: np.ndarray) -> np.ndarray:
+    """y = M x in float64 over the HM diagonals (host)."""
+    n = M.n
+    offs = _host_offsets(M)
+    starts = M.starts.cpu().numpy()
+    vals = M.values.cpu().numpy().astype(np.float64)
+    y = np.zeros(n)
+    for d, s in zip(offs, starts):
+        ln = n - abs(d)
+        r0 = max(-d, 0)
+        y[r0: r0 + ln] += vals[s: s + ln] * x[r0 + d: r0 + d + ln]
+    return y

@@ -1,0 +1,100 @@
+// Z = alpha * X + beta * Y for HM (compact diagonal) matrices, gfx950.
+//
+// Z's diagonal set is given by the caller and must contain every diagonal of
+// X and of Y (normally their union); a Z diagonal absent from X (or Y) takes
+// 0 from it.  All three offset lists are ascending and duplicate-free, so the
+// X / Y diagonal behind each Z diagonal is found by binary search.  Diagonals
+// of equal offset have equal length n - |d| and the same position meaning,
+// so the update is elementwise along each diagonal: one coalesced streaming
+// pass over Z (12 bytes per position where both X and Y hold the diagonal).
+//
+// No reference counterpart: the reference describes a matrix-power chain
+// (spmspm/gather_flat.cuh:13-14,110-117) but ships no driver for it.  The
+// Taylor chain needs this to scale H and to add each power into the sum.
+#include "common.hpp"
+
+namespace diagpu {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kSpan = kBlock * 4;   // positions per workgroup iteration
+
+__device__ __forceinline__ int find_offset(const int32_t* __restrict__ off, int cnt, int d)
+{
+    int lo = 0, hi = cnt - 1;
+    while (lo <= hi) {
+        const int mid = (lo + hi) >> 1;
+        const int v = off[mid];
+        if (v == d) return mid;
+        if (v < d) lo = mid + 1; else hi = mid - 1;
+    }
+    return -1;
+}
+
+__global__ __launch_bounds__(kBlock) void k_axpby(
+    int32_t n, const int32_t* __restrict__ X_off, const int64_t* __restrict__ X_starts, int32_t nx,
+    const float* Xv, float alpha, const int32_t* __restrict__ Y_off,
+    const int64_t* __restrict__ Y_starts, int32_t ny, const float* Yv, float beta,
+    const int32_t* __restrict__ Z_off, const int64_t* __restrict__ Z_starts, int32_t nz,
+    float* Zv, int32_t span_blocks)
+{
+    // blockIdx.x enumerates (Z diagonal, span) pairs, spans fastest.
+    for (int64_t w = blockIdx.x; w < (int64_t)nz * span_blocks; w += gridDim.x) {
+        const int z = (int)(w / span_blocks);
+        const int sb = (int)(w - (int64_t)z * span_blocks);
+        const int d = Z_off[z];
+        const int len = n - (d < 0 ? -d : d);
+        const int64_t p0 = (int64_t)sb * kSpan;
+        if (p0 >= len) continue;
+        const int xi = find_offset(X_off, nx, d);
+        const int yi = find_offset(Y_off, ny, d);
+        // Z may be X (or Y) itself, element for element: each lane reads its
+        // positions before it writes them, so the value pointers are not restrict.
+        const float* xp = xi >= 0 ? Xv + X_starts[xi] : nullptr;
+        const float* yp = yi >= 0 ? Yv + Y_starts[yi] : nullptr;
+        float* zp = Zv + Z_starts[z];
+        float xv[4], yv[4];
+        for (int e = 0; e < 4; ++e) {           // all loads first, then the stores
+            const int64_t p = p0 + (int64_t)e * kBlock + threadIdx.x;
+            xv[e] = (xp && p < len) ? xp[p] : 0.0f;
+            yv[e] = (yp && p < len) ? yp[p] : 0.0f;
+        }
+        for (int e = 0; e < 4; ++e) {
+            const int64_t p = p0 + (int64_t)e * kBlock + threadIdx.x;
+            if (p < len) zp[p] = alpha * xv[e] + beta * yv[e];
+        }
+    }
+}
+
+}  // namespace
+}  // namespace diagpu
+
+extern "C" {
+
+DIAGPU_API int diagpu_dia_axpby_f32(int32_t n, const int32_t* X_off, const int64_t* X_starts,
+                                    int32_t nx, const float* X_vals, float alpha,
+                                    const int32_t* Y_off, const int64_t* Y_starts, int32_t ny,
+                                    const float* Y_vals, float beta, const int32_t* Z_off,
+                                    const int64_t* Z_starts, int32_t nz, float* Z_vals, void* stream)
+{
+    using namespace diagpu;
+    const char* fn = "diagpu_dia_axpby_f32";
+    if (n < 1 || n > (1 << 30) || nx < 0 || ny < 0 || nz < 0)
+        return fail(DIAGPU_ERR_ARG, "%s: need 1 <= n <= 2^30 and counts >= 0", fn);
+    if (nz == 0) return DIAGPU_OK;
+    if (!Z_off || !Z_starts || !Z_vals) return fail(DIAGPU_ERR_ARG, "%s: Z arrays are NULL", fn);
+    if (nx > 0 && (!X_off || !X_starts || !X_vals)) return fail(DIAGPU_ERR_ARG, "%s: X arrays are NULL", fn);
+    if (ny > 0 && (!Y_off || !Y_starts || !Y_vals)) return fail(DIAGPU_ERR_ARG, "%s: Y arrays are NULL", fn);
+    if (alpha == 0.0f) nx = 0;      // BLAS convention: a zero factor's operand is not read
+    if (beta == 0.0f) ny = 0;
+    const int32_t spans = (int32_t)ceil_div<int64_t>(n, kSpan);
+    int64_t grid = (int64_t)nz * spans;
+    const int64_t cap = (int64_t)cu_count() * 16;
+    if (grid > cap) grid = cap;
+    hipLaunchKernelGGL(k_axpby, dim3((unsigned)grid), dim3(kBlock), 0, as_stream(stream), n, X_off,
+                       X_starts, nx, X_vals, alpha, Y_off, Y_starts, ny, Y_vals, beta, Z_off,
+                       Z_starts, nz, Z_vals, spans);
+    return check_launch(fn);
+}
+
+}  // extern "C"

@@ -169,6 +169,28 @@ DIAGPU_API int diagpu_spgemm_numeric_f32(
 DIAGPU_API int diagpu_rowpacked_as_hm(int32_t n, const int32_t* offsets, int32_t ndiag,
                                       int64_t* starts, int32_t* lengths, void* stream);
 
+/* ======================================================================
+ * DIA linear combination (matrix-power / Taylor chain)
+ * ====================================================================== */
+
+/* Z = alpha * X + beta * Y for square n x n HM matrices (diagonal d holds
+ * n - |d| values, element p at row max(-d, 0) + p).  Offsets of X, Y and Z
+ * are ascending and distinct, and Z's set contains X's and Y's (normally it
+ * is their union); a Z diagonal missing from X or Y takes 0 from it.  A zero
+ * alpha (beta) means X (Y) is not read, as in BLAS.  Every Z value is
+ * written.  Z may be X (or Y) in place when both describe the same
+ * diagonals at the same starts (e.g. adding the identity to an existing
+ * main diagonal); any other overlap is undefined.  Device kernel, async.
+ * No counterpart in the reference, whose matrix-power chain
+ * (spmspm/gather_flat.cuh:13-14,110-117) has no driver; the Taylor chain
+ * uses it to scale H and to add each power into the running sum. */
+DIAGPU_API int diagpu_dia_axpby_f32(int32_t n, const int32_t* X_off, const int64_t* X_starts,
+                                    int32_t nx, const float* X_vals, float alpha,
+                                    const int32_t* Y_off, const int64_t* Y_starts, int32_t ny,
+                                    const float* Y_vals, float beta, const int32_t* Z_off,
+                                    const int64_t* Z_starts, int32_t nz, float* Z_vals,
+                                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -103,3 +103,20 @@ def test_spgemm_argument_errors():
     assert lib.diagpu_rowpacked_as_hm(0, fake, 1, fake, fake, None) == _lib.ERR_ARG
     assert lib.diagpu_rowpacked_as_hm(10, None, 1, fake, fake, None) == _lib.ERR_ARG
     assert lib.diagpu_rowpacked_as_hm(10, None, 0, None, None, None) == _lib.OK
+
+
+def test_axpby_argument_errors():
+    lib = _lib.load()
+    fake = C.c_void_p(0x1000)
+    args = [100, fake, fake, 2, fake, 1.0, fake, fake, 2, fake, 1.0, fake, fake, 3, fake, None]
+    bad = list(args); bad[0] = 0
+    assert lib.diagpu_dia_axpby_f32(*bad) == _lib.ERR_ARG
+    bad = list(args); bad[13] = -1
+    assert lib.diagpu_dia_axpby_f32(*bad) == _lib.ERR_ARG
+    bad = list(args); bad[14] = None
+    assert lib.diagpu_dia_axpby_f32(*bad) == _lib.ERR_ARG
+    bad = list(args); bad[1] = None
+    assert lib.diagpu_dia_axpby_f32(*bad) == _lib.ERR_ARG
+    assert b"X arrays" in lib.diagpu_last_error()
+    bad = list(args); bad[13] = 0
+    assert lib.diagpu_dia_axpby_f32(*bad) == _lib.OK          # empty Z: no-op

@@ -1,0 +1,143 @@
+"""Matrix-power chain and Taylor series on the GPU (diagpu_amd.chain over
+diagpu_spgemm_symbolic / diagpu_spgemm_numeric_f32 / diagpu_dia_axpby_f32).
+
+The reference describes the chain (spmspm/gather_flat.cuh:13-14,110-117) but
+ships no driver, so there is no reference output to match; the checks are
+the mathematics:
+  - powers against dense float64 matrix powers, |err| <= 1e-5 * k * (|H|^k);
+  - the Taylor sum against scipy.linalg.expm, |err| <= 1e-5 * order *
+    expm(t|H|) + the series' truncation bound;
+  - at 2^20 rows, S x against the float64 recurrence sum_k t^k/k! H^k x;
+  - the diagonal set of every result equals the offset sumset.
+"""
+import math
+
+import numpy as np
+import pytest
+import scipy.linalg
+import torch
+
+from diagpu_amd import chain
+from diagpu_amd.workloads import hm_random, hm_stencil7
+
+pytestmark = pytest.mark.gpu
+
+
+def _sumset(a, b, n):
+    return sorted({x + y for x in a for y in b if abs(x + y) < n})
+
+
+def test_axpby_union(dev):
+    n = 333
+    X = hm_random(n, [-5, 0, 2], 1, dev)
+    Y = hm_random(n, [-5, 1, 2, 100], 2, dev)
+    Z = chain.axpby(0.75, X, -1.5, Y)
+    assert Z.offsets.cpu().tolist() == [-5, 0, 1, 2, 100]
+    Xd, Yd = chain.hm_to_dense(X), chain.hm_to_dense(Y)
+    want = 0.75 * Xd - 1.5 * Yd
+    bound = 0.75 * np.abs(Xd) + 1.5 * np.abs(Yd)
+    assert np.all(np.abs(chain.hm_to_dense(Z) - want) <= 1.2e-7 * bound)
+
+
+def test_axpby_zero_factor_does_not_read(dev):
+    n = 100
+    X = hm_random(n, [-1, 0, 1], 3, dev)
+    Y = hm_random(n, [0, 4], 4, dev)
+    Y.values.fill_(float("nan"))
+    Z = chain.axpby(2.0, X, 0.0, Y)
+    assert Z.offsets.cpu().tolist() == [-1, 0, 1, 4]
+    D = chain.hm_to_dense(Z)
+    assert np.isfinite(D).all()
+    assert np.array_equal(D, 2.0 * chain.hm_to_dense(X))   # exact: scaling by 2
+
+
+def test_axpby_rejects_unsorted(dev):
+    n = 50
+    X = hm_random(n, [0, 1], 5, dev)
+    X.offsets = torch.tensor([1, 0], dtype=torch.int32, device=dev)
+    with pytest.raises(ValueError):
+        chain.axpby(1.0, X, 1.0, None)
+
+
+@pytest.mark.parametrize("n,offs,k", [
+    (257, [-3, -1, 0, 1, 4], 5),
+    (300, [-2, 1], 4),                       # no main diagonal: parity classes
+    (200, [-150, -2, 0, 7, 120], 3),         # offsets near n: clipped sumset
+    (1000, [-16, -4, -1, 0, 1, 4, 16], 6),
+])
+def test_power_against_dense(dev, n, offs, k):
+    H = hm_random(n, offs, 10 + k, dev)
+    P = chain.power(H, k)
+    Hd = chain.hm_to_dense(H)
+    want = np.linalg.matrix_power(Hd, k)
+    bound = np.linalg.matrix_power(np.abs(Hd), k)
+    expect = offs
+    for _ in range(k - 1):
+        expect = _sumset(expect, offs, n)
+    assert P.offsets.cpu().tolist() == expect
+    err = np.abs(chain.hm_to_dense(P) - want)
+    assert np.all(err <= 1e-5 * k * bound + 1e-30), float((err / (bound + 1e-30)).max())
+
+
+@pytest.mark.parametrize("n,offs,t,order", [
+    (240, [-3, -1, 0, 1, 4], 0.2, 12),
+    (180, [-2, 1], 0.5, 14),
+])
+def test_taylor_against_expm(dev, n, offs, t, order):
+    H = hm_random(n, offs, 7, dev)
+    stats = chain.ChainStats()
+    S = chain.taylor_expm(H, t, order, stats)
+    assert len(stats.numeric) == order - 1 and len(stats.axpby) == 2 * order - 1
+    Hd = chain.hm_to_dense(H)
+    want = scipy.linalg.expm(t * Hd)
+    bound = scipy.linalg.expm(t * np.abs(Hd))
+    norm = t * np.abs(Hd).sum(axis=1).max()
+    trunc = norm ** (order + 1) / math.factorial(order + 1) * math.exp(norm)
+    err = np.abs(chain.hm_to_dense(S) - want)
+    assert np.all(err <= 1e-5 * order * bound + trunc)
+    # every offset reachable in at most `order` steps is present
+    reach, frontier = {0}, [0]
+    for _ in range(order):
+        frontier = _sumset(frontier, offs, n)
+        reach |= set(frontier)
+    assert S.offsets.cpu().tolist() == sorted(reach)
+
+
+def test_add_identity_in_place_and_union(dev):
+    n = 90
+    S = hm_random(n, [-3, 0, 2], 12, dev)
+    before = chain.hm_to_dense(S)
+    ptr = S.values.data_ptr()
+    T = chain.add_identity(S, 0.5)
+    assert T is S and T.values.data_ptr() == ptr        # main diagonal present: in place
+    want = before.astype(np.float32) + np.float32(0.5) * np.eye(n, dtype=np.float32)  # one fp32 rounding
+    assert np.array_equal(chain.hm_to_dense(T), want.astype(np.float64))
+    U = hm_random(n, [-3, 2], 13, dev)
+    V = chain.add_identity(U, 2.0)                       # no main diagonal: union
+    assert V.offsets.cpu().tolist() == [-3, 0, 2]
+    assert np.array_equal(chain.hm_to_dense(V), chain.hm_to_dense(U) + 2.0 * np.eye(n))
+
+
+def test_taylor_order_zero_is_identity(dev):
+    H = hm_random(64, [-1, 1], 9, dev)
+    S = chain.taylor_expm(H, 1.0, 0)
+    assert np.array_equal(chain.hm_to_dense(S), np.eye(64))
+
+
+def test_taylor_stencil_2pow20(dev):
+    """The 7-point stencil of SpGEMM config 4 (n = 2^20), order 4:
+    S x against sum_k t^k/k! H^k x in float64 for a random x."""
+    H = hm_stencil7(128, 128, 64, dev)
+    t, order = 0.05, 4
+    S = chain.taylor_expm(H, t, order)
+    assert S.ndiag == 129            # |a| + |b| + |c| <= 4 in three dimensions
+    rng = np.random.default_rng(0)
+    x = rng.uniform(-1.0, 1.0, H.n)
+    want, v = x.copy(), x.copy()
+    for k in range(1, order + 1):
+        v = chain.hm_matvec64(H, v)
+        want += t ** k / math.factorial(k) * v
+    got = chain.hm_matvec64(S, x)
+    # the stencil's absolute row sums are <= 12, so sum_k t^k/k! (|H|^k |x|) <= this
+    abs_bound = sum((t * 12) ** k / math.factorial(k) for k in range(order + 1)) * np.abs(x).max()
+    assert np.all(np.abs(got - want) <= 1e-5 * order * abs_bound)
