@@ -183,3 +183,25 @@ def test_unaligned_pointers_and_side_stream(dev, oracle):
     assert np.isnan(ybuf[:3].cpu().numpy()).all()
     y64, absum = oracle.spmv_recon_ref64(n, n, r_off, r_val, x)
     check_bound(y, y64, absum, TOL32)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 5, 6, 7, 12, 63, 64, 65, 130])
+def test_every_kernel_variant(dev, oracle, K, dtype):
+    """Each K path of the library (straight-line kernel for K <= 5, ring for
+    6..64, grouped ring above 64) in both precisions, with offsets wide enough
+    that several tiles at each end are edge tiles and a ragged last tile
+    (rows not a multiple of the tile).  Padding holds NaN, so a read of any
+    out-of-range Recon entry would show."""
+    rng = np.random.default_rng(1000 * K + (dtype == np.float64))
+    rows, cols = 20011, 19997
+    offs = rng.choice(np.arange(-2600, 2601), size=K, replace=False).astype(np.int32)
+    vals = rng.uniform(-1, 1, size=(K, cols)).astype(dtype)
+    for k, d in enumerate(offs):          # NaN where the row c - d is outside [0, rows)
+        c = np.arange(cols)
+        vals[k][(c - d < 0) | (c - d >= rows)] = np.nan
+    x = rng.standard_normal(cols).astype(dtype)
+    y = gpu_spmv(dev, offs, vals.reshape(-1), rows, cols, x)
+    y64, absum = oracle.spmv_recon_ref64(rows, cols, offs, np.nan_to_num(vals).reshape(-1), x)
+    assert not np.isnan(y).any()
+    check_bound(y, y64, absum, TOL32 if dtype == np.float32 else TOL64)
