@@ -45,8 +45,9 @@ def parse_args(argv=None):
     ap.add_argument("--extras", dest="extras", action="store_true", default=True)
     ap.add_argument("--no-extras", dest="extras", action="store_false")
     ap.add_argument("--only", default="",
-                    help="profiling aid: run just one workload (spmv2, spmv2d, spmv1, spmv3, "
-                         "spgemm4, spgemm5, taylor, copy) and print its line")
+                    help="profiling aid: run just one workload (spmv2, spmv2d, spmv2c, "
+                         "spmv2rc, spmv1, spmv3, spgemm4, spgemm5, taylor, krylov, copy) "
+                         "and print its line")
     return ap.parse_args(argv)
 
 
@@ -58,29 +59,42 @@ def log(msg: str) -> None:
 # SpMV
 # --------------------------------------------------------------------------
 
-def spmv_alg_bytes(R, elem: int) -> int:
-    return elem * (R.useful_terms() + R.cols + R.rows)
+def spmv_alg_bytes(R, elem: int, xelem: int | None = None) -> int:
+    """Values once (matrix element size `elem`), x once and y once (vector
+    element size `xelem`, default `elem`)."""
+    xe = elem if xelem is None else xelem
+    return elem * R.useful_terms() + xe * (R.cols + R.rows)
 
 
-def time_spmv(cfg: int, dtype, steps: int, warmup: int, seed: int, sets: int):
+def time_spmv(cfg: int, dtype, steps: int, warmup: int, seed: int, sets: int, xdtype=None):
+    """One SpMV per step over rotating buffer sets (>= 2x the MALL).  dtype is
+    the matrix dtype, xdtype the vector dtype (default: dtype; complex64
+    vectors with a float32 matrix use the real-matrix complex-state path)."""
     import torch
     from diagpu_amd import workloads
-    from diagpu_amd.spmv import recon_view, _stream_handle
+    from diagpu_amd.spmv import recon_view, _stream_handle, _SPMV
     from diagpu_amd import _lib
     import ctypes as C
 
-    R = workloads.spmv_config(cfg, seed=seed, device="cuda", dtype=dtype)
+    xdtype = xdtype or dtype
+    base = torch.float64 if dtype == torch.float64 else torch.float32
+    R = workloads.spmv_config(cfg, seed=seed, device="cuda", dtype=base)
+    if dtype == torch.complex64:        # complex values: (1 + 0.5i) times the real ones
+        R.values = (R.values * (1 + 0.5j)).to(torch.complex64).contiguous()
+    if xdtype == torch.complex64:
+        R.x = torch.complex(R.x, torch.roll(R.x, 1)).contiguous()
     elem = R.values.element_size()
-    per_set = (R.values.numel() + R.x.numel() + R.rows) * elem
+    xelem = R.x.element_size()
+    per_set = R.values.numel() * elem + (R.x.numel() + R.rows) * xelem
     nsets = sets or max(3, -(-2 * MALL_BYTES // per_set))
     bufs = []
     for _ in range(nsets):
         vals = R.values.clone()
         x = R.x.clone()
-        y = torch.empty(R.rows, dtype=dtype, device="cuda")
+        y = torch.empty(R.rows, dtype=xdtype, device="cuda")
         bufs.append((recon_view(R.offsets, vals, R.rows, R.cols), x, y))
     lib = _lib.load()
-    fn = lib.diagpu_spmv_recon_f32 if dtype == torch.float32 else lib.diagpu_spmv_recon_f64
+    fn = getattr(lib, _SPMV[(dtype, xdtype)])
     stream = torch.cuda.current_stream()
     sh = _stream_handle(stream)
 
@@ -101,8 +115,9 @@ def time_spmv(cfg: int, dtype, steps: int, warmup: int, seed: int, sets: int):
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
-    alg = spmv_alg_bytes(R, elem)
-    flops = 2 * R.useful_terms()
+    alg = spmv_alg_bytes(R, elem, xelem)
+    flops = 2 * R.useful_terms() * (4 if dtype == torch.complex64 else
+                                     2 if xdtype == torch.complex64 else 1)
     return {
         "R": R, "ms": ms, "alg_bytes": alg, "flops": flops, "sets": nsets,
         "set_bytes": per_set, "gbs": alg / (ms * 1e6), "gflops": flops / (ms * 1e6),
@@ -144,16 +159,52 @@ def load_traffic(name: str):
     return None
 
 
-def spmv_record(cfg, dtype, res):
+def spmv_record(cfg, dtype, res, xdtype=None):
     R = res["R"]
+    names = {"torch.float32": "f32", "torch.float64": "f64", "torch.complex64": "c64"}
+    vt = names[str(R.values.dtype)]
+    xt = names[str(R.x.dtype)]
     return {
         "workload": f"spmv_cfg{cfg}",
-        "dtype": "f32" if R.values.element_size() == 4 else "f64",
+        "dtype": vt if vt == xt else f"{vt}x{xt}",
         "n": R.rows, "K": R.K, "ms": round(res["ms"], 6),
         "GBs": round(res["gbs"], 1), "frac_hbm": round(res["gbs"] / HBM_PEAK_GBS, 4),
         "GFLOPs": round(res["gflops"], 1), "alg_bytes": res["alg_bytes"],
         "buffer_sets": res["sets"],
     }
+
+
+def time_krylov(m: int = 30, t: float = 1.0, reps: int = 5):
+    """exp(-i t H) psi_0 by Lanczos on config 2's 5-point stencil (real
+    symmetric H, n = 2^22) with a complex state: one call = m SpMV+dot steps,
+    m update+norm steps, one host sync and the combine pass."""
+    import torch
+    from diagpu_amd import workloads
+    from diagpu_amd.krylov import expm_krylov, KrylovWorkspace
+    R = workloads.spmv_config(2, seed=1, device="cuda", dtype=torch.float32)
+    n = R.rows
+    g = torch.Generator(device="cuda").manual_seed(1)
+    psi0 = torch.complex(torch.randn(n, device="cuda", generator=g),
+                         torch.randn(n, device="cuda", generator=g)).contiguous()
+    ws = KrylovWorkspace(n, m)
+    out = torch.empty_like(psi0)
+    expm_krylov(R.offsets, R.values, n, psi0, t, m, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        res = expm_krylov(R.offsets, R.values, n, psi0, t, m, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / reps
+    # algorithmic bytes: per step SpMV (values 4 B, x and y 8 B, x re-read by
+    # the dot) + update (z, u_j, u_{j-1} read, z written); norm of psi_0 and
+    # the combine (m vectors read, one written)
+    spmv = 4 * R.useful_terms() + 8 * 3 * n
+    upd = 8 * 4 * n
+    alg = m * (spmv + upd) + 8 * n + 8 * (m + 1) * n
+    return {"workload": "expm_krylov_cfg2", "n": n, "m": m, "t": t, "steps_used": res.steps,
+            "err_estimate": res.err_estimate, "ms_per_call": round(ms, 4),
+            "us_per_step": round(ms * 1e3 / m, 2), "alg_bytes": alg,
+            "GBs": round(alg / (ms * 1e6), 1), "frac_hbm": round(alg / (ms * 1e6) / HBM_PEAK_GBS, 4)}
 
 
 # --------------------------------------------------------------------------
@@ -277,9 +328,14 @@ def main(argv=None) -> int:
             print(json.dumps(copy_calibration(args.steps)), flush=True)
         elif w.startswith("spmv"):
             cfg = int(w[4])
-            dt = torch.float64 if w.endswith("d") else torch.float32
-            res = time_spmv(cfg, dt, args.steps, args.warmup, args.seed, args.sets)
-            print(json.dumps(spmv_record(cfg, dt, res)), flush=True)
+            suffix = w[5:]
+            dt, xt = {"": (torch.float32, None), "d": (torch.float64, None),
+                      "c": (torch.complex64, None),
+                      "rc": (torch.float32, torch.complex64)}[suffix]
+            res = time_spmv(cfg, dt, args.steps, args.warmup, args.seed, args.sets, xt)
+            print(json.dumps(spmv_record(cfg, dt, res, xt)), flush=True)
+        elif w == "krylov":
+            print(json.dumps(time_krylov()), flush=True)
         elif w.startswith("spgemm"):
             print(json.dumps(time_spgemm(int(w[6]), args.seed, args.steps)), flush=True)
         elif w == "taylor":
@@ -306,16 +362,18 @@ def main(argv=None) -> int:
 
     extras = {}
     if args.extras:
-        for cfg, dt in [(1, torch.float32), (2, torch.float64), (3, torch.float32)]:
+        for cfg, dt, xt in [(1, torch.float32, None), (2, torch.float64, None),
+                            (3, torch.float32, None), (2, torch.complex64, None),
+                            (2, torch.float32, torch.complex64)]:
             try:
-                res = time_spmv(cfg, dt, 200, 20, args.seed, 0)
-                extras[f"spmv_cfg{cfg}_{'f32' if dt == torch.float32 else 'f64'}"] = \
-                    spmv_record(cfg, dt, res)
-                log(f"extra spmv cfg{cfg} {dt}: {res['gbs']:.1f} GB/s")
+                res = time_spmv(cfg, dt, 200, 20, args.seed, 0, xt)
+                rec = spmv_record(cfg, dt, res, xt)
+                extras[f"spmv_cfg{cfg}_{rec['dtype']}"] = rec
+                log(f"extra spmv cfg{cfg} {rec['dtype']}: {res['gbs']:.1f} GB/s")
                 del res
                 torch.cuda.empty_cache()
             except Exception as e:  # report, keep the headline
-                extras[f"spmv_cfg{cfg}"] = {"error": repr(e)}
+                extras[f"spmv_cfg{cfg}_{dt}_{xt}"] = {"error": repr(e)}
         for cfg in (4, 5):
             try:
                 rec = time_spgemm(cfg, args.seed, 50 if cfg == 4 else 10)
@@ -324,6 +382,13 @@ def main(argv=None) -> int:
                 torch.cuda.empty_cache()
             except Exception as e:
                 extras[f"spgemm_cfg{cfg}"] = {"error": repr(e)}
+        try:
+            rec = time_krylov()
+            extras["krylov_expm"] = rec
+            log(f"extra krylov expm: {rec['ms_per_call']} ms per call, {rec['GBs']} GB/s")
+            torch.cuda.empty_cache()
+        except Exception as e:
+            extras["krylov_expm"] = {"error": repr(e)}
         try:
             rec = time_taylor()
             extras["taylor_chain"] = rec

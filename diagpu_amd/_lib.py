@@ -38,6 +38,16 @@ class ReconViewF64(C.Structure):
                 ("diag_offsets", C.c_void_p), ("values", C.c_void_p)]
 
 
+class ReconViewC64(C.Structure):
+    _fields_ = [("rows", C.c_int32), ("cols", C.c_int32), ("num_diags", C.c_int32),
+                ("diag_offsets", C.c_void_p), ("values", C.c_void_p)]
+
+
+class KrylovInfo(C.Structure):
+    _fields_ = [("steps", C.c_int32), ("breakdown", C.c_int32), ("psi0_norm", C.c_double),
+                ("err_estimate", C.c_double)]
+
+
 class GPair(C.Structure):
     _fields_ = [("ab", C.c_uint64), ("bb", C.c_uint64), ("ash", C.c_int32),
                 ("bsh", C.c_int32), ("al", C.c_int32), ("bl", C.c_int32)]
@@ -57,6 +67,13 @@ PROTOTYPES: dict[str, tuple] = {
     "diagpu_abi_version": (C.c_int, []),
     "diagpu_spmv_recon_f32": (C.c_int, [C.POINTER(ReconViewF32), _vp, _i64, _vp, _vp]),
     "diagpu_spmv_recon_f64": (C.c_int, [C.POINTER(ReconViewF64), _vp, _i64, _vp, _vp]),
+    "diagpu_spmv_recon_c64": (C.c_int, [C.POINTER(ReconViewC64), _vp, _i64, _vp, _vp]),
+    "diagpu_spmv_recon_f32_c64": (C.c_int, [C.POINTER(ReconViewF32), _vp, _i64, _vp, _vp]),
+    "diagpu_expm_krylov_workspace": (C.c_int, [_i32, _i32, C.POINTER(_sz)]),
+    "diagpu_expm_krylov_c64": (C.c_int, [C.POINTER(ReconViewC64), _vp, C.c_double, _i32, _vp,
+                                         _vp, _sz, _vp, _vp, C.POINTER(KrylovInfo), _vp]),
+    "diagpu_expm_krylov_f32": (C.c_int, [C.POINTER(ReconViewF32), _vp, C.c_double, _i32, _vp,
+                                         _vp, _sz, _vp, _vp, C.POINTER(KrylovInfo), _vp]),
     "diagpu_spgemm_symbolic_workspace": (C.c_int, [_i32, _i32, _i32, C.POINTER(_sz)]),
     "diagpu_spgemm_symbolic": (C.c_int, [
         _i32,

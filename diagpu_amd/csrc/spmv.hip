@@ -9,14 +9,19 @@
 // HBM stream: every useful value is read once and fused into its row's
 // accumulator.
 //
-// Mapping.  A workgroup of 256 lanes owns a tile of 256 x R consecutive rows,
-// R = 16 / sizeof(T) (4 floats or 2 doubles): each lane owns R consecutive
-// rows r..r+R-1.  For diagonal k the lane needs Recon[k][r+d_k ..] and
-// x[r+d_k ..]: both are 16-byte runs at the same column, one 128-bit load
-// each (dword aligned: gfx950 serves unaligned global loads), and the 64
-// lanes of a wave cover 1 KiB of each stream.  Value loads and the y store are
-// non-temporal: each value is used once, while x stays in L2 for the tiles
-// that re-read it.
+// Element types.  One kernel family serves real fp32 and fp64, complex64
+// matrices with complex64 vectors, and real fp32 matrices with complex64
+// vectors (a real Hamiltonian applied to a complex state: the matrix is read
+// once for both parts of x).  A lane owns R rows with R * sizeof(matrix
+// element) = 16 bytes; its x run and y run are R vector elements (16 or 32
+// bytes).
+//
+// Mapping.  A workgroup of 256 lanes owns a tile of 256 x R consecutive rows.
+// For diagonal k the lane needs Recon[k][r+d_k ..] and x[r+d_k ..]: runs at
+// the same column, loaded as 16-byte vectors (dword aligned: gfx950 serves
+// unaligned global loads); the 64 lanes of a wave cover 1 KiB of each
+// stream.  Value loads and the y store are non-temporal: each value is used
+// once, while x stays in L2 for the tiles that re-read it.
 //
 // Memory-level parallelism.  What bounds this kernel is how many HBM bytes
 // each CU keeps in flight, not the x re-reads or the misalignment (measured:
@@ -24,84 +29,150 @@
 // adding the x loads costs 3 points).  So loads are never drained in chunks:
 // the ring kernel keeps W diagonals' loads in flight per lane at all times --
 // step j consumes slot j and refills it with the diagonal W ahead, and
-// sched_barrier pins that order so the compiler emits a steady
-// s_waitcnt vmcnt(2W-2) instead of hoisting or sinking the loads.  Offsets
-// travel 64 at a time in one VGPR (lane l holds d_{g0+l}) and are broadcast
-// with readlane, which needs no memory wait.  For K <= 5 the short kernel
-// takes the offsets with scalar loads (the scalar cache does not queue behind
-// the HBM stream) and issues all 2K loads straight-line.
+// sched_barrier pins that order so the compiler emits a steady vmcnt window
+// instead of hoisting or sinking the loads.  Offsets travel 64 at a time in
+// one VGPR (lane l holds d_{g0+l}) and are broadcast with readlane, which
+// needs no memory wait.  For K <= 5 the short kernel takes the offsets with
+// scalar loads (the scalar cache does not queue behind the HBM stream) and
+// issues all 2K loads straight-line.
 //
 // Edge tiles.  A tile whose rows or columns leave the matrix for some
 // diagonal runs the same ring with per-element loads at clamped (always
-// valid) columns and masked FMAs: no branch around a load, so the loads
-// pipeline like the interior ones.  An edge tile is also dispatched early
-// (odd XCDs walk their row range from the end), since the slowest tile sets
-// the kernel's end.
+// valid) columns and masked accumulation: no branch around a load, so the
+// loads pipeline like the interior ones.  An edge tile is also dispatched
+// early (odd XCDs walk their row range from the end), since the slowest tile
+// sets the kernel's end.
 //
 // XCD awareness: workgroup b runs on XCD b mod 8; tiles are remapped so each
 // XCD owns one contiguous eighth of the rows.  x[c] is used by rows c - d_k
 // of every diagonal, i.e. by this tile and by tiles up to max|d_k| rows away,
 // which then sit on the same XCD and find x in its L2.
+//
+// Dot epilogue (Krylov drivers).  With DOT, each workgroup also forms
+// sum_r Re(conj(x[r]) * y[r]) over its rows in fp64 and stores it as one
+// partial; a one-workgroup kernel launched next adds the partials in tile
+// order (a deterministic result).
 #include <climits>
 
 #include "common.hpp"
+#include "reduce.hpp"
+#include "spmv_internal.hpp"
 
 namespace diagpu {
 namespace {
 
 constexpr int kBlock = 256;
-
-template <typename T> struct Vec16;   // 16 bytes of T, element-aligned
-template <> struct Vec16<float> {
-    typedef float type __attribute__((ext_vector_type(4), aligned(4)));
-};
-template <> struct Vec16<double> {
-    typedef double type __attribute__((ext_vector_type(2), aligned(8)));
-};
-
-template <typename T> constexpr int rows_per_lane() { return 16 / (int)sizeof(T); }
-template <typename T> constexpr int tile_rows() { return kBlock * rows_per_lane<T>(); }
-
-// Diagonals in flight per lane: interior ring (16-byte loads) and edge ring
-// (per-element loads).  Chosen so the kernel stays within 64 VGPRs (8 waves
-// per SIMD).
-constexpr int kRing = 6;
-constexpr int kRingEdge = 3;
 constexpr int kShortMax = 5;   // K <= kShortMax: straight-line kernel
 
-template <typename T>
-__device__ __forceinline__ typename Vec16<T>::type ld16_stream(const T* p)
-{
-    return __builtin_nontemporal_load(reinterpret_cast<const typename Vec16<T>::type*>(p));
-}
-template <typename T>
-__device__ __forceinline__ typename Vec16<T>::type ld16(const T* p)
-{
-    return *reinterpret_cast<const typename Vec16<T>::type*>(p);
-}
-template <typename T>
-__device__ __forceinline__ void st16_stream(T* p, typename Vec16<T>::type v)
-{
-    __builtin_nontemporal_store(v, reinterpret_cast<typename Vec16<T>::type*>(p));
-}
+// ---------------------------------------------------------------------------
+// Element types and arithmetic
+// ---------------------------------------------------------------------------
 
-__device__ __forceinline__ float fma_(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
-__device__ __forceinline__ double fma_(double a, double b, double c) { return __builtin_fma(a, b, c); }
+inline __device__ float fma_(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+inline __device__ double fma_(double a, double b, double c) { return __builtin_fma(a, b, c); }
 
-// Lane-wise helpers on 16-byte vectors.
-template <typename V>
-__device__ __forceinline__ V vfma(const V& a, const V& b, const V& c)
+// acc + a * x for (matrix element, vector element)
+inline __device__ float mad(float acc, float a, float x) { return fma_(a, x, acc); }
+inline __device__ double mad(double acc, double a, double x) { return fma_(a, x, acc); }
+inline __device__ cf32 mad(cf32 acc, cf32 a, cf32 x)
 {
-    V r;
-#pragma unroll
-    for (int e = 0; e < (int)(16 / sizeof(a[0])); ++e) r[e] = fma_(a[e], b[e], c[e]);
+    cf32 r;
+    r.re = fma_(-a.im, x.im, fma_(a.re, x.re, acc.re));
+    r.im = fma_(a.im, x.re, fma_(a.re, x.im, acc.im));
     return r;
 }
+inline __device__ cf32 mad(cf32 acc, float a, cf32 x)
+{
+    cf32 r;
+    r.re = fma_(a, x.re, acc.re);
+    r.im = fma_(a, x.im, acc.im);
+    return r;
+}
+
+inline __device__ float sel(bool c, float a, float b) { return c ? a : b; }
+inline __device__ double sel(bool c, double a, double b) { return c ? a : b; }
+inline __device__ cf32 sel(bool c, cf32 a, cf32 b)
+{
+    cf32 r;
+    r.re = c ? a.re : b.re;
+    r.im = c ? a.im : b.im;
+    return r;
+}
+
+template <typename T> inline __device__ T zero_of();
+template <> inline __device__ float zero_of<float>() { return 0.f; }
+template <> inline __device__ double zero_of<double>() { return 0.0; }
+template <> inline __device__ cf32 zero_of<cf32>() { return cf32{0.f, 0.f}; }
+
+// Re(conj(u) * y) in fp64
+inline __device__ double dotpart(float u, float y) { return (double)u * (double)y; }
+inline __device__ double dotpart(double u, double y) { return u * y; }
+inline __device__ double dotpart(cf32 u, cf32 y) { return (double)u.re * y.re + (double)u.im * y.im; }
+
+// One element, loaded as a plain vector register value.
+template <typename T> struct ElemRaw { typedef T type; };
+template <> struct ElemRaw<cf32> { typedef float type __attribute__((ext_vector_type(2))); };
+
+template <typename T, bool NT>
+inline __device__ T load_elem(const T* p)
+{
+    typedef typename ElemRaw<T>::type Raw;
+    Raw v = NT ? __builtin_nontemporal_load(reinterpret_cast<const Raw*>(p))
+               : *reinterpret_cast<const Raw*>(p);
+    T r;
+    __builtin_memcpy(&r, &v, sizeof(T));
+    return r;
+}
+
+// A lane's run of R consecutive elements (16 or 32 bytes), moved as 16-byte
+// vectors.
+template <typename T, int R> struct Run { T v[R]; };
+
+typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
+
+template <typename T, int R, bool NT>
+inline __device__ Run<T, R> load_run(const T* p)
+{
+    static_assert((R * sizeof(T)) % 16 == 0, "runs are whole 16-byte vectors");
+    constexpr int NQ = (int)(R * sizeof(T) / 16);
+    f4u q[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; ++i)
+        q[i] = NT ? __builtin_nontemporal_load(reinterpret_cast<const f4u*>(p) + i)
+                  : reinterpret_cast<const f4u*>(p)[i];
+    Run<T, R> r;
+    __builtin_memcpy(&r, q, sizeof(r));
+    return r;
+}
+
+template <typename T, int R>
+inline __device__ void store_run_nt(T* p, const Run<T, R>& r)
+{
+    constexpr int NQ = (int)(R * sizeof(T) / 16);
+    f4u q[NQ];
+    __builtin_memcpy(q, &r, sizeof(r));
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) __builtin_nontemporal_store(q[i], reinterpret_cast<f4u*>(p) + i);
+}
+
+// Per (matrix element, vector element) pair: rows per lane and ring depths,
+// chosen so the kernels stay within 64 VGPRs (8 waves per SIMD).
+template <typename TV, typename TX> struct Shape {
+    static constexpr int R = (int)(16 / sizeof(TV));
+    static constexpr bool wide_x = R * sizeof(TX) > 16;   // 32-byte x runs
+    static constexpr int W = wide_x ? 4 : 6;              // interior ring
+    static constexpr int WE = wide_x ? 2 : 3;             // edge ring
+    static constexpr int TILE = kBlock * R;
+};
+
+// ---------------------------------------------------------------------------
+// Shared pieces
+// ---------------------------------------------------------------------------
 
 // Tile index of workgroup b: XCD x = b mod 8 owns tiles [x*per_xcd,
 // (x+1)*per_xcd); even XCDs walk their range upwards, odd ones downwards, so
 // the last tile of the matrix (an edge tile) is among the first dispatched.
-__device__ __forceinline__ int tile_of_block(int per_xcd)
+inline __device__ int tile_of_block(int per_xcd)
 {
     const int x = (int)(blockIdx.x % kNumXcd);
     const int l = (int)(blockIdx.x / kNumXcd);
@@ -110,7 +181,7 @@ __device__ __forceinline__ int tile_of_block(int per_xcd)
 
 // min and max of a group of offsets held one per lane (lanes >= gn hold a
 // copy of a valid offset), uniform across the wave.
-__device__ __forceinline__ void wave_minmax(int v, int& lo, int& hi)
+inline __device__ void wave_minmax(int v, int& lo, int& hi)
 {
     int a = v, b = v;
 #pragma unroll
@@ -126,20 +197,21 @@ __device__ __forceinline__ void wave_minmax(int v, int& lo, int& hi)
 
 // One group of gn <= 64 diagonals (offsets in `ov`, lane l = d_{g0+l};
 // values `vg` = Recon row g0) accumulated into `acc` for the lane's R rows
-// starting at row `r`.  W loads in flight; every index is clamped to the
-// group so all loads are valid, and the slots past the group are masked.
+// starting at row `r`.  W diagonals' loads in flight; every index is clamped
+// to the group so all loads are valid, and the slots past the group are
+// masked.
 //
 // EDGE = false: the whole tile is in range (rows < `rows`, every column in
-// [0, lim)); 16-byte loads.  EDGE = true: per-element loads at columns
+// [0, lim)); 16-byte vector loads.  EDGE = true: per-element loads at columns
 // clamped into [0, lim), terms whose column is outside masked.
-template <typename T, int W, bool EDGE>
+template <typename TV, typename TX, int W, bool EDGE>
 __device__ __forceinline__ void ring_group(int64_t r, int64_t cols, int64_t lim, int gn, int ov,
-                                           const T* __restrict__ vg, const T* __restrict__ x,
-                                           typename Vec16<T>::type& acc)
+                                           const TV* __restrict__ vg, const TX* __restrict__ x,
+                                           Run<TX, Shape<TV, TX>::R>& acc)
 {
-    typedef typename Vec16<T>::type V;
-    constexpr int R = rows_per_lane<T>();
-    V a[W], b[W];
+    constexpr int R = Shape<TV, TX>::R;
+    Run<TV, R> a[W];
+    Run<TX, R> b[W];
     // EDGE: the lane's first column for the slot's diagonal, clamped to
     // [-R, lim] (a column outside that range is as out of range as its clamp)
     int32_t c0[W];
@@ -147,33 +219,30 @@ __device__ __forceinline__ void ring_group(int64_t r, int64_t cols, int64_t lim,
     auto issue = [&](int j, int k) {
         const int d = __builtin_amdgcn_readlane(ov, k);
         if constexpr (!EDGE) {
-            a[j] = ld16_stream<T>(vg + (int64_t)k * cols + r + d);
-            b[j] = ld16<T>(x + r + d);
+            a[j] = load_run<TV, R, true>(vg + (int64_t)k * cols + r + d);
+            b[j] = load_run<TX, R, false>(x + r + d);
         } else {
             const int64_t c = r + d;
             c0[j] = (int32_t)(c < -R ? -R : (c > lim ? lim : c));
-            const T* vk = vg + (int64_t)k * cols;
+            const TV* vk = vg + (int64_t)k * cols;
 #pragma unroll
             for (int e = 0; e < R; ++e) {
                 int64_t cc = c + e;
                 cc = cc < 0 ? 0 : (cc >= lim ? lim - 1 : cc);   // always a valid address
-                a[j][e] = __builtin_nontemporal_load(vk + (uint32_t)cc);
-                b[j][e] = x[(uint32_t)cc];
+                a[j].v[e] = load_elem<TV, true>(vk + (uint32_t)cc);
+                b[j].v[e] = load_elem<TX, false>(x + (uint32_t)cc);
             }
         }
     };
     auto consume = [&](int j, bool on) {
-        if constexpr (!EDGE) {
-            const V t = vfma(a[j], b[j], acc);
-            acc = on ? t : acc;
-        } else {
 #pragma unroll
-            for (int e = 0; e < R; ++e) {
+        for (int e = 0; e < R; ++e) {
+            bool ok = on;
+            if constexpr (EDGE) {
                 const int64_t c = (int64_t)c0[j] + e;
-                const bool ok = on && c >= 0 && c < lim;
-                const T t = fma_(a[j][e], b[j][e], acc[e]);
-                acc[e] = ok ? t : acc[e];
+                ok = ok && c >= 0 && c < lim;
             }
+            acc.v[e] = sel(ok, mad(acc.v[e], a[j].v[e], b[j].v[e]), acc.v[e]);
         }
     };
 
@@ -205,34 +274,58 @@ __device__ __forceinline__ void ring_group(int64_t r, int64_t cols, int64_t lim,
     for (int j = 0; j < W - 1; ++j) consume(j, k0 + W + j < gn);
 }
 
-template <typename T>
-__device__ __forceinline__ void store_rows(T* __restrict__ y, int64_t r, int64_t rows,
-                                           const typename Vec16<T>::type& acc, bool full)
+template <typename TX, int R>
+__device__ __forceinline__ void store_rows(TX* __restrict__ y, int64_t r, int64_t rows,
+                                           const Run<TX, R>& acc, bool full)
 {
     if (full) {
-        st16_stream<T>(y + r, acc);
+        store_run_nt<TX, R>(y + r, acc);
     } else {
 #pragma unroll
-        for (int e = 0; e < rows_per_lane<T>(); ++e)
-            if (r + e < rows) y[r + e] = acc[e];
+        for (int e = 0; e < R; ++e)
+            if (r + e < rows) y[r + e] = acc.v[e];
     }
 }
 
+// DOT epilogue: see the file comment.  x must hold the lane's rows
+// (x_size >= rows, checked by the host).
+template <typename TX, int R>
+__device__ __forceinline__ void dot_epilogue(const Run<TX, R>& acc, const TX* __restrict__ x,
+                                             int64_t r, int64_t rows, bool full, int tile,
+                                             int tiles, const DotArgs& da)
+{
+    double s = 0.0;
+    if (full) {
+        const Run<TX, R> u = load_run<TX, R, false>(x + r);
+#pragma unroll
+        for (int e = 0; e < R; ++e) s += dotpart(u.v[e], acc.v[e]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < R; ++e)
+            if (r + e < rows) s += dotpart(x[r + e], acc.v[e]);
+    }
+    store_partial<kBlock>(s, tile, da.partials);
+}
+
+// ---------------------------------------------------------------------------
+// Kernels
+// ---------------------------------------------------------------------------
+
 // General K: groups of 64 diagonals, each through the ring (MULTI = false:
 // K <= 64, one group, the offsets VGPR loaded once).
-template <typename T, bool MULTI>
+template <typename TV, typename TX, bool MULTI, bool DOT>
 __global__ __launch_bounds__(kBlock) void spmv_ring_kernel(
     int32_t rows, int32_t cols, int64_t lim, int32_t K, const int32_t* __restrict__ offs,
-    const T* __restrict__ vals, const T* __restrict__ x, T* __restrict__ y, int32_t tiles,
-    int32_t per_xcd)
+    const TV* __restrict__ vals, const TX* __restrict__ x, TX* __restrict__ y, int32_t tiles,
+    int32_t per_xcd, DotArgs da)
 {
-    typedef typename Vec16<T>::type V;
-    constexpr int TILE = tile_rows<T>();
+    typedef Shape<TV, TX> S;
+    constexpr int R = S::R;
     const int tile = tile_of_block(per_xcd);
     if (tile >= tiles) return;
     const int lane = (int)threadIdx.x & 63;
-    const int64_t r0 = (int64_t)tile * TILE;
-    const int64_t r = r0 + (int64_t)threadIdx.x * rows_per_lane<T>();
+    const int64_t r0 = (int64_t)tile * S::TILE;
+    const int64_t r = r0 + (int64_t)threadIdx.x * R;
 
     // offset range over all groups (one vector load per 64 offsets)
     const int g0n = K < 64 ? K : 64;
@@ -248,43 +341,45 @@ __global__ __launch_bounds__(kBlock) void spmv_ring_kernel(
             dmax = hi > dmax ? hi : dmax;
         }
     }
-    const bool interior = r0 + TILE <= rows && r0 + dmin >= 0 && r0 + TILE + (int64_t)dmax <= lim;
+    const bool interior =
+        r0 + S::TILE <= rows && r0 + dmin >= 0 && r0 + S::TILE + (int64_t)dmax <= lim;
 
-    V acc;
+    Run<TX, R> acc;
 #pragma unroll
-    for (int e = 0; e < rows_per_lane<T>(); ++e) acc[e] = T(0);
+    for (int e = 0; e < R; ++e) acc.v[e] = zero_of<TX>();
     if constexpr (!MULTI) {
         if (interior)
-            ring_group<T, kRing, false>(r, cols, lim, K, ov0, vals, x, acc);
+            ring_group<TV, TX, S::W, false>(r, cols, lim, K, ov0, vals, x, acc);
         else
-            ring_group<T, kRingEdge, true>(r, cols, lim, K, ov0, vals, x, acc);
+            ring_group<TV, TX, S::WE, true>(r, cols, lim, K, ov0, vals, x, acc);
     } else {
         for (int g0 = 0; g0 < K; g0 += 64) {
             const int gn = (K - g0) < 64 ? (K - g0) : 64;
             const int ov = g0 == 0 ? ov0 : offs[g0 + (lane < gn ? lane : gn - 1)];
-            const T* vg = vals + (int64_t)g0 * cols;
+            const TV* vg = vals + (int64_t)g0 * cols;
             if (interior)
-                ring_group<T, kRing, false>(r, cols, lim, gn, ov, vg, x, acc);
+                ring_group<TV, TX, S::W, false>(r, cols, lim, gn, ov, vg, x, acc);
             else
-                ring_group<T, kRingEdge, true>(r, cols, lim, gn, ov, vg, x, acc);
+                ring_group<TV, TX, S::WE, true>(r, cols, lim, gn, ov, vg, x, acc);
         }
     }
-    store_rows<T>(y, r, rows, acc, interior);
+    store_rows<TX, R>(y, r, rows, acc, interior);
+    if constexpr (DOT) dot_epilogue<TX, R>(acc, x, r, rows, interior, tile, tiles, da);
 }
 
 // K == KF <= kShortMax: offsets by scalar loads, all 2K loads straight-line.
-template <typename T, int KF>
+template <typename TV, typename TX, int KF, bool DOT>
 __global__ __launch_bounds__(kBlock) void spmv_short_kernel(
     int32_t rows, int32_t cols, int64_t lim, int32_t K, const int32_t* __restrict__ offs,
-    const T* __restrict__ vals, const T* __restrict__ x, T* __restrict__ y, int32_t tiles,
-    int32_t per_xcd)
+    const TV* __restrict__ vals, const TX* __restrict__ x, TX* __restrict__ y, int32_t tiles,
+    int32_t per_xcd, DotArgs da)
 {
-    typedef typename Vec16<T>::type V;
-    constexpr int TILE = tile_rows<T>();
+    typedef Shape<TV, TX> S;
+    constexpr int R = S::R;
     const int tile = tile_of_block(per_xcd);
     if (tile >= tiles) return;
-    const int64_t r0 = (int64_t)tile * TILE;
-    const int64_t r = r0 + (int64_t)threadIdx.x * rows_per_lane<T>();
+    const int64_t r0 = (int64_t)tile * S::TILE;
+    const int64_t r = r0 + (int64_t)threadIdx.x * R;
     (void)K;
 
     int d[KF > 0 ? KF : 1];
@@ -295,77 +390,124 @@ __global__ __launch_bounds__(kBlock) void spmv_short_kernel(
         dmin = d[k] < dmin ? d[k] : dmin;
         dmax = d[k] > dmax ? d[k] : dmax;
     }
-    const bool interior =
-        r0 + TILE <= rows && (KF == 0 || (r0 + dmin >= 0 && r0 + TILE + (int64_t)dmax <= lim));
+    const bool interior = r0 + S::TILE <= rows &&
+                          (KF == 0 || (r0 + dmin >= 0 && r0 + S::TILE + (int64_t)dmax <= lim));
 
-    V acc;
+    Run<TX, R> acc;
 #pragma unroll
-    for (int e = 0; e < rows_per_lane<T>(); ++e) acc[e] = T(0);
+    for (int e = 0; e < R; ++e) acc.v[e] = zero_of<TX>();
     if constexpr (KF > 0) {
         if (interior) {
-            V a[KF], b[KF];
+            Run<TV, R> a[KF];
+            Run<TX, R> b[KF];
 #pragma unroll
             for (int k = 0; k < KF; ++k) {
-                a[k] = ld16_stream<T>(vals + (int64_t)k * cols + r + d[k]);
-                b[k] = ld16<T>(x + r + d[k]);
+                a[k] = load_run<TV, R, true>(vals + (int64_t)k * cols + r + d[k]);
+                b[k] = load_run<TX, R, false>(x + r + d[k]);
             }
 #pragma unroll
-            for (int k = 0; k < KF; ++k) acc = vfma(a[k], b[k], acc);
+            for (int k = 0; k < KF; ++k)
+#pragma unroll
+                for (int e = 0; e < R; ++e) acc.v[e] = mad(acc.v[e], a[k].v[e], b[k].v[e]);
         } else {
             const int lane = (int)threadIdx.x & 63;
             const int ov = offs[lane < KF ? lane : KF - 1];
-            ring_group<T, kRingEdge, true>(r, cols, lim, KF, ov, vals, x, acc);
+            ring_group<TV, TX, S::WE, true>(r, cols, lim, KF, ov, vals, x, acc);
         }
     }
-    store_rows<T>(y, r, rows, acc, interior);
+    store_rows<TX, R>(y, r, rows, acc, interior);
+    if constexpr (DOT) dot_epilogue<TX, R>(acc, x, r, rows, interior, tile, tiles, da);
 }
 
-template <typename T>
-using SpmvKernel = void (*)(int32_t, int32_t, int64_t, int32_t, const int32_t*, const T*,
-                            const T*, T*, int32_t, int32_t);
+template <typename TV, typename TX>
+using SpmvKernel = void (*)(int32_t, int32_t, int64_t, int32_t, const int32_t*, const TV*,
+                            const TX*, TX*, int32_t, int32_t, DotArgs);
 
-template <typename T>
-SpmvKernel<T> pick_kernel(int K)
+template <typename TV, typename TX, bool DOT>
+SpmvKernel<TV, TX> pick_kernel(int K)
 {
     switch (K) {
-    case 0: return spmv_short_kernel<T, 0>;
-    case 1: return spmv_short_kernel<T, 1>;
-    case 2: return spmv_short_kernel<T, 2>;
-    case 3: return spmv_short_kernel<T, 3>;
-    case 4: return spmv_short_kernel<T, 4>;
-    case 5: return spmv_short_kernel<T, 5>;
-    default: return K <= 64 ? spmv_ring_kernel<T, false> : spmv_ring_kernel<T, true>;
+    case 0: return spmv_short_kernel<TV, TX, 0, DOT>;
+    case 1: return spmv_short_kernel<TV, TX, 1, DOT>;
+    case 2: return spmv_short_kernel<TV, TX, 2, DOT>;
+    case 3: return spmv_short_kernel<TV, TX, 3, DOT>;
+    case 4: return spmv_short_kernel<TV, TX, 4, DOT>;
+    case 5: return spmv_short_kernel<TV, TX, 5, DOT>;
+    default:
+        return K <= 64 ? spmv_ring_kernel<TV, TX, false, DOT> : spmv_ring_kernel<TV, TX, true, DOT>;
     }
 }
 static_assert(kShortMax == 5, "pick_kernel covers K = 0..5");
 
-template <typename T, typename View>
-int spmv_launch(const View* R, const T* x, int64_t x_size, T* y, void* stream, const char* name)
+}  // namespace
+
+template <typename TV, typename TX>
+int32_t spmv_tiles(int32_t rows)
 {
-    if (!R) return fail(DIAGPU_ERR_ARG, "%s: R is NULL", name);
-    if (R->rows < 0 || R->cols < 0 || R->num_diags < 0)
-        return fail(DIAGPU_ERR_ARG, "%s: negative size (rows=%d cols=%d num_diags=%d)", name,
-                    R->rows, R->cols, R->num_diags);
-    if (x_size < 0) return fail(DIAGPU_ERR_ARG, "%s: negative x_size %lld", name, (long long)x_size);
-    if (R->rows == 0) return DIAGPU_OK;
-    if (!y) return fail(DIAGPU_ERR_ARG, "%s: y is NULL", name);
-    const int64_t lim = x_size < R->cols ? x_size : (int64_t)R->cols;
-    int K = R->num_diags;
-    if (K > 0) {
-        if (!R->diag_offsets) return fail(DIAGPU_ERR_ARG, "%s: diag_offsets is NULL", name);
-        if (R->cols > 0 && !R->values) return fail(DIAGPU_ERR_ARG, "%s: values is NULL", name);
-        if (lim > 0 && !x) return fail(DIAGPU_ERR_ARG, "%s: x is NULL", name);
-    }
-    if (lim == 0) K = 0;   // no column in range: y = 0 without touching values or x
-    const int32_t tiles = (int32_t)ceil_div<int64_t>(R->rows, tile_rows<T>());
-    const int32_t per_xcd = ceil_div<int32_t>(tiles, kNumXcd);
-    hipLaunchKernelGGL(pick_kernel<T>(K), dim3(per_xcd * kNumXcd), dim3(kBlock), 0,
-                       as_stream(stream), R->rows, R->cols, lim, K, R->diag_offsets, R->values, x,
-                       y, tiles, per_xcd);
-    return check_launch(name);
+    return (int32_t)ceil_div<int64_t>(rows, Shape<TV, TX>::TILE);
 }
 
+template <typename TV, typename TX>
+int spmv_run(int32_t rows, int32_t cols, int32_t num_diags, const int32_t* offs, const TV* vals,
+             const TX* x, int64_t x_size, TX* y, const DotArgs* dot, void* stream,
+             const char* name)
+{
+    if (rows < 0 || cols < 0 || num_diags < 0)
+        return fail(DIAGPU_ERR_ARG, "%s: negative size (rows=%d cols=%d num_diags=%d)", name,
+                    rows, cols, num_diags);
+    if (x_size < 0) return fail(DIAGPU_ERR_ARG, "%s: negative x_size %lld", name, (long long)x_size);
+    if (rows == 0) return DIAGPU_OK;
+    if (!y) return fail(DIAGPU_ERR_ARG, "%s: y is NULL", name);
+    const int64_t lim = x_size < cols ? x_size : (int64_t)cols;
+    int K = num_diags;
+    if (K > 0) {
+        if (!offs) return fail(DIAGPU_ERR_ARG, "%s: diag_offsets is NULL", name);
+        if (cols > 0 && !vals) return fail(DIAGPU_ERR_ARG, "%s: values is NULL", name);
+        if (lim > 0 && !x) return fail(DIAGPU_ERR_ARG, "%s: x is NULL", name);
+    }
+    if (dot && (x_size < rows || !x || !dot->partials || !dot->out))
+        return fail(DIAGPU_ERR_ARG, "%s: the dot epilogue needs x_size >= rows and its buffers",
+                    name);
+    if (lim == 0) K = 0;   // no column in range: y = 0 without touching values or x
+    const int32_t tiles = spmv_tiles<TV, TX>(rows);
+    const int32_t per_xcd = ceil_div<int32_t>(tiles, kNumXcd);
+    const DotArgs da = dot ? *dot : DotArgs{nullptr, nullptr};
+    hipLaunchKernelGGL((dot ? pick_kernel<TV, TX, true>(K) : pick_kernel<TV, TX, false>(K)),
+                       dim3(per_xcd * kNumXcd), dim3(kBlock), 0, as_stream(stream), rows, cols,
+                       lim, K, offs, vals, x, y, tiles, per_xcd, da);
+    const int st = check_launch(name);
+    if (st || !dot) return st;
+    return sum_partials(dot->partials, tiles, dot->out, stream);
+}
+
+namespace {
+__global__ __launch_bounds__(kBlock) void k_sum_partials(const double* __restrict__ partials,
+                                                         int32_t n, double* __restrict__ out)
+{
+    double t = 0.0;
+    for (int i = (int)threadIdx.x; i < n; i += kBlock) t += partials[i];
+    t = block_sum<kBlock>(t);
+    if (threadIdx.x == 0) *out = t;
+}
 }  // namespace
+
+int sum_partials(const double* partials, int32_t n, double* out, void* stream)
+{
+    hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(kBlock), 0, as_stream(stream), partials, n,
+                       out);
+    return check_launch("sum_partials");
+}
+
+#define DIAGPU_SPMV_INSTANCE(TV, TX)                                                          \
+    template int32_t spmv_tiles<TV, TX>(int32_t);                                             \
+    template int spmv_run<TV, TX>(int32_t, int32_t, int32_t, const int32_t*, const TV*,       \
+                                  const TX*, int64_t, TX*, const DotArgs*, void*, const char*);
+DIAGPU_SPMV_INSTANCE(float, float)
+DIAGPU_SPMV_INSTANCE(double, double)
+DIAGPU_SPMV_INSTANCE(cf32, cf32)
+DIAGPU_SPMV_INSTANCE(float, cf32)
+#undef DIAGPU_SPMV_INSTANCE
+
 }  // namespace diagpu
 
 extern "C" {
@@ -373,13 +515,43 @@ extern "C" {
 DIAGPU_API int diagpu_spmv_recon_f32(const diagpu_recon_view_f32* R, const float* x,
                                      int64_t x_size, float* y, void* stream)
 {
-    return diagpu::spmv_launch<float>(R, x, x_size, y, stream, "diagpu_spmv_recon_f32");
+    const char* fn = "diagpu_spmv_recon_f32";
+    if (!R) return diagpu::fail(DIAGPU_ERR_ARG, "%s: R is NULL", fn);
+    return diagpu::spmv_run<float, float>(R->rows, R->cols, R->num_diags, R->diag_offsets,
+                                          R->values, x, x_size, y, nullptr, stream, fn);
 }
 
 DIAGPU_API int diagpu_spmv_recon_f64(const diagpu_recon_view_f64* R, const double* x,
                                      int64_t x_size, double* y, void* stream)
 {
-    return diagpu::spmv_launch<double>(R, x, x_size, y, stream, "diagpu_spmv_recon_f64");
+    const char* fn = "diagpu_spmv_recon_f64";
+    if (!R) return diagpu::fail(DIAGPU_ERR_ARG, "%s: R is NULL", fn);
+    return diagpu::spmv_run<double, double>(R->rows, R->cols, R->num_diags, R->diag_offsets,
+                                            R->values, x, x_size, y, nullptr, stream, fn);
+}
+
+DIAGPU_API int diagpu_spmv_recon_c64(const diagpu_recon_view_c64* R, const diagpu_complex64* x,
+                                     int64_t x_size, diagpu_complex64* y, void* stream)
+{
+    using diagpu::cf32;
+    const char* fn = "diagpu_spmv_recon_c64";
+    if (!R) return diagpu::fail(DIAGPU_ERR_ARG, "%s: R is NULL", fn);
+    return diagpu::spmv_run<cf32, cf32>(R->rows, R->cols, R->num_diags, R->diag_offsets,
+                                        reinterpret_cast<const cf32*>(R->values),
+                                        reinterpret_cast<const cf32*>(x), x_size,
+                                        reinterpret_cast<cf32*>(y), nullptr, stream, fn);
+}
+
+DIAGPU_API int diagpu_spmv_recon_f32_c64(const diagpu_recon_view_f32* R,
+                                         const diagpu_complex64* x, int64_t x_size,
+                                         diagpu_complex64* y, void* stream)
+{
+    using diagpu::cf32;
+    const char* fn = "diagpu_spmv_recon_f32_c64";
+    if (!R) return diagpu::fail(DIAGPU_ERR_ARG, "%s: R is NULL", fn);
+    return diagpu::spmv_run<float, cf32>(R->rows, R->cols, R->num_diags, R->diag_offsets,
+                                         R->values, reinterpret_cast<const cf32*>(x), x_size,
+                                         reinterpret_cast<cf32*>(y), nullptr, stream, fn);
 }
 
 }  // extern "C"

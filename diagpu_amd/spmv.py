@@ -3,7 +3,7 @@ spmv/src/dia_reconstruct.cuh:61-118, the launcher of
 spmv/src/tc_spmv_regdirect_kernel.cu:135-147).
 
 torch tensors only carry device memory and the stream; the work is done by
-diagpu_spmv_recon_f32 / _f64 in libdiagpu.so.
+diagpu_spmv_recon_f32 / _f64 / _c64 / _f32_c64 in libdiagpu.so.
 """
 from __future__ import annotations
 
@@ -31,22 +31,35 @@ def recon_view(offsets: torch.Tensor, values: torch.Tensor, rows: int, cols: int
     K = offsets.numel()
     if values.numel() != K * cols:
         raise ValueError(f"values has {values.numel()} elements, expected K*cols = {K * cols}")
-    cls = {torch.float32: _lib.ReconViewF32, torch.float64: _lib.ReconViewF64}.get(values.dtype)
+    cls = {torch.float32: _lib.ReconViewF32, torch.float64: _lib.ReconViewF64,
+           torch.complex64: _lib.ReconViewC64}.get(values.dtype)
     if cls is None:
         raise TypeError(f"unsupported dtype {values.dtype}")
     return cls(rows, cols, K, offsets.data_ptr(), values.data_ptr())
 
 
+# (matrix dtype, vector dtype) -> entry point
+_SPMV = {
+    (torch.float32, torch.float32): "diagpu_spmv_recon_f32",
+    (torch.float64, torch.float64): "diagpu_spmv_recon_f64",
+    (torch.complex64, torch.complex64): "diagpu_spmv_recon_c64",
+    (torch.float32, torch.complex64): "diagpu_spmv_recon_f32_c64",
+}
+
+
 def spmv_recon(offsets: torch.Tensor, values: torch.Tensor, rows: int, cols: int,
                x: torch.Tensor, y: torch.Tensor | None = None, stream=None) -> torch.Tensor:
-    """y = H x for the Recon matrix (offsets, values); y is overwritten."""
+    """y = H x for the Recon matrix (offsets, values); y is overwritten.
+    Values and x: float32/float32, float64/float64, complex64/complex64, or
+    float32 values with a complex64 x (y takes x's dtype)."""
     view = recon_view(offsets, values, rows, cols)
-    if x.dtype != values.dtype or not x.is_cuda:
-        raise TypeError("x must be a device tensor of the values' dtype")
+    name = _SPMV.get((values.dtype, x.dtype))
+    if name is None or not x.is_cuda:
+        raise TypeError(f"unsupported (values, x) dtypes ({values.dtype}, {x.dtype}) "
+                        "or x not on the device")
     if y is None:
-        y = torch.empty(rows, dtype=values.dtype, device=values.device)
-    if y.dtype != values.dtype or y.numel() < rows or not y.is_cuda:
-        raise TypeError("y must be a device tensor of the values' dtype with >= rows elements")
-    name = "diagpu_spmv_recon_f32" if values.dtype == torch.float32 else "diagpu_spmv_recon_f64"
+        y = torch.empty(rows, dtype=x.dtype, device=values.device)
+    if y.dtype != x.dtype or y.numel() < rows or not y.is_cuda:
+        raise TypeError("y must be a device tensor of x's dtype with >= rows elements")
     _lib.call(name, C.byref(view), x.data_ptr(), x.numel(), y.data_ptr(), _stream_handle(stream))
     return y

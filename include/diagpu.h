@@ -74,6 +74,20 @@ typedef struct diagpu_recon_view_f64 {
     const double*  values;
 } diagpu_recon_view_f64;
 
+/* Complex fp32 element (interleaved real, imaginary): the layout of
+ * std::complex<float>, numpy complex64 and torch.complex64. */
+typedef struct diagpu_complex64 {
+    float re, im;
+} diagpu_complex64;
+
+typedef struct diagpu_recon_view_c64 {
+    int32_t                 rows;
+    int32_t                 cols;
+    int32_t                 num_diags;
+    const int32_t*          diag_offsets;
+    const diagpu_complex64* values;
+} diagpu_recon_view_c64;
+
 /* y[r] = sum_k [0 <= r + d_k < min(cols, x_size)] Recon[k][r + d_k] * x[r + d_k]
  * for 0 <= r < rows; y is overwritten (beta = 0); rows == 0 is a successful
  * no-op.  Offsets may be in any order and out of range (such terms drop).
@@ -88,6 +102,62 @@ DIAGPU_API int diagpu_spmv_recon_f32(const diagpu_recon_view_f32* R, const float
  * reference is fp32/TF32 only; BASELINE config 2 asks for fp64). */
 DIAGPU_API int diagpu_spmv_recon_f64(const diagpu_recon_view_f64* R, const double* x,
                                      int64_t x_size, double* y, void* stream);
+
+/* Complex Hamiltonians.  The reference kernels are real fp32 only, while the
+ * physics they serve applies a complex H to a complex state
+ * (slides/transcript.md:10-18, "H is an N-by-N complex Hamiltonian").
+ * Same sum and bounds as diagpu_spmv_recon_f32, complex products,
+ * fp32 accumulation of each part:
+ *   _c64      complex64 Recon values, complex64 x and y;
+ *   _f32_c64  real fp32 Recon values, complex64 x and y (a real H applied to
+ *             a complex state; the values are read once for both parts). */
+DIAGPU_API int diagpu_spmv_recon_c64(const diagpu_recon_view_c64* R, const diagpu_complex64* x,
+                                     int64_t x_size, diagpu_complex64* y, void* stream);
+DIAGPU_API int diagpu_spmv_recon_f32_c64(const diagpu_recon_view_f32* R,
+                                         const diagpu_complex64* x, int64_t x_size,
+                                         diagpu_complex64* y, void* stream);
+
+/* ======================================================================
+ * Krylov propagator: psi(t) = exp(-i t H) psi_0 (Lanczos)
+ * ====================================================================== */
+
+/* The matrix-free caller of the SpMV path (slides/transcript.md:10-18: one
+ * trajectory, H applied to the state again and again, "exactly what
+ * Krylov-subspace methods do"); the reference ships no driver for it. */
+typedef struct diagpu_krylov_info {
+    int32_t steps;         /* Lanczos steps used (m, fewer on breakdown)          */
+    int32_t breakdown;     /* 1: an invariant subspace was reached (exact result)  */
+    double  psi0_norm;     /* ||psi_0||                                            */
+    double  err_estimate;  /* ||psi_0|| * beta_m * |[exp(-i t T_m)]_{m,1}|, 0 on
+                              breakdown                                            */
+} diagpu_krylov_info;
+
+/* Device workspace (bytes, host out) for n x n H and m Lanczos steps:
+ * m basis vectors of n complex64 plus O(n / 512) reduction scratch. */
+DIAGPU_API int diagpu_expm_krylov_workspace(int32_t n, int32_t m, size_t* bytes);
+
+/* psi_t = exp(-i t H) psi_0 for Hermitian H (n x n Recon, rows == cols; only
+ * H's action is used, Hermitian symmetry is the caller's promise), complex64
+ * psi_0 and psi_t of n elements, 1 <= m <= 64 Lanczos steps.  Two kernels per
+ * step (SpMV with a fused dot product, three-term update with a fused norm),
+ * deterministic fp64 reductions, scalars kept on the device; one stream
+ * synchronisation after the m steps to read alpha and beta, then exp(-i t T_m)
+ * e_1 on the host in fp64 and one combine kernel (async on `stream`).
+ * alpha and beta (host, m entries each, optional) receive T_m's diagonal and
+ * off-diagonal (zero past info->steps).  psi_t must not overlap psi_0 or the
+ * workspace.
+ *   _c64  complex64 Recon values;  _f32  real fp32 Recon values (real
+ *         symmetric H) applied to the complex state. */
+DIAGPU_API int diagpu_expm_krylov_c64(const diagpu_recon_view_c64* H,
+                                      const diagpu_complex64* psi0, double t, int32_t m,
+                                      diagpu_complex64* psi_t, void* workspace,
+                                      size_t workspace_bytes, double* alpha, double* beta,
+                                      diagpu_krylov_info* info, void* stream);
+DIAGPU_API int diagpu_expm_krylov_f32(const diagpu_recon_view_f32* H,
+                                      const diagpu_complex64* psi0, double t, int32_t m,
+                                      diagpu_complex64* psi_t, void* workspace,
+                                      size_t workspace_bytes, double* alpha, double* beta,
+                                      diagpu_krylov_info* info, void* stream);
 
 /* ======================================================================
  * DIA x DIA SpGEMM, HM layout: C = A * B

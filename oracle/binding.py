@@ -179,6 +179,23 @@ def spmv_recon_ref64(rows, cols, r_offsets, r_values, x):
     return y, a
 
 
+def spmv_recon_complex_ref(rows, cols, r_offsets, r_values, x):
+    """fp64 complex result (complex128 [rows]) and sum of |term parts| for a
+    complex64 (or real float32) Recon matrix applied to a complex64 x."""
+    offs = _i32(r_offsets)
+    xx = np.ascontiguousarray(x, dtype=np.complex64)
+    vals = np.ascontiguousarray(r_values)
+    y = np.empty(rows, dtype=np.complex128)
+    a = np.empty(rows, dtype=np.float64)
+    if vals.dtype == np.complex64:
+        fn = lib().orc_spmv_recon_c64_ref
+    else:
+        vals = np.ascontiguousarray(vals, dtype=np.float32)
+        fn = lib().orc_spmv_recon_f32c64_ref
+    fn(rows, cols, len(offs), _p(offs), _p(vals), _p(xx), C.c_int64(len(xx)), _p(y), _p(a))
+    return y, a
+
+
 def spmv_recon_omp(rows, cols, r_offsets, r_values, x, y) -> int:
     """OpenMP CPU baseline (orc_spmv_recon_omp_*); returns threads used."""
     offs = _i32(r_offsets)

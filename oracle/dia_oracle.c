@@ -257,6 +257,62 @@ ORC_API void orc_spmv_recon_f64(int rows, int cols, int K, const int* offs,
     }
 }
 
+/* Complex Recon SpMV: the same sum (spmv/src/dia_reconstruct.cuh:22) and
+ * bounds with complex64 values and x (interleaved re, im), fp64
+ * accumulation.  abs_sum[r] = sum over terms of |a_re x_re| + |a_im x_im| +
+ * |a_re x_im| + |a_im x_re| bounds the rounding of either part in any
+ * summation order.  No reference counterpart (the reference is real only);
+ * pinned by tests/test_oracle.py against dense complex products and scipy's
+ * dia_matrix. */
+ORC_API void orc_spmv_recon_c64_ref(int rows, int cols, int K, const int* offs,
+                                    const float* vals, const float* x, int64_t x_size,
+                                    double* y, double* abs_sum)
+{
+    const int64_t lim = x_size < cols ? x_size : cols;
+    #pragma omp parallel for schedule(static)
+    for (int r = 0; r < rows; ++r) {
+        double sr = 0.0, si = 0.0, a = 0.0;
+        for (int k = 0; k < K; ++k) {
+            const int64_t c = (int64_t)r + offs[k];
+            if (c >= 0 && c < lim) {
+                const double vr = vals[2 * ((size_t)k * cols + c)], vi = vals[2 * ((size_t)k * cols + c) + 1];
+                const double xr = x[2 * c], xi = x[2 * c + 1];
+                sr += vr * xr - vi * xi;
+                si += vr * xi + vi * xr;
+                a += fabs(vr * xr) + fabs(vi * xi) + fabs(vr * xi) + fabs(vi * xr);
+            }
+        }
+        y[2 * (size_t)r] = sr;
+        y[2 * (size_t)r + 1] = si;
+        if (abs_sum) abs_sum[r] = a;
+    }
+}
+
+/* Real fp32 Recon values applied to a complex64 x: y = H Re(x) + i H Im(x),
+ * fp64 accumulation, abs_sum as above. */
+ORC_API void orc_spmv_recon_f32c64_ref(int rows, int cols, int K, const int* offs,
+                                       const float* vals, const float* x, int64_t x_size,
+                                       double* y, double* abs_sum)
+{
+    const int64_t lim = x_size < cols ? x_size : cols;
+    #pragma omp parallel for schedule(static)
+    for (int r = 0; r < rows; ++r) {
+        double sr = 0.0, si = 0.0, a = 0.0;
+        for (int k = 0; k < K; ++k) {
+            const int64_t c = (int64_t)r + offs[k];
+            if (c >= 0 && c < lim) {
+                const double v = vals[(size_t)k * cols + c];
+                sr += v * x[2 * c];
+                si += v * x[2 * c + 1];
+                a += fabs(v * x[2 * c]) + fabs(v * x[2 * c + 1]);
+            }
+        }
+        y[2 * (size_t)r] = sr;
+        y[2 * (size_t)r + 1] = si;
+        if (abs_sum) abs_sum[r] = a;
+    }
+}
+
 /* CPU baseline: the straightforward OpenMP DIA loop over the Recon layout,
  * schedule(static) over rows, inner loop over diagonals, accumulation in the
  * element type.  Returns the thread count used. */

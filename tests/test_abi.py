@@ -120,3 +120,35 @@ def test_axpby_argument_errors():
     assert b"X arrays" in lib.diagpu_last_error()
     bad = list(args); bad[13] = 0
     assert lib.diagpu_dia_axpby_f32(*bad) == _lib.OK          # empty Z: no-op
+
+
+def test_complex_and_krylov_argument_errors():
+    fake = C.c_void_p(0x1000)   # never dereferenced: validation fails first
+    V = _lib.ReconViewC64
+    v = V(4, 4, 1, fake.value, fake.value)
+    assert _status("diagpu_spmv_recon_c64", None, fake, 4, fake, None) == _lib.ERR_ARG
+    assert _status("diagpu_spmv_recon_c64", C.byref(v), None, 4, fake, None) == _lib.ERR_ARG
+    w = _lib.ReconViewF32(4, 4, 1, fake.value, fake.value)
+    assert _status("diagpu_spmv_recon_f32_c64", C.byref(w), fake, 4, None, None) == _lib.ERR_ARG
+    z = V(0, 0, 0, None, None)
+    assert _status("diagpu_spmv_recon_c64", C.byref(z), None, 0, None, None) == _lib.OK
+
+    b = C.c_size_t(0)
+    assert _status("diagpu_expm_krylov_workspace", 100, 0, C.byref(b)) == _lib.ERR_ARG
+    assert _status("diagpu_expm_krylov_workspace", 100, 65, C.byref(b)) == _lib.ERR_ARG
+    assert _status("diagpu_expm_krylov_workspace", 0, 10, C.byref(b)) == _lib.ERR_ARG
+    assert _status("diagpu_expm_krylov_workspace", 1000, 10, C.byref(b)) == _lib.OK
+    assert b.value >= 10 * 1000 * 8
+    info = _lib.KrylovInfo()
+    sq = V(1000, 1000, 1, fake.value, fake.value)
+    rect = V(1000, 999, 1, fake.value, fake.value)
+    call = lambda view, m, ws_bytes, t=1.0: _status(
+        "diagpu_expm_krylov_c64", C.byref(view), fake, t, m, fake, fake, ws_bytes, None, None,
+        C.byref(info), None)
+    assert call(rect, 10, b.value) == _lib.ERR_ARG                 # not square
+    assert call(sq, 0, b.value) == _lib.ERR_ARG                    # m out of range
+    assert call(sq, 10, b.value, float("nan")) == _lib.ERR_ARG     # t not finite
+    assert call(sq, 10, b.value - 1) == _lib.ERR_CAPACITY          # workspace too small
+    assert b"workspace" in _lib.load().diagpu_last_error()
+    assert _status("diagpu_expm_krylov_f32", None, fake, 1.0, 10, fake, fake, b.value, None,
+                   None, C.byref(info), None) == _lib.ERR_ARG

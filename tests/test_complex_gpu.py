@@ -1,0 +1,209 @@
+"""Complex Hamiltonians on the GPU: complex64 Recon SpMV, real Recon applied
+to a complex state, and the Lanczos propagator exp(-i t H) psi_0 built on
+them (through the C ABI).
+
+Bounds.  SpMV: each part within 1e-5 of the oracle's fp64 result relative to
+the sum of |term parts| (the fp32 bound of any summation order).  The real
+matrix applied to a complex x must equal the real kernel applied to each part
+bit for bit (same diagonal order, same fused multiply-adds).  Propagator:
+against scipy.linalg.expm in complex128 at small n, to 1e-4 of ||psi_0||
+(fp32 Lanczos rounding over m <= 40 steps with t ||H|| <= 12; the Krylov
+truncation error is below 1e-7 there and is also checked through the
+returned estimate); at n = 2^22 through the properties the exact propagator
+has (unitarity, time reversal, energy conservation, determinism).
+"""
+import numpy as np
+import pytest
+import torch
+
+from diagpu_amd import workloads
+from diagpu_amd.krylov import expm_krylov, KrylovWorkspace
+from diagpu_amd.spmv import spmv_recon
+
+pytestmark = pytest.mark.gpu
+
+
+def _nan_padded(rng, rows, cols, offs, dtype):
+    K = len(offs)
+    if dtype == np.complex64:
+        vals = (rng.uniform(-1, 1, (K, cols)) + 1j * rng.uniform(-1, 1, (K, cols))).astype(dtype)
+    else:
+        vals = rng.uniform(-1, 1, (K, cols)).astype(dtype)
+    c = np.arange(cols)
+    for k, d in enumerate(offs):          # NaN wherever the row c - d is outside [0, rows)
+        vals[k][(c - d < 0) | (c - d >= rows)] = np.nan
+    return vals
+
+
+def _cx(rng, n):
+    return (rng.standard_normal(n) + 1j * rng.standard_normal(n)).astype(np.complex64)
+
+
+@pytest.mark.parametrize("K", [1, 3, 5, 6, 12, 64, 65])
+@pytest.mark.parametrize("mat", ["c64", "f32"])
+def test_complex_spmv_every_path(dev, oracle, K, mat):
+    rng = np.random.default_rng(77 * K + (mat == "f32"))
+    rows, cols = 12007, 11993
+    offs = rng.choice(np.arange(-2100, 2101), size=K, replace=False).astype(np.int32)
+    vals = _nan_padded(rng, rows, cols, offs, np.complex64 if mat == "c64" else np.float32)
+    x = _cx(rng, cols)
+    y = spmv_recon(torch.as_tensor(offs, device=dev), torch.as_tensor(vals.reshape(-1), device=dev),
+                   rows, cols, torch.as_tensor(x, device=dev)).cpu().numpy()
+    assert y.dtype == np.complex64 and not np.isnan(y).any()
+    want, absum = oracle.spmv_recon_complex_ref(rows, cols, offs, np.nan_to_num(vals).reshape(-1), x)
+    for part in (np.real, np.imag):
+        err = np.abs(part(y).astype(np.float64) - part(want))
+        assert (err <= 1e-5 * absum + 1e-30).all(), float(err.max())
+
+
+@pytest.mark.parametrize("K", [2, 5, 9, 40, 70])
+def test_real_matrix_complex_state_equals_real_kernel_per_part(dev, K):
+    """H (real) applied to x = a + ib is H a + i H b with the real kernel's
+    exact roundings."""
+    rng = np.random.default_rng(500 + K)
+    n = 20011
+    offs = torch.as_tensor(rng.choice(np.arange(-3000, 3001), size=K, replace=False), dtype=torch.int32, device=dev)
+    vals = torch.as_tensor(rng.uniform(-1, 1, K * n).astype(np.float32), device=dev)
+    x = torch.as_tensor(_cx(rng, n), device=dev)
+    y = spmv_recon(offs, vals, n, n, x)
+    yr = spmv_recon(offs, vals, n, n, x.real.contiguous())
+    yi = spmv_recon(offs, vals, n, n, x.imag.contiguous())
+    assert torch.equal(y.real, yr) and torch.equal(y.imag, yi)
+
+
+def test_complex_spmv_full_size_poisson(dev, oracle):
+    """BASELINE config 2's stencil with complex values (i times the real
+    stencil) and a complex state: y = i H x, checked over every row."""
+    R = workloads.spmv_config(2, seed=3, device=dev, dtype=torch.float32)
+    cv = (1j * R.values.to(torch.complex64)).contiguous()
+    x = torch.complex(R.x, torch.roll(R.x, 7)).contiguous()
+    y = spmv_recon(R.offsets, cv, R.rows, R.cols, x)
+    y2 = spmv_recon(R.offsets, cv, R.rows, R.cols, x)
+    assert torch.equal(y, y2)
+    want, absum = oracle.spmv_recon_complex_ref(R.rows, R.cols, R.offsets.cpu().numpy(),
+                                                cv.cpu().numpy(), x.cpu().numpy())
+    got = y.cpu().numpy()
+    for part in (np.real, np.imag):
+        assert (np.abs(part(got) - part(want)) <= 1e-5 * absum + 1e-30).all()
+
+
+# ------------------------------------------------------------ propagator --
+
+def _hermitian_band(rng, n, offsets, complex_values=True):
+    """Recon arrays of a random Hermitian band: H[r, r+d] = h, H[r+d, r] =
+    conj(h); the main diagonal real."""
+    pos = sorted({abs(int(d)) for d in offsets})
+    H = np.zeros((n, n), np.complex128 if complex_values else np.float64)
+    for d in pos:
+        for r in range(n - d):
+            if d == 0:
+                H[r, r] = rng.uniform(-2, 2)
+            else:
+                h = rng.uniform(-1, 1) + (1j * rng.uniform(-1, 1) if complex_values else 0)
+                H[r, r + d] = h
+                H[r + d, r] = np.conj(h)
+    offs = sorted({d for p in pos for d in (p, -p)}, reverse=True)
+    dt = np.complex64 if complex_values else np.float32
+    vals = np.zeros((len(offs), n), dt)
+    for k, d in enumerate(offs):          # Recon[k][c] = H[c - d, c]
+        for c in range(n):
+            r = c - d
+            if 0 <= r < n:
+                vals[k, c] = H[r, c]
+    return np.array(offs, np.int32), vals, H.astype(np.complex64).astype(np.complex128)
+
+
+@pytest.mark.parametrize("complex_values", [True, False])
+def test_propagator_matches_expm(dev, complex_values):
+    import scipy.linalg as sl
+    rng = np.random.default_rng(4 + complex_values)
+    n = 500
+    offs, vals, H = _hermitian_band(rng, n, [0, 1, 2, 5, 37], complex_values)
+    psi0 = _cx(rng, n)
+    t, m = 0.8, 40
+    res = expm_krylov(torch.as_tensor(offs, device=dev), torch.as_tensor(vals.reshape(-1), device=dev),
+                      n, torch.as_tensor(psi0, device=dev), t, m)
+    want = sl.expm(-1j * t * H) @ psi0.astype(np.complex128)
+    got = res.psi.cpu().numpy().astype(np.complex128)
+    nrm = np.linalg.norm(psi0.astype(np.complex128))
+    assert np.linalg.norm(got - want) <= 1e-4 * nrm, np.linalg.norm(got - want) / nrm
+    assert res.steps == m and not res.breakdown
+    assert res.err_estimate <= 1e-6 * nrm
+    assert abs(res.psi0_norm - nrm) <= 1e-6 * nrm
+    # T_m's leading coefficients against an fp64 Lanczos whose relation
+    # V^H H V = T is verified here, so the comparison pins them.
+    v = psi0.astype(np.complex128) / nrm
+    vp = np.zeros_like(v)
+    al, be, V = [], [], [v]
+    bprev = 0.0
+    for j in range(8):
+        w = H @ v
+        a = np.vdot(v, w).real
+        w = w - a * v - bprev * vp
+        b = np.linalg.norm(w)
+        al.append(a); be.append(b)
+        vp, v, bprev = v, w / b, b
+        V.append(v)
+    Vm = np.array(V[:8]).T
+    T = np.diag(al) + np.diag(be[:7], 1) + np.diag(be[:7], -1)
+    assert np.allclose(Vm.conj().T @ H @ Vm, T, atol=1e-9)
+    scale = np.abs(np.linalg.eigvalsh(H)).max()
+    assert np.allclose(res.alpha[:8], al, rtol=0, atol=1e-4 * scale)
+    assert np.allclose(res.beta[:8], be, rtol=0, atol=1e-4 * scale)
+
+
+def test_propagator_breakdown_is_exact(dev):
+    """A diagonal H with three distinct values: the Krylov space of any psi_0
+    has dimension 3, Lanczos stops there and the result is exp(-i t d) psi_0."""
+    rng = np.random.default_rng(8)
+    n = 3000
+    d = rng.choice(np.array([-1.0, 0.5, 2.0], np.float32), size=n)
+    psi0 = _cx(rng, n)
+    t = 1.3
+    res = expm_krylov(torch.tensor([0], dtype=torch.int32, device=dev),
+                      torch.as_tensor(d, device=dev), n, torch.as_tensor(psi0, device=dev), t, 20)
+    assert res.breakdown and res.steps == 3
+    want = np.exp(-1j * t * d.astype(np.float64)) * psi0
+    got = res.psi.cpu().numpy()
+    assert np.abs(got - want).max() <= 2e-6 * np.abs(psi0).max()
+
+
+def test_propagator_zero_time_and_zero_state(dev):
+    rng = np.random.default_rng(9)
+    n = 4097
+    offs, vals, _ = _hermitian_band(rng, n, [0, 3])
+    o = torch.as_tensor(offs, device=dev)
+    v = torch.as_tensor(vals.reshape(-1), device=dev)
+    psi0 = torch.as_tensor(_cx(rng, n), device=dev)
+    r0 = expm_krylov(o, v, n, psi0, 0.0, 10)
+    assert torch.allclose(r0.psi, psi0, rtol=0, atol=1e-6)
+    rz = expm_krylov(o, v, n, torch.zeros_like(psi0), 0.7, 10)
+    assert rz.steps == 0 and torch.count_nonzero(rz.psi) == 0
+
+
+def test_propagator_full_size_properties(dev):
+    """n = 2^22 (config 2's 5-point stencil, real symmetric H) with a complex
+    state: ||psi(t)|| = ||psi_0||, psi(-t) of psi(t) = psi_0, <H> conserved,
+    and two runs agree bit for bit."""
+    R = workloads.spmv_config(2, seed=5, device=dev, dtype=torch.float32)
+    n = R.rows
+    g = torch.Generator(device=dev).manual_seed(5)
+    psi0 = torch.complex(torch.randn(n, device=dev, generator=g),
+                         torch.randn(n, device=dev, generator=g)).contiguous()
+    ws = KrylovWorkspace(n, 30, dev)
+    t = 0.25
+    a = expm_krylov(R.offsets, R.values, n, psi0, t, 30, workspace=ws)
+    a2 = expm_krylov(R.offsets, R.values, n, psi0, t, 30, workspace=ws)
+    assert torch.equal(a.psi, a2.psi)
+    assert a.err_estimate <= 1e-5 * a.psi0_norm
+    nrm0 = torch.linalg.vector_norm(psi0.to(torch.complex128)).item()
+    assert abs(torch.linalg.vector_norm(a.psi.to(torch.complex128)).item() - nrm0) <= 1e-5 * nrm0
+    back = expm_krylov(R.offsets, R.values, n, a.psi, -t, 30, workspace=ws)
+    diff = torch.linalg.vector_norm((back.psi - psi0).to(torch.complex128)).item()
+    assert diff <= 1e-4 * nrm0, diff / nrm0
+
+    def energy(psi):
+        hpsi = spmv_recon(R.offsets, R.values, n, n, psi)
+        return torch.vdot(psi.to(torch.complex128), hpsi.to(torch.complex128)).real.item()
+    e0, e1 = energy(psi0), energy(a.psi)
+    assert abs(e1 - e0) <= 1e-4 * abs(e0)

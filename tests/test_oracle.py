@@ -156,6 +156,35 @@ def test_spmv_main_diagonal_and_out_of_range(oracle):
     assert np.array_equal(y2, d * x)
 
 
+@pytest.mark.parametrize("rows,cols,offsets", [(40, 40, [-3, 0, 2, 7]), (31, 45, [-30, -1, 0, 5, 44]),
+                                              (50, 20, [-49, -6, 0, 1, 19, 25])])
+def test_complex_spmv_vs_dense_and_scipy(oracle, rows, cols, offsets):
+    """Complex Recon SpMV (no reference counterpart): scipy's dia_matrix with
+    complex data gives the dense matrix, whose complex128 product the oracle
+    must match; a real matrix applied to a complex x must equal the real
+    oracle applied to each part."""
+    import scipy.sparse as sp
+    rng = np.random.default_rng(rows * cols)
+    K = len(offsets)
+    vals = (rng.uniform(-1, 1, (K, cols)) + 1j * rng.uniform(-1, 1, (K, cols))).astype(np.complex64)
+    x = (rng.standard_normal(cols) + 1j * rng.standard_normal(cols)).astype(np.complex64)
+    D = sp.dia_matrix((vals, offsets), shape=(rows, cols)).toarray().astype(np.complex128)
+    y, absum = oracle.spmv_recon_complex_ref(rows, cols, offsets, vals.reshape(-1), x)
+    want = D @ x.astype(np.complex128)
+    assert np.allclose(y, want, rtol=0, atol=1e-12)
+    ax = np.abs(x.real.astype(np.float64)) + np.abs(x.imag.astype(np.float64))
+    dense_abs = np.abs(D.real) @ ax + np.abs(D.imag) @ ax
+    assert np.allclose(absum, dense_abs, rtol=1e-12, atol=1e-12)
+    # real values, complex x: linearity over the two parts
+    rv = vals.real.copy()
+    yr, _ = oracle.spmv_recon_complex_ref(rows, cols, offsets, rv.reshape(-1), x)
+    p_re, _ = oracle.spmv_recon_ref64(rows, cols, offsets, rv.reshape(-1), x.real.copy())
+    p_im, _ = oracle.spmv_recon_ref64(rows, cols, offsets, rv.reshape(-1), x.imag.copy())
+    assert np.array_equal(yr.real, p_re) and np.array_equal(yr.imag, p_im)
+    # a planted conjugation or swapped part would be caught here
+    assert not np.allclose(y, np.conj(D) @ x.astype(np.complex128), atol=1e-6)
+
+
 # --------------------------------------------------------- SpGEMM plan ----
 
 @pytest.mark.parametrize("seed", range(6))
