@@ -5,4 +5,5 @@
 #include "common.hpp"
 #include "dia_reconstruct.hpp"
 #include "gemm_diag.hpp"
+#include "krylov.hpp"
 #include "spgemm.hpp"

@@ -13,7 +13,7 @@ pytestmark = pytest.mark.gpu
 BIN = Path(__file__).resolve().parent / "cpp" / "bin"
 
 
-@pytest.mark.parametrize("program", ["test_dia_api", "test_chain"])
+@pytest.mark.parametrize("program", ["test_dia_api", "test_chain", "test_krylov"])
 def test_cpp_program(dev, program):
     exe = BIN / program
     assert exe.exists(), f"{exe} missing: run __graft_entry__.build() first"
