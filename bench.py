@@ -46,7 +46,8 @@ def parse_args(argv=None):
     ap.add_argument("--no-extras", dest="extras", action="store_false")
     ap.add_argument("--only", default="",
                     help="profiling aid: run just one workload (spmv2, spmv2d, spmv2c, "
-                         "spmv2rc, spmv1, spmv3, spgemm4, spgemm5, taylor, krylov, copy) "
+                         "spmv2rc, spmv1, spmv3, spgemm4, spgemm5, spgemm4c, spgemm5c, taylor, krylov, "
+                         "copy) "
                          "and print its line")
     return ap.parse_args(argv)
 
@@ -211,11 +212,17 @@ def time_krylov(m: int = 30, t: float = 1.0, reps: int = 5):
 # SpGEMM (configs 4 and 5)
 # --------------------------------------------------------------------------
 
-def time_spgemm(cfg: int, seed: int, reps: int):
+def time_spgemm(cfg: int, seed: int, reps: int, complex_values: bool = False):
     import torch
     from diagpu_amd import workloads
     from diagpu_amd.spgemm import SpgemmPlan
     A, B = workloads.spgemm_config(cfg, seed=seed, device="cuda")
+    if complex_values:   # same structure, values v + i * roll(v)
+        A = workloads.HM(A.n, A.offsets, A.lengths, A.starts,
+                         torch.complex(A.values, torch.roll(A.values, 1)).contiguous())
+        B = workloads.HM(B.n, B.offsets, B.lengths, B.starts,
+                         torch.complex(B.values, torch.roll(B.values, 1)).contiguous())
+    esz = A.values.element_size()
     stream = torch.cuda.current_stream()
     t0 = time.perf_counter()
     plan = SpgemmPlan(A, B)
@@ -230,10 +237,10 @@ def time_spgemm(cfg: int, seed: int, reps: int):
     torch.cuda.synchronize()
     sym_ms = e0.elapsed_time(e1) / 3
     # operand/result sets rotated so that together they exceed twice the MALL
-    set_bytes = 4 * (A.nnz + B.nnz + plan.info.c_nnz)
+    set_bytes = esz * (A.nnz + B.nnz + plan.info.c_nnz)
     nsets = 1 if set_bytes >= 2 * MALL_BYTES else max(3, -(-2 * MALL_BYTES // set_bytes))
     sets = [(A.values.clone(), B.values.clone(),
-             torch.empty(plan.info.c_nnz, dtype=torch.float32, device="cuda"))
+             torch.empty(plan.info.c_nnz, dtype=A.values.dtype, device="cuda"))
             for _ in range(nsets)]
     for i in range(2):
         plan.numeric(*sets[i % nsets])
@@ -244,10 +251,10 @@ def time_spgemm(cfg: int, seed: int, reps: int):
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / reps
-    alg = 4 * (A.nnz + B.nnz + plan.info.c_nnz)
-    flops = plan.info.useful_flops
+    alg = esz * (A.nnz + B.nnz + plan.info.c_nnz)
+    flops = plan.info.useful_flops * (4 if complex_values else 1)   # complex MAC = 4 real
     return {
-        "workload": f"spgemm_cfg{cfg}", "dtype": "f32", "n": A.n,
+        "workload": f"spgemm_cfg{cfg}", "dtype": "c64" if complex_values else "f32", "n": A.n,
         "A_diags": A.ndiag, "B_diags": B.ndiag, "C_diags": plan.info.c_ndiag,
         "pairs": plan.info.n_pairs, "max_pairs_per_C": plan.info.max_pairs,
         "C_nnz": plan.info.c_nnz, "numeric_ms": round(ms, 5),
@@ -337,7 +344,8 @@ def main(argv=None) -> int:
         elif w == "krylov":
             print(json.dumps(time_krylov()), flush=True)
         elif w.startswith("spgemm"):
-            print(json.dumps(time_spgemm(int(w[6]), args.seed, args.steps)), flush=True)
+            print(json.dumps(time_spgemm(int(w[6]), args.seed, args.steps, w.endswith("c"))),
+                  flush=True)
         elif w == "taylor":
             print(json.dumps(time_taylor()), flush=True)
         else:

@@ -89,6 +89,11 @@ PROTOTYPES: dict[str, tuple] = {
         _vp, _vp, _vp, _i64,
         _vp, _vp, _i64,
         _vp, _vp]),
+    "diagpu_spgemm_numeric_c64": (C.c_int, [
+        _i32, _vp, _vp,
+        _vp, _vp, _vp, _i64,
+        _vp, _vp, _i64,
+        _vp, _vp]),
     "diagpu_rowpacked_as_hm": (C.c_int, [_i32, _vp, _i32, _vp, _vp, _vp]),
     "diagpu_dia_axpby_f32": (C.c_int, [
         _i32, _vp, _vp, _i32, _vp, C.c_float,

@@ -1,4 +1,4 @@
-// DIA x DIA SpGEMM, numeric phase on the GPU (HM layout, fp32).
+// DIA x DIA SpGEMM, numeric phase on the GPU (HM layout, fp32 or complex64).
 //
 //   C[k][p] = sum over the plan entries g of C diagonal k of
 //             Av[g.ab + p + g.ash] * Bv[g.bb + p + g.bsh]
@@ -7,13 +7,17 @@
 //   hm_structured_sparse_matmul_kernel (spmspm/paper_hm_kernel.cu:31-93) and
 //   of gather_flat_kernel (spmspm/gather_flat.cuh:47-62), evaluated in plan
 //   order with fp32 accumulation.  Every C value is written exactly once: no
-//   atomics, no pre-zeroing, deterministic.
+//   atomics, no pre-zeroing, deterministic.  The complex64 variant (complex
+//   Hamiltonians; the reference is real only) runs the same plan with
+//   complex products; a lane then owns 2 positions instead of 4, so its loads
+//   and stores stay 16 bytes.
 //
-// Work decomposition.  An item is (row block rb, C diagonal k): the 1024
-// positions of diagonal k whose matrix rows fall in block rb (shifted by at
-// most 3 so the item's first C element is 16-byte aligned).  Each lane owns 4
-// consecutive positions: one aligned 128-bit streaming store of C and, per
-// plan entry, one 128-bit load each of A and B (dword aligned).  A workgroup
+// Work decomposition.  An item is (row block rb, C diagonal k): the 256 x E
+// positions of diagonal k whose matrix rows fall in block rb (E = 4 for fp32,
+// 2 for complex64; shifted by at most E - 1 so the item's first C element is
+// 16-byte aligned).  Each lane owns E consecutive positions: one aligned
+// 128-bit streaming store of C and, per plan entry, one 128-bit load each of A
+// and B (dword aligned).  A workgroup
 // takes a batch of 16 consecutive C diagonals of one row block: their
 // metadata and plan entries (1.7 per diagonal on average) are resolved once
 // into LDS, then the flattened entry list is walked in chunks whose loads are
@@ -31,18 +35,21 @@
 // through that range's items in order, so each XCD's L2 streams one
 // contiguous band of rows.  Each workgroup's item loop ends at a fixed count.
 #include "common.hpp"
+#include "elem.hpp"
 
 namespace diagpu {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kTB = kBlock * 4;   // positions per item
 constexpr int kBatch = 16;        // consecutive C diagonals per batch
 
-typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
-typedef float f4a __attribute__((ext_vector_type(4), aligned(16)));
+// Positions per lane (16 bytes of T) and per item.
+template <typename T> constexpr int epl() { return (int)(16 / sizeof(T)); }
+template <typename T> constexpr int item_positions() { return kBlock * epl<T>(); }
 
-__device__ __forceinline__ f4u ld4(const float* p) { return *reinterpret_cast<const f4u*>(p); }
+// acc + a * b over a lane's positions
+__device__ __forceinline__ float mac(float acc, float a, float b) { return __builtin_fmaf(a, b, acc); }
+__device__ __forceinline__ cf32 mac(cf32 acc, cf32 a, cf32 b) { return mad(acc, a, b); }
 
 // One C diagonal of the current batch, for the current row block.
 struct DiagRec {
@@ -62,14 +69,17 @@ struct PairRec {
     int32_t cover;    // 1: covers the whole item, 0: part of it, -1: none of it
 };
 
-template <int PC>
+template <typename T, int PC>
 __global__ __launch_bounds__(kBlock) void k_gather(
-    const float* __restrict__ Av, const float* __restrict__ Bv,
+    const T* __restrict__ Av, const T* __restrict__ Bv,
     const int32_t* __restrict__ C_off, const int32_t* __restrict__ C_len,
     const int64_t* __restrict__ C_starts, int32_t nC, const int64_t* __restrict__ pair_ptr,
-    const diagpu_gpair* __restrict__ pairs, float* __restrict__ Cv, int32_t NB,
+    const diagpu_gpair* __restrict__ pairs, T* __restrict__ Cv, int32_t NB,
     int32_t nb_per_xcd, int32_t wg_per_xcd)
 {
+    constexpr int E = epl<T>();
+    constexpr int TB = item_positions<T>();
+    typedef Run<T, E> V;
     __shared__ DiagRec drec[kBatch];
     __shared__ int64_t ptr_s[kBatch + 1];
     __shared__ PairRec prec[kBlock];
@@ -81,7 +91,7 @@ __global__ __launch_bounds__(kBlock) void k_gather(
     if (rb0 >= rb_end || nC <= 0) return;
     const int nbat = (nC + kBatch - 1) / kBatch;
     const int t = (int)threadIdx.x;
-    const int64_t p_lane = (int64_t)t * 4;
+    const int64_t p_lane = (int64_t)t * E;
     const int64_t nwork = (int64_t)(rb_end - rb0) * nbat;
 
     for (int64_t j = l; j < nwork; j += wg_per_xcd) {
@@ -96,7 +106,7 @@ __global__ __launch_bounds__(kBlock) void k_gather(
             const int64_t cst = C_starts[kb + t];
             const int mc = dc < 0 ? dc : 0;
             DiagRec d;
-            d.P0 = (int64_t)rb * kTB + mc - (int)((cst + mc) & 3);
+            d.P0 = (int64_t)rb * TB + mc - (int)((cst + mc) & (E - 1));
             d.cst = cst;
             d.len = C_len[kb + t];
             d.pad0 = 0;
@@ -106,19 +116,20 @@ __global__ __launch_bounds__(kBlock) void k_gather(
         __syncthreads();
 
         const int64_t gb = ptr_s[0], ge = ptr_s[gv];
-        float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+        V acc;
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc.v[e] = zero_of<T>();
         int cur = -1;
         auto flush = [&](int ci) {
             const DiagRec d = drec[ci];
             const int64_t p = d.P0 + p_lane;
-            float* __restrict__ cp = Cv + d.cst;
-            if (d.P0 >= 0 && d.P0 + kTB <= d.len) {
-                __builtin_nontemporal_store(f4a{acc0, acc1, acc2, acc3}, reinterpret_cast<f4a*>(cp + p));
-            } else if (d.P0 < d.len && d.P0 + kTB > 0) {
-                const float r[4] = {acc0, acc1, acc2, acc3};
+            T* __restrict__ cp = Cv + d.cst;
+            if (d.P0 >= 0 && d.P0 + TB <= d.len) {
+                store_run_nt<T, E>(cp + p, acc);   // cst + P0 is a multiple of E: 16-byte aligned
+            } else if (d.P0 < d.len && d.P0 + TB > 0) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (p + e >= 0 && p + e < d.len) cp[p + e] = r[e];
+                for (int e = 0; e < E; ++e)
+                    if (p + e >= 0 && p + e < d.len) cp[p + e] = acc.v[e];
             }
         };
 
@@ -141,30 +152,31 @@ __global__ __launch_bounds__(kBlock) void k_gather(
                 r.plo = lo;
                 r.phi = hi;
                 r.ci = ci;
-                r.cover = (d.P0 >= lo && d.P0 + kTB <= hi) ? 1
-                          : ((d.P0 + kTB > lo && d.P0 < hi) ? 0 : -1);
+                r.cover = (d.P0 >= lo && d.P0 + TB <= hi) ? 1
+                          : ((d.P0 + TB > lo && d.P0 < hi) ? 0 : -1);
                 prec[t] = r;
             }
             __syncthreads();
 
             for (int s0 = 0; s0 < cnt; s0 += PC) {
                 // A chunk in which no entry covers only part of the item takes
-                // the straight-line path: all 2*PC quad loads are issued before
-                // the first FMA (a masked element path in the same block would
-                // make the compiler drain the loads at its merge point).
+                // the straight-line path: all 2*PC vector loads are issued
+                // before the first multiply-add (a masked element path in the
+                // same block would make the compiler drain the loads at its
+                // merge point).
                 bool fast = true;
 #pragma unroll
                 for (int c = 0; c < PC; ++c)
                     if (s0 + c < cnt && prec[s0 + c].cover == 0) fast = false;
                 if (fast) {
-                    f4u a[PC], b[PC];
+                    V a[PC], b[PC];
 #pragma unroll
                     for (int c = 0; c < PC; ++c) {
                         if (s0 + c < cnt && prec[s0 + c].cover > 0) {
                             const PairRec r = prec[s0 + c];
                             const int64_t p = drec[r.ci].P0 + p_lane;
-                            a[c] = ld4(Av + r.a_base + p);
-                            b[c] = ld4(Bv + r.b_base + p);
+                            a[c] = load_run<T, E, false>(Av + r.a_base + p);
+                            b[c] = load_run<T, E, false>(Bv + r.b_base + p);
                         }
                     }
 #pragma unroll
@@ -173,14 +185,13 @@ __global__ __launch_bounds__(kBlock) void k_gather(
                         const PairRec r = prec[s0 + c];
                         if (r.ci != cur) {
                             if (cur >= 0) flush(cur);
-                            acc0 = acc1 = acc2 = acc3 = 0.f;
+#pragma unroll
+                            for (int e = 0; e < E; ++e) acc.v[e] = zero_of<T>();
                             cur = r.ci;
                         }
                         if (r.cover > 0) {
-                            acc0 = __builtin_fmaf(a[c].x, b[c].x, acc0);
-                            acc1 = __builtin_fmaf(a[c].y, b[c].y, acc1);
-                            acc2 = __builtin_fmaf(a[c].z, b[c].z, acc2);
-                            acc3 = __builtin_fmaf(a[c].w, b[c].w, acc3);
+#pragma unroll
+                            for (int e = 0; e < E; ++e) acc.v[e] = mac(acc.v[e], a[c].v[e], b[c].v[e]);
                         }
                     }
                 } else {
@@ -188,30 +199,67 @@ __global__ __launch_bounds__(kBlock) void k_gather(
                         const PairRec r = prec[s0 + c];
                         if (r.ci != cur) {
                             if (cur >= 0) flush(cur);
-                            acc0 = acc1 = acc2 = acc3 = 0.f;
+#pragma unroll
+                            for (int e = 0; e < E; ++e) acc.v[e] = zero_of<T>();
                             cur = r.ci;
                         }
                         if (r.cover < 0) continue;
                         const int64_t p = drec[r.ci].P0 + p_lane;
-                        float av[4], bv[4];
-                        bool ok[4];
+                        T av[E], bv[E];
+                        bool ok[E];
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
+                        for (int e = 0; e < E; ++e) {
                             const int64_t x = p + e;
                             ok[e] = x >= r.plo && x < r.phi;
-                            av[e] = ok[e] ? Av[r.a_base + x] : 0.f;
-                            bv[e] = ok[e] ? Bv[r.b_base + x] : 0.f;
+                            av[e] = ok[e] ? Av[r.a_base + x] : zero_of<T>();
+                            bv[e] = ok[e] ? Bv[r.b_base + x] : zero_of<T>();
                         }
-                        acc0 = ok[0] ? __builtin_fmaf(av[0], bv[0], acc0) : acc0;
-                        acc1 = ok[1] ? __builtin_fmaf(av[1], bv[1], acc1) : acc1;
-                        acc2 = ok[2] ? __builtin_fmaf(av[2], bv[2], acc2) : acc2;
-                        acc3 = ok[3] ? __builtin_fmaf(av[3], bv[3], acc3) : acc3;
+#pragma unroll
+                        for (int e = 0; e < E; ++e)
+                            acc.v[e] = ok[e] ? mac(acc.v[e], av[e], bv[e]) : acc.v[e];
                     }
                 }
             }
         }
         if (cur >= 0) flush(cur);
     }
+}
+
+template <typename T>
+int numeric_launch(int32_t n, const T* A_vals, const T* B_vals, const int32_t* C_off,
+                   const int32_t* C_len, const int64_t* C_starts, int64_t c_ndiag,
+                   const int64_t* pair_ptr, const diagpu_gpair* pairs, int64_t max_pairs,
+                   T* C_vals, void* stream, const char* fn)
+{
+    if (n < 1 || n > (1 << 30)) return fail(DIAGPU_ERR_ARG, "%s: n=%d outside [1, 2^30]", fn, n);
+    if (c_ndiag < 0 || c_ndiag > 2 * (int64_t)n - 1)
+        return fail(DIAGPU_ERR_ARG, "%s: c_ndiag=%lld outside [0, 2n-1]", fn, (long long)c_ndiag);
+    if (max_pairs < 0) return fail(DIAGPU_ERR_ARG, "%s: negative max_pairs", fn);
+    if (c_ndiag == 0) return DIAGPU_OK;
+    if (!C_off || !C_len || !C_starts || !pair_ptr || !C_vals)
+        return fail(DIAGPU_ERR_ARG, "%s: C structure, pair_ptr or C_vals is NULL", fn);
+    if (max_pairs > 0 && (!pairs || !A_vals || !B_vals))
+        return fail(DIAGPU_ERR_ARG, "%s: pairs or operand values are NULL", fn);
+
+    constexpr int TB = item_positions<T>();
+    const int32_t NB = (int32_t)ceil_div<int64_t>((int64_t)n + epl<T>() - 1, TB);
+    const int32_t nb_per_xcd = ceil_div<int32_t>(NB, kNumXcd);
+    // Many C diagonals (wide operands): 4-entry chunks, 4 workgroups per CU;
+    // few: 8-entry chunks and 8 workgroups per CU for more loads in flight.
+    const bool wide = c_ndiag >= 1024;
+    const int64_t batches_per_xcd = (int64_t)nb_per_xcd * ceil_div<int64_t>(c_ndiag, kBatch);
+    int64_t wg = (int64_t)(cu_count() / kNumXcd) * (wide ? 4 : 8);
+    if (wg > batches_per_xcd) wg = batches_per_xcd;
+    if (wg < 1) wg = 1;
+    if (wide)
+        hipLaunchKernelGGL((k_gather<T, 4>), dim3((unsigned)(wg * kNumXcd)), dim3(kBlock), 0,
+                           as_stream(stream), A_vals, B_vals, C_off, C_len, C_starts,
+                           (int32_t)c_ndiag, pair_ptr, pairs, C_vals, NB, nb_per_xcd, (int32_t)wg);
+    else
+        hipLaunchKernelGGL((k_gather<T, 8>), dim3((unsigned)(wg * kNumXcd)), dim3(kBlock), 0,
+                           as_stream(stream), A_vals, B_vals, C_off, C_len, C_starts,
+                           (int32_t)c_ndiag, pair_ptr, pairs, C_vals, NB, nb_per_xcd, (int32_t)wg);
+    return check_launch(fn);
 }
 
 }  // namespace
@@ -225,36 +273,23 @@ DIAGPU_API int diagpu_spgemm_numeric_f32(
     const int64_t* pair_ptr, const diagpu_gpair* pairs, int64_t max_pairs,
     float* C_vals, void* stream)
 {
-    using namespace diagpu;
-    const char* fn = "diagpu_spgemm_numeric_f32";
-    if (n < 1 || n > (1 << 30)) return fail(DIAGPU_ERR_ARG, "%s: n=%d outside [1, 2^30]", fn, n);
-    if (c_ndiag < 0 || c_ndiag > 2 * (int64_t)n - 1)
-        return fail(DIAGPU_ERR_ARG, "%s: c_ndiag=%lld outside [0, 2n-1]", fn, (long long)c_ndiag);
-    if (max_pairs < 0) return fail(DIAGPU_ERR_ARG, "%s: negative max_pairs", fn);
-    if (c_ndiag == 0) return DIAGPU_OK;
-    if (!C_off || !C_len || !C_starts || !pair_ptr || !C_vals)
-        return fail(DIAGPU_ERR_ARG, "%s: C structure, pair_ptr or C_vals is NULL", fn);
-    if (max_pairs > 0 && (!pairs || !A_vals || !B_vals))
-        return fail(DIAGPU_ERR_ARG, "%s: pairs or operand values are NULL", fn);
+    return diagpu::numeric_launch<float>(n, A_vals, B_vals, C_off, C_len, C_starts, c_ndiag,
+                                         pair_ptr, pairs, max_pairs, C_vals, stream,
+                                         "diagpu_spgemm_numeric_f32");
+}
 
-    const int32_t NB = (int32_t)ceil_div<int64_t>((int64_t)n + 3, kTB);
-    const int32_t nb_per_xcd = ceil_div<int32_t>(NB, kNumXcd);
-    // Many C diagonals (wide operands): 4-entry chunks, 4 workgroups per CU;
-    // few: 8-entry chunks and 8 workgroups per CU for more loads in flight.
-    const bool wide = c_ndiag >= 1024;
-    const int64_t batches_per_xcd = (int64_t)nb_per_xcd * ceil_div<int64_t>(c_ndiag, kBatch);
-    int64_t wg = (int64_t)(cu_count() / kNumXcd) * (wide ? 4 : 8);
-    if (wg > batches_per_xcd) wg = batches_per_xcd;
-    if (wg < 1) wg = 1;
-    if (wide)
-        hipLaunchKernelGGL(k_gather<4>, dim3((unsigned)(wg * kNumXcd)), dim3(kBlock), 0,
-                           as_stream(stream), A_vals, B_vals, C_off, C_len, C_starts,
-                           (int32_t)c_ndiag, pair_ptr, pairs, C_vals, NB, nb_per_xcd, (int32_t)wg);
-    else
-        hipLaunchKernelGGL(k_gather<8>, dim3((unsigned)(wg * kNumXcd)), dim3(kBlock), 0,
-                           as_stream(stream), A_vals, B_vals, C_off, C_len, C_starts,
-                           (int32_t)c_ndiag, pair_ptr, pairs, C_vals, NB, nb_per_xcd, (int32_t)wg);
-    return check_launch(fn);
+DIAGPU_API int diagpu_spgemm_numeric_c64(
+    int32_t n, const diagpu_complex64* A_vals, const diagpu_complex64* B_vals,
+    const int32_t* C_off, const int32_t* C_len, const int64_t* C_starts, int64_t c_ndiag,
+    const int64_t* pair_ptr, const diagpu_gpair* pairs, int64_t max_pairs,
+    diagpu_complex64* C_vals, void* stream)
+{
+    using diagpu::cf32;
+    return diagpu::numeric_launch<cf32>(n, reinterpret_cast<const cf32*>(A_vals),
+                                        reinterpret_cast<const cf32*>(B_vals), C_off, C_len,
+                                        C_starts, c_ndiag, pair_ptr, pairs, max_pairs,
+                                        reinterpret_cast<cf32*>(C_vals), stream,
+                                        "diagpu_spgemm_numeric_c64");
 }
 
 }  // extern "C"

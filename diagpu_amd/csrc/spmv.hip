@@ -55,6 +55,7 @@
 #include <climits>
 
 #include "common.hpp"
+#include "elem.hpp"
 #include "reduce.hpp"
 #include "spmv_internal.hpp"
 
@@ -63,97 +64,6 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kShortMax = 5;   // K <= kShortMax: straight-line kernel
-
-// ---------------------------------------------------------------------------
-// Element types and arithmetic
-// ---------------------------------------------------------------------------
-
-inline __device__ float fma_(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
-inline __device__ double fma_(double a, double b, double c) { return __builtin_fma(a, b, c); }
-
-// acc + a * x for (matrix element, vector element)
-inline __device__ float mad(float acc, float a, float x) { return fma_(a, x, acc); }
-inline __device__ double mad(double acc, double a, double x) { return fma_(a, x, acc); }
-inline __device__ cf32 mad(cf32 acc, cf32 a, cf32 x)
-{
-    cf32 r;
-    r.re = fma_(-a.im, x.im, fma_(a.re, x.re, acc.re));
-    r.im = fma_(a.im, x.re, fma_(a.re, x.im, acc.im));
-    return r;
-}
-inline __device__ cf32 mad(cf32 acc, float a, cf32 x)
-{
-    cf32 r;
-    r.re = fma_(a, x.re, acc.re);
-    r.im = fma_(a, x.im, acc.im);
-    return r;
-}
-
-inline __device__ float sel(bool c, float a, float b) { return c ? a : b; }
-inline __device__ double sel(bool c, double a, double b) { return c ? a : b; }
-inline __device__ cf32 sel(bool c, cf32 a, cf32 b)
-{
-    cf32 r;
-    r.re = c ? a.re : b.re;
-    r.im = c ? a.im : b.im;
-    return r;
-}
-
-template <typename T> inline __device__ T zero_of();
-template <> inline __device__ float zero_of<float>() { return 0.f; }
-template <> inline __device__ double zero_of<double>() { return 0.0; }
-template <> inline __device__ cf32 zero_of<cf32>() { return cf32{0.f, 0.f}; }
-
-// Re(conj(u) * y) in fp64
-inline __device__ double dotpart(float u, float y) { return (double)u * (double)y; }
-inline __device__ double dotpart(double u, double y) { return u * y; }
-inline __device__ double dotpart(cf32 u, cf32 y) { return (double)u.re * y.re + (double)u.im * y.im; }
-
-// One element, loaded as a plain vector register value.
-template <typename T> struct ElemRaw { typedef T type; };
-template <> struct ElemRaw<cf32> { typedef float type __attribute__((ext_vector_type(2))); };
-
-template <typename T, bool NT>
-inline __device__ T load_elem(const T* p)
-{
-    typedef typename ElemRaw<T>::type Raw;
-    Raw v = NT ? __builtin_nontemporal_load(reinterpret_cast<const Raw*>(p))
-               : *reinterpret_cast<const Raw*>(p);
-    T r;
-    __builtin_memcpy(&r, &v, sizeof(T));
-    return r;
-}
-
-// A lane's run of R consecutive elements (16 or 32 bytes), moved as 16-byte
-// vectors.
-template <typename T, int R> struct Run { T v[R]; };
-
-typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
-
-template <typename T, int R, bool NT>
-inline __device__ Run<T, R> load_run(const T* p)
-{
-    static_assert((R * sizeof(T)) % 16 == 0, "runs are whole 16-byte vectors");
-    constexpr int NQ = (int)(R * sizeof(T) / 16);
-    f4u q[NQ];
-#pragma unroll
-    for (int i = 0; i < NQ; ++i)
-        q[i] = NT ? __builtin_nontemporal_load(reinterpret_cast<const f4u*>(p) + i)
-                  : reinterpret_cast<const f4u*>(p)[i];
-    Run<T, R> r;
-    __builtin_memcpy(&r, q, sizeof(r));
-    return r;
-}
-
-template <typename T, int R>
-inline __device__ void store_run_nt(T* p, const Run<T, R>& r)
-{
-    constexpr int NQ = (int)(R * sizeof(T) / 16);
-    f4u q[NQ];
-    __builtin_memcpy(q, &r, sizeof(r));
-#pragma unroll
-    for (int i = 0; i < NQ; ++i) __builtin_nontemporal_store(q[i], reinterpret_cast<f4u*>(p) + i);
-}
 
 // Per (matrix element, vector element) pair: rows per lane and ring depths,
 // chosen so the kernels stay within 64 VGPRs (8 waves per SIMD).

@@ -1,5 +1,6 @@
 """Host-side SpGEMM calls over device tensors: the symbolic plan
-(diagpu_spgemm_symbolic) and the numeric phase (diagpu_spgemm_numeric_f32)
+(diagpu_spgemm_symbolic) and the numeric phase (diagpu_spgemm_numeric_f32, or
+_c64 for complex64 values)
 for HM operands, and gemm_diag on row-packed operands
 (diagpu_rowpacked_as_hm + the same two phases).
 
@@ -88,12 +89,19 @@ class SpgemmPlan:
 
     # numeric ---------------------------------------------------------------
     def numeric(self, A_vals: torch.Tensor, B_vals: torch.Tensor, C_vals: torch.Tensor) -> None:
-        _check_dev(A_vals, torch.float32, "A_vals")
-        _check_dev(B_vals, torch.float32, "B_vals")
-        _check_dev(C_vals, torch.float32, "C_vals")
+        """C values for the plan's structure; float32 or complex64 (all three
+        tensors the same dtype)."""
+        dt = A_vals.dtype
+        name = {torch.float32: "diagpu_spgemm_numeric_f32",
+                torch.complex64: "diagpu_spgemm_numeric_c64"}.get(dt)
+        if name is None:
+            raise TypeError(f"unsupported value dtype {dt}")
+        _check_dev(A_vals, dt, "A_vals")
+        _check_dev(B_vals, dt, "B_vals")
+        _check_dev(C_vals, dt, "C_vals")
         if C_vals.numel() < self.info.c_nnz:
             raise ValueError(f"C_vals has {C_vals.numel()} elements, needs {self.info.c_nnz}")
-        st = _lib.load().diagpu_spgemm_numeric_f32(
+        st = getattr(_lib.load(), name)(
             self.n, A_vals.data_ptr(), B_vals.data_ptr(), self.C_off.data_ptr(),
             self.C_len.data_ptr(), self.C_starts.data_ptr(), self.info.c_ndiag,
             self.ptr.data_ptr(), self.pairs.data_ptr(), self.info.max_pairs,
@@ -102,7 +110,7 @@ class SpgemmPlan:
             _lib.check(st)
 
     def multiply(self, A_vals: torch.Tensor, B_vals: torch.Tensor) -> torch.Tensor:
-        Cv = torch.empty(max(1, self.info.c_nnz), dtype=torch.float32, device=A_vals.device)
+        Cv = torch.empty(max(1, self.info.c_nnz), dtype=A_vals.dtype, device=A_vals.device)
         self.numeric(A_vals, B_vals, Cv)
         return Cv[: self.info.c_nnz]
 

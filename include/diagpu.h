@@ -226,6 +226,15 @@ DIAGPU_API int diagpu_spgemm_numeric_f32(
     const int64_t* pair_ptr, const diagpu_gpair* pairs, int64_t max_pairs,
     float* C_vals, void* stream);
 
+/* Complex64 variant of diagpu_spgemm_numeric_f32 for complex Hamiltonians
+ * (the reference is real only): the same plan, complex products, fp32
+ * accumulation of each part, same write-once semantics. */
+DIAGPU_API int diagpu_spgemm_numeric_c64(
+    int32_t n, const diagpu_complex64* A_vals, const diagpu_complex64* B_vals,
+    const int32_t* C_off, const int32_t* C_len, const int64_t* C_starts, int64_t c_ndiag,
+    const int64_t* pair_ptr, const diagpu_gpair* pairs, int64_t max_pairs,
+    diagpu_complex64* C_vals, void* stream);
+
 /* ======================================================================
  * gemm_diag: row-packed operands, HM-layout C
  * ====================================================================== */

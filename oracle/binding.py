@@ -288,6 +288,23 @@ def spgemm_pairs_f64(A_v, B_v, C_len, C_starts, pair_ptr, pairs, kbeg, kend):
     return out[:total], ab[:total]
 
 
+def spgemm_pairs_complex(A_v, B_v, C_len, C_starts, pair_ptr, pairs, kbeg, kend):
+    """Plan-driven complex numeric phase (complex64 data, fp64 accumulation)
+    over C diagonals [kbeg, kend): complex128 values and the term bound."""
+    C_len, C_starts = _i32(C_len), _i64(C_starts)
+    pair_ptr = _i64(pair_ptr)
+    pairs = np.ascontiguousarray(pairs, dtype=GPAIR_DTYPE)
+    if kend <= kbeg:
+        return np.zeros(0, np.complex128), np.zeros(0)
+    total = int(C_starts[kend - 1] + C_len[kend - 1] - C_starts[kbeg])
+    out = np.empty(max(total, 1), dtype=np.complex128)
+    ab = np.empty(max(total, 1), dtype=np.float64)
+    lib().orc_spgemm_pairs_c128(_p(np.ascontiguousarray(A_v, np.complex64)),
+                                _p(np.ascontiguousarray(B_v, np.complex64)), _p(C_len),
+                                _p(C_starts), _p(pair_ptr), _p(pairs), kbeg, kend, _p(out), _p(ab))
+    return out[:total], ab[:total]
+
+
 def spgemm_pairs_omp_f32(A_v, B_v, C_len, C_starts, pair_ptr, pairs, kbeg, kend, out) -> int:
     """OpenMP CPU baseline over C diagonals [kbeg, kend); returns threads used."""
     return lib().orc_spgemm_pairs_omp_f32(_p(A_v), _p(B_v), _p(C_len), _p(C_starts),

@@ -527,6 +527,39 @@ ORC_API void orc_spgemm_pairs_f64(const float* A_vals, const float* B_vals,
     }
 }
 
+/* The same plan-driven numeric phase with complex64 values (interleaved re,
+ * im) and complex products, fp64 accumulation (no reference counterpart: the
+ * reference is real only).  out holds re, im pairs; abs_out[p] = sum over
+ * terms of |a_re b_re| + |a_im b_im| + |a_re b_im| + |a_im b_re|.  Pinned by
+ * tests/test_oracle.py against dense complex products and against
+ * orc_spgemm_pairs_f64 on the four real part products. */
+ORC_API void orc_spgemm_pairs_c128(const float* A_vals, const float* B_vals,
+                                   const int* C_len, const int64_t* C_starts,
+                                   const int64_t* pair_ptr, const orc_gpair* pairs,
+                                   int kbeg, int kend, double* out, double* abs_out)
+{
+    const int64_t base = C_starts[kbeg];
+    #pragma omp parallel for schedule(dynamic)
+    for (int k = kbeg; k < kend; ++k) {
+        for (int p = 0; p < C_len[k]; ++p) {
+            double sr = 0.0, si = 0.0, aab = 0.0;
+            for (int64_t q = pair_ptr[k]; q < pair_ptr[k + 1]; ++q) {
+                const orc_gpair g = pairs[q];
+                const int pa = p + g.ash, pb = p + g.bsh;
+                if (pa < 0 || pa >= g.al || pb < 0 || pb >= g.bl) continue;
+                const double ar = A_vals[2 * (g.ab + pa)], ai = A_vals[2 * (g.ab + pa) + 1];
+                const double br = B_vals[2 * (g.bb + pb)], bi = B_vals[2 * (g.bb + pb) + 1];
+                sr += ar * br - ai * bi;
+                si += ar * bi + ai * br;
+                aab += fabs(ar * br) + fabs(ai * bi) + fabs(ar * bi) + fabs(ai * br);
+            }
+            out[2 * (C_starts[k] - base + p)] = sr;
+            out[2 * (C_starts[k] - base + p) + 1] = si;
+            if (abs_out) abs_out[C_starts[k] - base + p] = aab;
+        }
+    }
+}
+
 /* CPU baseline for SpGEMM: OpenMP over C diagonals, schedule(dynamic) as
  * spmspm/bench_spmspm.cu:384, with each C diagonal's pair list resolved once
  * (the plan) rather than per element; fp32 accumulation in plan order.

@@ -207,3 +207,88 @@ def test_propagator_full_size_properties(dev):
         return torch.vdot(psi.to(torch.complex128), hpsi.to(torch.complex128)).real.item()
     e0, e1 = energy(psi0), energy(a.psi)
     assert abs(e1 - e0) <= 1e-4 * abs(e0)
+
+
+# ------------------------------------------------------- complex SpGEMM --
+
+def _complexify(M, shift):
+    """The same HM structure with complex values v + i * roll(v, shift)."""
+    from diagpu_amd.workloads import HM
+    v = M.values
+    return HM(M.n, M.offsets, M.lengths, M.starts,
+              torch.complex(v, torch.roll(v, shift)).contiguous())
+
+
+def _plan_host(oracle, plan, A, B):
+    a_off, a_len, a_st = (t.cpu().numpy() for t in (A.offsets, A.lengths, A.starts))
+    b_off, b_len, b_st = (t.cpu().numpy() for t in (B.offsets, B.lengths, B.starts))
+    c_off, c_len, c_st, nnz = oracle.c_structure(A.n, a_off, b_off)
+    ptr, pairs = oracle.pairs_only(A.n, a_off, a_len, a_st, b_off, b_len, b_st, c_off)
+    assert np.array_equal(plan.c_offsets().cpu().numpy(), c_off)
+    assert np.array_equal(plan.pair_ptr().cpu().numpy(), ptr)
+    return c_len, c_st, ptr, pairs
+
+
+def _check_complex(got, want, ab):
+    for part in (np.real, np.imag):
+        err = np.abs(part(got).astype(np.float64) - part(want))
+        assert (err <= 1e-5 * ab + 1e-300).all(), float(err.max())
+
+
+@pytest.mark.parametrize("seed,n,na,nb,span", [
+    (0, 37, 5, 4, 36), (1, 1000, 12, 30, 999), (2, 3001, 40, 8, 2999), (3, 1031, 64, 64, 1030)])
+def test_complex_spgemm_random(dev, oracle, seed, n, na, nb, span):
+    from diagpu_amd.spgemm import SpgemmPlan
+    rng = np.random.default_rng(seed)
+    oa = rng.choice(np.arange(-span, span + 1), size=na, replace=False)
+    ob = rng.choice(np.arange(-span, span + 1), size=nb, replace=False)
+    A = _complexify(workloads.hm_random(n, oa, seed=seed, device=dev), 3)
+    B = _complexify(workloads.hm_random(n, ob, seed=seed + 50, device=dev), 5)
+    plan = SpgemmPlan(A, B)
+    c_len, c_st, ptr, pairs = _plan_host(oracle, plan, A, B)
+    C1 = plan.multiply(A.values, B.values)
+    C2 = plan.multiply(A.values, B.values)
+    assert C1.dtype == torch.complex64 and torch.equal(C1, C2)
+    want, ab = oracle.spgemm_pairs_complex(A.values.cpu().numpy(), B.values.cpu().numpy(),
+                                           c_len, c_st, ptr, pairs, 0, len(c_len))
+    _check_complex(C1.cpu().numpy(), want, ab)
+
+
+def test_complex_spgemm_real_values_equal_real_kernel(dev):
+    """Zero imaginary parts: the complex kernel's real part is the real
+    kernel's result bit for bit and its imaginary part is zero."""
+    from diagpu_amd.spgemm import SpgemmPlan
+    from diagpu_amd.workloads import HM
+    A, B = workloads.spgemm_config(4, seed=7, device=dev)
+    plan = SpgemmPlan(A, B)
+    Cr = plan.multiply(A.values, B.values)
+    Ac = torch.complex(A.values, torch.zeros_like(A.values)).contiguous()
+    Bc = torch.complex(B.values, torch.zeros_like(B.values)).contiguous()
+    Cc = plan.multiply(Ac, Bc)
+    assert torch.equal(Cc.real, Cr) and torch.count_nonzero(Cc.imag) == 0
+
+
+def test_complex_spgemm_config4_and_config5(dev, oracle):
+    """Config 4's structure with complex values over every C value; config 5
+    on a sample of C diagonals (C has 2.4e9 complex values)."""
+    from diagpu_amd.spgemm import SpgemmPlan
+    for cfg, sample in ((4, None), (5, 24)):
+        A, B = workloads.spgemm_config(cfg, seed=cfg, device=dev)
+        A, B = _complexify(A, 1), _complexify(B, 2)
+        plan = SpgemmPlan(A, B)
+        c_len, c_st, ptr, pairs = _plan_host(oracle, plan, A, B)
+        Cv = plan.multiply(A.values, B.values)
+        torch.cuda.synchronize()
+        Av, Bv = A.values.cpu().numpy(), B.values.cpu().numpy()
+        if sample is None:
+            want, ab = oracle.spgemm_pairs_complex(Av, Bv, c_len, c_st, ptr, pairs, 0, len(c_len))
+            _check_complex(Cv.cpu().numpy(), want, ab)
+        else:
+            rng = np.random.default_rng(cfg)
+            ks = sorted({0, len(c_len) - 1, *rng.choice(len(c_len), sample).tolist()})
+            for k in ks:
+                want, ab = oracle.spgemm_pairs_complex(Av, Bv, c_len, c_st, ptr, pairs, k, k + 1)
+                got = Cv[int(c_st[k]):int(c_st[k]) + int(c_len[k])].cpu().numpy()
+                _check_complex(got, want, ab)
+        del Cv, plan
+        torch.cuda.empty_cache()

@@ -27,8 +27,8 @@ TC_CASES = [  # spmv/test/test_tc_spmv.cu:168-179
 
 
 def hm_to_dense(n, offs, starts, vals):
-    """hm_to_dense of spmspm/paper_hm.cuh:68-83."""
-    D = np.zeros((n, n))
+    """hm_to_dense of spmspm/paper_hm.cuh:68-83 (real or complex values)."""
+    D = np.zeros((n, n), dtype=np.result_type(np.asarray(vals).dtype, np.float64))
     for d, s in zip(offs, starts):
         sr, sc = (0, d) if d >= 0 else (-d, 0)
         for p in range(n - abs(d)):
@@ -249,6 +249,37 @@ def test_pair_plan_and_numeric_vs_dense(oracle, seed):
     oracle.spgemm_pairs_omp_f32(A[3], B[3], c_len.astype(np.int32), c_st, ptr, pairs, 0,
                                 len(c_off), out)
     assert np.all(np.abs(out - want) <= 1e-5 * ab + 1e-30)
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_complex_pair_numeric_vs_dense(oracle, seed):
+    """Complex plan-driven numeric phase (no reference counterpart): the dense
+    complex product gives every C value, and each part equals the real oracle
+    on the four real part products (Re = ArBr - AiBi, Im = ArBi + AiBr)."""
+    rng = np.random.default_rng(300 + seed)
+    n = int(rng.integers(20, 70))
+    oa = rng.choice(np.arange(-n + 1, n), size=int(rng.integers(1, 8)), replace=False)
+    ob = rng.choice(np.arange(-n + 1, n), size=int(rng.integers(1, 8)), replace=False)
+    A = hm_random_np(n, oa, rng)
+    B = hm_random_np(n, ob, rng)
+    Ai = rng.uniform(-1, 1, A[3].size).astype(np.float32)
+    Bi = rng.uniform(-1, 1, B[3].size).astype(np.float32)
+    Ac = (A[3] + 1j * Ai).astype(np.complex64)
+    Bc = (B[3] + 1j * Bi).astype(np.complex64)
+    c_off, c_len, c_st, nnz = oracle.c_structure(n, A[0], B[0])
+    ptr, pairs = oracle.pairs_only(n, A[0], A[1], A[2], B[0], B[1], B[2], c_off)
+    got, ab = oracle.spgemm_pairs_complex(Ac, Bc, c_len, c_st, ptr, pairs, 0, len(c_off))
+    dense = (hm_to_dense(n, A[0], A[2], Ac.astype(np.complex128))
+             @ hm_to_dense(n, B[0], B[2], Bc.astype(np.complex128)))
+    want = np.zeros(nnz, np.complex128)
+    for d, s0, ln in zip(c_off, c_st, c_len):
+        sr, sc = (0, d) if d >= 0 else (-d, 0)
+        want[s0:s0 + ln] = dense[sr + np.arange(ln), sc + np.arange(ln)]
+    assert np.allclose(got, want, rtol=0, atol=1e-12)
+    part = lambda a, b: oracle.spgemm_pairs_f64(a, b, c_len, c_st, ptr, pairs, 0, len(c_off))[0]
+    assert np.allclose(got.real, part(A[3], B[3]) - part(Ai, Bi), rtol=0, atol=1e-12)
+    assert np.allclose(got.imag, part(A[3], Bi) + part(Ai, B[3]), rtol=0, atol=1e-12)
+    assert np.all(ab >= np.abs(got.real) - 1e-12) and np.all(ab >= np.abs(got.imag) - 1e-12)
 
 
 def test_gemm_diag_formula_vs_dense(oracle):
