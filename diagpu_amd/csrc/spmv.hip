@@ -391,20 +391,34 @@ int spmv_run(int32_t rows, int32_t cols, int32_t num_diags, const int32_t* offs,
 }
 
 namespace {
-__global__ __launch_bounds__(kBlock) void k_sum_partials(const double* __restrict__ partials,
-                                                         int32_t n, double* __restrict__ out)
+constexpr int kSumBlock = 1024;
+constexpr int kSumUnroll = 8;
+
+// Lane l adds partials l, l + 1024, l + 2048, ... in that order (loads of a
+// batch of 8 issued before their adds), then a fixed tree: deterministic, and
+// up to 8192 partials cost one memory round trip.
+__global__ __launch_bounds__(kSumBlock) void k_sum_partials(const double* __restrict__ partials,
+                                                            int32_t n, double* __restrict__ out)
 {
     double t = 0.0;
-    for (int i = (int)threadIdx.x; i < n; i += kBlock) t += partials[i];
-    t = block_sum<kBlock>(t);
+    int i = (int)threadIdx.x;
+    for (; i + (kSumUnroll - 1) * kSumBlock < n; i += kSumUnroll * kSumBlock) {
+        double v[kSumUnroll];
+#pragma unroll
+        for (int u = 0; u < kSumUnroll; ++u) v[u] = partials[i + u * kSumBlock];
+#pragma unroll
+        for (int u = 0; u < kSumUnroll; ++u) t += v[u];
+    }
+    for (; i < n; i += kSumBlock) t += partials[i];
+    t = block_sum<kSumBlock>(t);
     if (threadIdx.x == 0) *out = t;
 }
 }  // namespace
 
 int sum_partials(const double* partials, int32_t n, double* out, void* stream)
 {
-    hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(kBlock), 0, as_stream(stream), partials, n,
-                       out);
+    hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(kSumBlock), 0, as_stream(stream), partials,
+                       n, out);
     return check_launch("sum_partials");
 }
 
