@@ -212,7 +212,55 @@ def time_krylov(m: int = 30, t: float = 1.0, reps: int = 5):
 # SpGEMM (configs 4 and 5)
 # --------------------------------------------------------------------------
 
-def time_spgemm(cfg: int, seed: int, reps: int, complex_values: bool = False):
+def cpu_spgemm_baseline(plan, A, B, seconds: float):
+    """The oracle's OpenMP SpGEMM loop (schedule(dynamic) over C diagonals,
+    each C diagonal's pairs resolved once, fp32 accumulation) on the host
+    cores, over a bounded prefix of C diagonals (about `seconds` of work,
+    growing the prefix until it takes at least a tenth of that); GFLOP/s and
+    GB/s from the sample's own useful flops and algorithmic bytes."""
+    import numpy as np
+    from oracle import binding as orc
+    Av = A.values.cpu().numpy()
+    Bv = B.values.cpu().numpy()
+    c_len = plan.c_lengths().cpu().numpy().astype(np.int32)
+    c_st = plan.c_starts().cpu().numpy()
+    ptr = plan.pair_ptr().cpu().numpy()
+    pairs = plan.pairs_numpy()
+    nC = len(c_len)
+    counts = np.diff(ptr)
+    # useful flops per C diagonal: 2 * sum over its pairs of the overlap
+    ov = (np.minimum(pairs["al"] - pairs["ash"], pairs["bl"] - pairs["bsh"])
+          - np.maximum(0, np.maximum(-pairs["ash"], -pairs["bsh"])))
+    ov = np.minimum(ov, np.repeat(c_len.astype(np.int64), counts)).clip(min=0)
+    fl_k = 2 * np.add.reduceat(ov.astype(np.int64), ptr[:-1]) if nC else np.zeros(0)
+    k = max(1, min(nC, 64))
+    while True:
+        out = np.empty(int(c_st[k - 1] + c_len[k - 1] - c_st[0]), np.float32)
+        t0 = time.perf_counter()
+        threads = orc.spgemm_pairs_omp_f32(Av, Bv, c_len, c_st, ptr, pairs, 0, k, out)
+        el = time.perf_counter() - t0
+        if el >= seconds / 10 or k == nC:
+            break
+        k = min(nC, k * 4)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        orc.spgemm_pairs_omp_f32(Av, Bv, c_len, c_st, ptr, pairs, 0, k, out)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 3 and el >= seconds / 2:
+            break
+    sec = el / reps
+    flops = float(fl_k[:k].sum())
+    # bytes: the sample's C values once plus the A and B values its pairs read
+    byt = 4 * (2 * float(ov[: ptr[k]].sum()) + out.size)
+    return {"value": round(flops / sec / 1e9, 2), "unit": "GFLOP/s", "GBs": round(byt / sec / 1e9, 2),
+            "cores": threads, "kind": "port",
+            "sample": f"C diagonals 0..{k - 1} of {nC} ({100.0 * flops / max(1.0, float(fl_k.sum())):.1f}% "
+                      f"of the flops), {reps} runs of {sec * 1e3:.1f} ms, oracle OpenMP loop"}
+
+
+def time_spgemm(cfg: int, seed: int, reps: int, complex_values: bool = False,
+                cpu_seconds: float = 0.0):
     import torch
     from diagpu_amd import workloads
     from diagpu_amd.spgemm import SpgemmPlan
@@ -262,6 +310,9 @@ def time_spgemm(cfg: int, seed: int, reps: int, complex_values: bool = False):
         "GFLOPs": round(flops / (ms * 1e6), 1), "useful_flops": flops,
         "GBs": round(alg / (ms * 1e6), 1), "frac_hbm": round(alg / (ms * 1e6) / HBM_PEAK_GBS, 4),
         "alg_bytes": alg, "buffer_sets": nsets,
+        "total_ms": round(ms + sym_ms, 5),
+        "cpu_baseline": (cpu_spgemm_baseline(plan, A, B, cpu_seconds)
+                         if cpu_seconds > 0 and not complex_values else None),
     }
 
 
@@ -382,9 +433,20 @@ def main(argv=None) -> int:
                 torch.cuda.empty_cache()
             except Exception as e:  # report, keep the headline
                 extras[f"spmv_cfg{cfg}_{dt}_{xt}"] = {"error": repr(e)}
+        # warm (MALL-resident) headline: one buffer set, the same matrix
+        try:
+            res = time_spmv(2, torch.float32, 400, 40, args.seed, 1)
+            rec = spmv_record(2, torch.float32, res)
+            rec["note"] = "warm: one buffer set (117 MB), reused every step from the MALL"
+            extras["spmv_cfg2_f32_warm"] = rec
+            log(f"extra spmv cfg2 warm: {res['gbs']:.1f} GB/s")
+            del res
+        except Exception as e:
+            extras["spmv_cfg2_f32_warm"] = {"error": repr(e)}
         for cfg in (4, 5):
             try:
-                rec = time_spgemm(cfg, args.seed, 50 if cfg == 4 else 10)
+                rec = time_spgemm(cfg, args.seed, 50 if cfg == 4 else 10,
+                                  cpu_seconds=min(3.0, args.cpu_seconds))
                 extras[f"spgemm_cfg{cfg}"] = rec
                 log(f"extra spgemm cfg{cfg}: {rec['GFLOPs']} GFLOP/s, {rec['GBs']} GB/s")
                 torch.cuda.empty_cache()

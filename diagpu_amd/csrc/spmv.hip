@@ -71,7 +71,7 @@ template <typename TV, typename TX> struct Shape {
     static constexpr int R = (int)(16 / sizeof(TV));
     static constexpr bool wide_x = R * sizeof(TX) > 16;   // 32-byte x runs
     static constexpr int W = wide_x ? 4 : 6;              // interior ring
-    static constexpr int WE = wide_x ? 2 : 3;             // edge ring
+    static constexpr int WE = wide_x ? 2 : 5;             // edge ring
     static constexpr int TILE = kBlock * R;
 };
 
