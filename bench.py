@@ -47,7 +47,7 @@ def parse_args(argv=None):
     ap.add_argument("--only", default="",
                     help="profiling aid: run just one workload (spmv2, spmv2d, spmv2c, "
                          "spmv2rc, spmv1, spmv3, spgemm4, spgemm5, spgemm4c, spgemm5c, taylor, krylov, "
-                         "copy) "
+                         "propagator, copy) "
                          "and print its line")
     return ap.parse_args(argv)
 
@@ -345,6 +345,64 @@ def time_taylor(order: int = 6, t: float = 0.05):
             "steps": steps}
 
 
+def time_propagator(order: int = 6, dt: float = 0.02, m: int = 12, reps: int = 20):
+    """The two propagation workflows of slides/transcript.md:10-18 on the
+    7-point stencil of SpGEMM config 4 (n = 2^20): build U = exp(-i dt H)
+    once (complex Taylor chain + device HM->Recon) and apply it by the
+    complex SpMV, against one Lanczos call per time step on H itself.
+    Break-even = the number of steps after which building U has paid off."""
+    import torch
+    from diagpu_amd import chain, workloads
+    from diagpu_amd.krylov import expm_krylov, KrylovWorkspace
+    from diagpu_amd.spmv import spmv_recon
+    H = workloads.hm_stencil7(128, 128, 64, device="cuda")
+    n = H.n
+    chain.to_recon(chain.propagator(H, dt, order))          # warm-up (plans, allocator)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    U = chain.propagator(H, dt, order)
+    u_off, u_val = chain.to_recon(U)
+    torch.cuda.synchronize()
+    build_ms = (time.perf_counter() - t0) * 1e3
+    del U
+    g = torch.Generator(device="cuda").manual_seed(4)
+    psi = torch.complex(torch.randn(n, device="cuda", generator=g),
+                        torch.randn(n, device="cuda", generator=g)).contiguous()
+    y = torch.empty_like(psi)
+    for _ in range(3):
+        spmv_recon(u_off, u_val, n, n, psi, y)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        spmv_recon(u_off, u_val, n, n, psi, y)
+    e1.record()
+    torch.cuda.synchronize()
+    apply_ms = e0.elapsed_time(e1) / reps
+    K = u_off.numel()
+    apply_bytes = 8 * K * n + 8 * 2 * n                    # U values + x + y (padding included)
+    h_off, h_val = chain.to_recon(H)
+    ws = KrylovWorkspace(n, m)
+    out = torch.empty_like(psi)
+    expm_krylov(h_off, h_val, n, psi, dt, m, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        res = expm_krylov(h_off, h_val, n, psi, dt, m, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    kry_ms = (time.perf_counter() - t0) * 1e3 / reps
+    nrm = torch.linalg.vector_norm(psi.to(torch.complex128)).item()
+    rel = torch.linalg.vector_norm((y - out).to(torch.complex128)).item() / nrm
+    return {"workload": "propagator_stencil7_cfg4", "n": n, "order": order, "dt": dt,
+            "U_diags": K, "U_bytes": 8 * K * n, "build_ms": round(build_ms, 3),
+            "apply_ms": round(apply_ms, 4),
+            "apply_GBs": round(apply_bytes / (apply_ms * 1e6), 1),
+            "apply_frac_hbm": round(apply_bytes / (apply_ms * 1e6) / HBM_PEAK_GBS, 4),
+            "krylov_m": m, "krylov_ms": round(kry_ms, 4), "krylov_steps": res.steps,
+            "krylov_err_estimate": res.err_estimate, "rel_diff_U_vs_krylov": rel,
+            "break_even_steps": (round(build_ms / (kry_ms - apply_ms), 1)
+                                 if kry_ms > apply_ms else None)}
+
+
 def copy_calibration(steps: int):
     """A plain device copy of known size, for scaling rocprof FETCH/WRITE counters."""
     import torch
@@ -399,6 +457,8 @@ def main(argv=None) -> int:
                   flush=True)
         elif w == "taylor":
             print(json.dumps(time_taylor()), flush=True)
+        elif w == "propagator":
+            print(json.dumps(time_propagator()), flush=True)
         else:
             raise SystemExit(f"unknown --only {w}")
         return 0
@@ -466,6 +526,14 @@ def main(argv=None) -> int:
             torch.cuda.empty_cache()
         except Exception as e:
             extras["taylor_chain"] = {"error": repr(e)}
+        try:
+            rec = time_propagator()
+            extras["propagator"] = rec
+            log(f"extra propagator: build {rec['build_ms']} ms, apply {rec['apply_ms']} ms, "
+                f"krylov {rec['krylov_ms']} ms")
+            torch.cuda.empty_cache()
+        except Exception as e:
+            extras["propagator"] = {"error": repr(e)}
 
     traffic = load_traffic("spmv_cfg2_f32")
     line = {

@@ -43,6 +43,10 @@ class ReconViewC64(C.Structure):
                 ("diag_offsets", C.c_void_p), ("values", C.c_void_p)]
 
 
+class Complex64(C.Structure):
+    _fields_ = [("re", C.c_float), ("im", C.c_float)]
+
+
 class KrylovInfo(C.Structure):
     _fields_ = [("steps", C.c_int32), ("breakdown", C.c_int32), ("psi0_norm", C.c_double),
                 ("err_estimate", C.c_double)]
@@ -99,6 +103,12 @@ PROTOTYPES: dict[str, tuple] = {
         _i32, _vp, _vp, _i32, _vp, C.c_float,
         _vp, _vp, _i32, _vp, C.c_float,
         _vp, _vp, _i32, _vp, _vp]),
+    "diagpu_dia_axpby_c64": (C.c_int, [
+        _i32, _vp, _vp, _i32, _vp, Complex64,
+        _vp, _vp, _i32, _vp, Complex64,
+        _vp, _vp, _i32, _vp, _vp]),
+    "diagpu_hm_to_recon_f32": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp]),
+    "diagpu_hm_to_recon_c64": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp]),
 }
 
 _lib: C.CDLL | None = None

@@ -5,9 +5,12 @@ A grows"; :110-117 "fully on-device plan build").
 
 Every product builds its C structure and pair plan on the GPU
 (diagpu_spgemm_symbolic; one stream sync returns the counts) and fills C with
-diagpu_spgemm_numeric_f32.  Sums and scalings use diagpu_dia_axpby_f32 over
-the union of the operands' diagonals; the union itself is a merge of two
-short sorted offset lists on the host.
+diagpu_spgemm_numeric_f32 (or _c64).  Sums and scalings use
+diagpu_dia_axpby_f32 (or _c64) over the union of the operands' diagonals; the
+union itself is a merge of two short sorted offset lists on the host.  Values
+are float32 or complex64; a complex factor or operand makes the result
+complex (propagator(H, dt, order) builds exp(-i dt H), and to_recon hands it
+to the SpMV path).
 
 torch tensors only carry device memory; all arithmetic is in libdiagpu.
 """
@@ -25,7 +28,7 @@ from .spmv import _stream_handle
 from .workloads import HM, hm_layout
 
 
-def hm_structure(n: int, offsets, device) -> HM:
+def hm_structure(n: int, offsets, device, dtype=torch.float32) -> HM:
     """An HM matrix with the given (ascending, distinct) offsets and
     uninitialised values."""
     offs, lens, starts = hm_layout(n, offsets)
@@ -36,37 +39,61 @@ def hm_structure(n: int, offsets, device) -> HM:
     return HM(n, torch.tensor(offs, dtype=torch.int32, device=device),
               torch.tensor(lens, dtype=torch.int32, device=device),
               torch.tensor(starts, dtype=torch.int64, device=device),
-              torch.empty(max(1, int(sum(lens))), dtype=torch.float32, device=device)[: int(sum(lens))])
+              torch.empty(max(1, int(sum(lens))), dtype=dtype, device=device)[: int(sum(lens))])
 
 
-def identity(n: int, device) -> HM:
-    I = hm_structure(n, [0], device)
+def identity(n: int, device, dtype=torch.float32) -> HM:
+    I = hm_structure(n, [0], device, dtype)
     I.values.fill_(1.0)
     return I
+
+
+def as_complex(M: HM) -> HM:
+    """The same matrix with complex64 values (a copy; M itself if already complex)."""
+    if M.values.dtype == torch.complex64:
+        return M
+    return HM(M.n, M.offsets, M.lengths, M.starts, M.values.to(torch.complex64))
+
+
+def _c64(z) -> "_lib.Complex64":
+    z = complex(z)
+    return _lib.Complex64(z.real, z.imag)
 
 
 def _host_offsets(M: HM) -> list[int]:
     return M.offsets.cpu().tolist()
 
 
-def axpby(alpha: float, X: HM, beta: float, Y: HM | None, stream=None) -> HM:
-    """Z = alpha * X + beta * Y on the union of the two diagonal sets."""
+def axpby(alpha, X: HM, beta, Y: HM | None, stream=None) -> HM:
+    """Z = alpha * X + beta * Y on the union of the two diagonal sets (complex
+    if either factor or operand is)."""
     if Y is not None and Y.n != X.n:
         raise ValueError("X and Y must have the same dimension")
+    cplx = (isinstance(alpha, complex) or isinstance(beta, complex)
+            or X.values.dtype == torch.complex64
+            or (Y is not None and Y.values.dtype == torch.complex64))
+    if cplx:
+        X = as_complex(X)
+        Y = as_complex(Y) if Y is not None else None
+    dt = torch.complex64 if cplx else torch.float32
     ox = _host_offsets(X)
     oy = _host_offsets(Y) if Y is not None else []
     for offs, nm in ((ox, "X"), (oy, "Y")):
         if any(b <= a for a, b in zip(offs, offs[1:])):
             raise ValueError(f"{nm} offsets must be ascending and distinct")
-    Z = hm_structure(X.n, sorted(set(ox) | set(oy)), X.values.device)
+    Z = hm_structure(X.n, sorted(set(ox) | set(oy)), X.values.device, dt)
     for M, nm in ((X, "X"), (Y, "Y")):
         if M is not None:
-            _check_dev(M.values, torch.float32, f"{nm}.values")
+            _check_dev(M.values, dt, f"{nm}.values")
     ny = Y.ndiag if Y is not None else 0
-    _lib.call("diagpu_dia_axpby_f32", X.n,
-              X.offsets.data_ptr(), X.starts.data_ptr(), X.ndiag, X.values.data_ptr(), float(alpha),
+    if cplx:
+        a, b, name = _c64(alpha), _c64(beta), "diagpu_dia_axpby_c64"
+    else:
+        a, b, name = float(alpha), float(beta), "diagpu_dia_axpby_f32"
+    _lib.call(name, X.n,
+              X.offsets.data_ptr(), X.starts.data_ptr(), X.ndiag, X.values.data_ptr(), a,
               Y.offsets.data_ptr() if ny else None, Y.starts.data_ptr() if ny else None, ny,
-              Y.values.data_ptr() if ny else None, float(beta),
+              Y.values.data_ptr() if ny else None, b,
               Z.offsets.data_ptr(), Z.starts.data_ptr(), Z.ndiag, Z.values.data_ptr(),
               _stream_handle(stream))
     return Z
@@ -97,13 +124,15 @@ def _timed(stats_list, fn, *args, **kw):
 def multiply(A: HM, B: HM, stats: ChainStats | None = None) -> HM:
     """C = A * B with its plan built on the device for this product (torch's
     current stream; one sync for the symbolic counts)."""
+    if A.values.dtype != B.values.dtype:          # a complex operand makes both complex
+        A, B = as_complex(A), as_complex(B)
     if stats is not None:
         torch.cuda.synchronize()
     t0 = time.perf_counter()
     plan = SpgemmPlan(A, B)
     inf = plan.info
     C = HM(A.n, plan.c_offsets().clone(), plan.c_lengths().clone(), plan.c_starts().clone(),
-           torch.empty(max(1, inf.c_nnz), dtype=torch.float32, device=A.values.device)[: inf.c_nnz])
+           torch.empty(max(1, inf.c_nnz), dtype=A.values.dtype, device=A.values.device)[: inf.c_nnz])
     if stats is not None:
         torch.cuda.synchronize()
     t1 = time.perf_counter()
@@ -129,27 +158,32 @@ def power(H: HM, k: int, stats: ChainStats | None = None) -> HM:
     return P
 
 
-def add_identity(S: HM, sigma: float = 1.0, stream=None) -> HM:
+def add_identity(S: HM, sigma=1.0, stream=None) -> HM:
     """S + sigma I: in place when S holds the main diagonal, else a new
     matrix on the union of the diagonal sets."""
     offs = _host_offsets(S)
+    dt = S.values.dtype
     if 0 not in offs:
-        return axpby(1.0, S, sigma, identity(S.n, S.values.device), stream)
+        return axpby(1.0, S, sigma, identity(S.n, S.values.device, dt), stream)
     i = offs.index(0)
-    I = identity(S.n, S.values.device)
+    I = identity(S.n, S.values.device, dt)
     o4, s8 = S.offsets.element_size(), S.starts.element_size()
+    if dt == torch.complex64:
+        one, sg, name = _c64(1.0), _c64(sigma), "diagpu_dia_axpby_c64"
+    else:
+        one, sg, name = 1.0, float(sigma), "diagpu_dia_axpby_f32"
     # X = Z = S's main diagonal alone (one offset, its start), Y = I
-    _lib.call("diagpu_dia_axpby_f32", S.n,
+    _lib.call(name, S.n,
               S.offsets.data_ptr() + i * o4, S.starts.data_ptr() + i * s8, 1,
-              S.values.data_ptr(), 1.0,
-              I.offsets.data_ptr(), I.starts.data_ptr(), 1, I.values.data_ptr(), float(sigma),
+              S.values.data_ptr(), one,
+              I.offsets.data_ptr(), I.starts.data_ptr(), 1, I.values.data_ptr(), sg,
               S.offsets.data_ptr() + i * o4, S.starts.data_ptr() + i * s8, 1,
               S.values.data_ptr(), _stream_handle(stream))
     return S
 
 
-def taylor_expm(H: HM, t: float, order: int, stats: ChainStats | None = None) -> HM:
-    """S = sum_{k=0..order} (t H)^k / k! in Horner form,
+def taylor_expm(H: HM, t, order: int, stats: ChainStats | None = None) -> HM:
+    """S = sum_{k=0..order} (t H)^k / k! (t real or complex) in Horner form,
 
         S_order = I + (t/order) H,   S_j = I + S_{j+1} * ((t/j) H),   S = S_1,
 
@@ -161,15 +195,39 @@ def taylor_expm(H: HM, t: float, order: int, stats: ChainStats | None = None) ->
     if order < 0:
         raise ValueError("order must be >= 0")
     dev = H.values.device
+    if isinstance(t, complex):
+        H = as_complex(H)
     if order == 0:
-        return identity(H.n, dev)
+        return identity(H.n, dev, H.values.dtype)
     ax = stats.axpby if stats else None
-    S = _timed(ax, axpby, t / order, H, 1.0, identity(H.n, dev))
+    S = _timed(ax, axpby, t / order, H, 1.0, identity(H.n, dev, H.values.dtype))
     for j in range(order - 1, 0, -1):
         Hj = _timed(ax, axpby, t / j, H, 0.0, None)
         S = multiply(S, Hj, stats)
         S = _timed(ax, add_identity, S)
     return S
+
+
+def propagator(H: HM, dt: float, order: int, stats: ChainStats | None = None) -> HM:
+    """U = sum_{k=0..order} (-i dt H)^k / k!, the truncated Taylor propagator
+    exp(-i dt H) (complex64) built by the SpGEMM chain: the "build U once,
+    apply it cheaply" side of slides/transcript.md:10-18."""
+    return taylor_expm(H, complex(0.0, -dt), order, stats)
+
+
+def to_recon(M: HM, stream=None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(offsets descending, values ndiag x n) of M in the Recon layout, built
+    on the device (diagpu_hm_to_recon_f32 / _c64), for the SpMV path."""
+    dt = M.values.dtype
+    name = {torch.float32: "diagpu_hm_to_recon_f32",
+            torch.complex64: "diagpu_hm_to_recon_c64"}.get(dt)
+    if name is None:
+        raise TypeError(f"unsupported value dtype {dt}")
+    r_off = torch.empty(M.ndiag, dtype=torch.int32, device=M.values.device)
+    r_val = torch.empty(M.ndiag * M.n, dtype=dt, device=M.values.device)
+    _lib.call(name, M.n, M.offsets.data_ptr(), M.starts.data_ptr(), M.ndiag,
+              M.values.data_ptr(), r_off.data_ptr(), r_val.data_ptr(), _stream_handle(stream))
+    return r_off, r_val
 
 
 # ---- host helpers for tests and examples ----------------------------------
@@ -179,8 +237,9 @@ def hm_to_dense(M: HM) -> np.ndarray:
     n = M.n
     offs = _host_offsets(M)
     starts = M.starts.cpu().numpy()
-    vals = M.values.cpu().numpy().astype(np.float64)
-    D = np.zeros((n, n))
+    v = M.values.cpu().numpy()
+    vals = v.astype(np.complex128 if np.iscomplexobj(v) else np.float64)
+    D = np.zeros((n, n), vals.dtype)
     for d, s in zip(offs, starts):
         ln = n - abs(d)
         r = np.arange(ln) + max(-d, 0)
@@ -189,12 +248,15 @@ def hm_to_dense(M: HM) -> np.ndarray:
 
 
 def hm_matvec64(M: HM, x: np.ndarray) -> np.ndarray:
-    """y = M x in float64 over the HM diagonals (host)."""
+    """y = M x in float64 (complex128 for complex M or x) over the HM
+    diagonals (host)."""
     n = M.n
     offs = _host_offsets(M)
     starts = M.starts.cpu().numpy()
-    vals = M.values.cpu().numpy().astype(np.float64)
-    y = np.zeros(n)
+    v = M.values.cpu().numpy()
+    cplx = np.iscomplexobj(v) or np.iscomplexobj(x)
+    vals = v.astype(np.complex128 if cplx else np.float64)
+    y = np.zeros(n, np.complex128 if cplx else np.float64)
     for d, s in zip(offs, starts):
         ln = n - abs(d)
         r0 = max(-d, 0)

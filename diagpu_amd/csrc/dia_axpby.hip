@@ -12,6 +12,7 @@
 // (spmspm/gather_flat.cuh:13-14,110-117) but ships no driver for it.  The
 // Taylor chain needs this to scale H and to add each power into the sum.
 #include "common.hpp"
+#include "elem.hpp"
 
 namespace diagpu {
 namespace {
@@ -31,12 +32,22 @@ __device__ __forceinline__ int find_offset(const int32_t* __restrict__ off, int 
     return -1;
 }
 
+__device__ __forceinline__ float axpby_(float a, float x, float b, float y) { return a * x + b * y; }
+__device__ __forceinline__ cf32 axpby_(cf32 a, cf32 x, cf32 b, cf32 y)
+{
+    cf32 r;
+    r.re = a.re * x.re - a.im * x.im + (b.re * y.re - b.im * y.im);
+    r.im = a.re * x.im + a.im * x.re + (b.re * y.im + b.im * y.re);
+    return r;
+}
+
+template <typename T>
 __global__ __launch_bounds__(kBlock) void k_axpby(
     int32_t n, const int32_t* __restrict__ X_off, const int64_t* __restrict__ X_starts, int32_t nx,
-    const float* Xv, float alpha, const int32_t* __restrict__ Y_off,
-    const int64_t* __restrict__ Y_starts, int32_t ny, const float* Yv, float beta,
+    const T* Xv, T alpha, const int32_t* __restrict__ Y_off,
+    const int64_t* __restrict__ Y_starts, int32_t ny, const T* Yv, T beta,
     const int32_t* __restrict__ Z_off, const int64_t* __restrict__ Z_starts, int32_t nz,
-    float* Zv, int32_t span_blocks)
+    T* Zv, int32_t span_blocks)
 {
     // blockIdx.x enumerates (Z diagonal, span) pairs, spans fastest.
     for (int64_t w = blockIdx.x; w < (int64_t)nz * span_blocks; w += gridDim.x) {
@@ -50,20 +61,47 @@ __global__ __launch_bounds__(kBlock) void k_axpby(
         const int yi = find_offset(Y_off, ny, d);
         // Z may be X (or Y) itself, element for element: each lane reads its
         // positions before it writes them, so the value pointers are not restrict.
-        const float* xp = xi >= 0 ? Xv + X_starts[xi] : nullptr;
-        const float* yp = yi >= 0 ? Yv + Y_starts[yi] : nullptr;
-        float* zp = Zv + Z_starts[z];
-        float xv[4], yv[4];
+        const T* xp = xi >= 0 ? Xv + X_starts[xi] : nullptr;
+        const T* yp = yi >= 0 ? Yv + Y_starts[yi] : nullptr;
+        T* zp = Zv + Z_starts[z];
+        T xv[4], yv[4];
         for (int e = 0; e < 4; ++e) {           // all loads first, then the stores
             const int64_t p = p0 + (int64_t)e * kBlock + threadIdx.x;
-            xv[e] = (xp && p < len) ? xp[p] : 0.0f;
-            yv[e] = (yp && p < len) ? yp[p] : 0.0f;
+            xv[e] = (xp && p < len) ? xp[p] : zero_of<T>();
+            yv[e] = (yp && p < len) ? yp[p] : zero_of<T>();
         }
         for (int e = 0; e < 4; ++e) {
             const int64_t p = p0 + (int64_t)e * kBlock + threadIdx.x;
-            if (p < len) zp[p] = alpha * xv[e] + beta * yv[e];
+            if (p < len) zp[p] = axpby_(alpha, xv[e], beta, yv[e]);
         }
     }
+}
+
+inline bool is_zero(float a) { return a == 0.0f; }
+inline bool is_zero(cf32 a) { return a.re == 0.0f && a.im == 0.0f; }
+
+template <typename T>
+int axpby_launch(int32_t n, const int32_t* X_off, const int64_t* X_starts, int32_t nx,
+                 const T* X_vals, T alpha, const int32_t* Y_off, const int64_t* Y_starts,
+                 int32_t ny, const T* Y_vals, T beta, const int32_t* Z_off,
+                 const int64_t* Z_starts, int32_t nz, T* Z_vals, void* stream, const char* fn)
+{
+    if (n < 1 || n > (1 << 30) || nx < 0 || ny < 0 || nz < 0)
+        return fail(DIAGPU_ERR_ARG, "%s: need 1 <= n <= 2^30 and counts >= 0", fn);
+    if (nz == 0) return DIAGPU_OK;
+    if (!Z_off || !Z_starts || !Z_vals) return fail(DIAGPU_ERR_ARG, "%s: Z arrays are NULL", fn);
+    if (nx > 0 && (!X_off || !X_starts || !X_vals)) return fail(DIAGPU_ERR_ARG, "%s: X arrays are NULL", fn);
+    if (ny > 0 && (!Y_off || !Y_starts || !Y_vals)) return fail(DIAGPU_ERR_ARG, "%s: Y arrays are NULL", fn);
+    if (is_zero(alpha)) nx = 0;      // BLAS convention: a zero factor's operand is not read
+    if (is_zero(beta)) ny = 0;
+    const int32_t spans = (int32_t)ceil_div<int64_t>(n, kSpan);
+    int64_t grid = (int64_t)nz * spans;
+    const int64_t cap = (int64_t)cu_count() * 16;
+    if (grid > cap) grid = cap;
+    hipLaunchKernelGGL(k_axpby<T>, dim3((unsigned)grid), dim3(kBlock), 0, as_stream(stream), n,
+                       X_off, X_starts, nx, X_vals, alpha, Y_off, Y_starts, ny, Y_vals, beta,
+                       Z_off, Z_starts, nz, Z_vals, spans);
+    return check_launch(fn);
 }
 
 }  // namespace
@@ -77,24 +115,24 @@ DIAGPU_API int diagpu_dia_axpby_f32(int32_t n, const int32_t* X_off, const int64
                                     const float* Y_vals, float beta, const int32_t* Z_off,
                                     const int64_t* Z_starts, int32_t nz, float* Z_vals, void* stream)
 {
-    using namespace diagpu;
-    const char* fn = "diagpu_dia_axpby_f32";
-    if (n < 1 || n > (1 << 30) || nx < 0 || ny < 0 || nz < 0)
-        return fail(DIAGPU_ERR_ARG, "%s: need 1 <= n <= 2^30 and counts >= 0", fn);
-    if (nz == 0) return DIAGPU_OK;
-    if (!Z_off || !Z_starts || !Z_vals) return fail(DIAGPU_ERR_ARG, "%s: Z arrays are NULL", fn);
-    if (nx > 0 && (!X_off || !X_starts || !X_vals)) return fail(DIAGPU_ERR_ARG, "%s: X arrays are NULL", fn);
-    if (ny > 0 && (!Y_off || !Y_starts || !Y_vals)) return fail(DIAGPU_ERR_ARG, "%s: Y arrays are NULL", fn);
-    if (alpha == 0.0f) nx = 0;      // BLAS convention: a zero factor's operand is not read
-    if (beta == 0.0f) ny = 0;
-    const int32_t spans = (int32_t)ceil_div<int64_t>(n, kSpan);
-    int64_t grid = (int64_t)nz * spans;
-    const int64_t cap = (int64_t)cu_count() * 16;
-    if (grid > cap) grid = cap;
-    hipLaunchKernelGGL(k_axpby, dim3((unsigned)grid), dim3(kBlock), 0, as_stream(stream), n, X_off,
-                       X_starts, nx, X_vals, alpha, Y_off, Y_starts, ny, Y_vals, beta, Z_off,
-                       Z_starts, nz, Z_vals, spans);
-    return check_launch(fn);
+    return diagpu::axpby_launch<float>(n, X_off, X_starts, nx, X_vals, alpha, Y_off, Y_starts, ny,
+                                       Y_vals, beta, Z_off, Z_starts, nz, Z_vals, stream,
+                                       "diagpu_dia_axpby_f32");
+}
+
+DIAGPU_API int diagpu_dia_axpby_c64(int32_t n, const int32_t* X_off, const int64_t* X_starts,
+                                    int32_t nx, const diagpu_complex64* X_vals,
+                                    diagpu_complex64 alpha, const int32_t* Y_off,
+                                    const int64_t* Y_starts, int32_t ny,
+                                    const diagpu_complex64* Y_vals, diagpu_complex64 beta,
+                                    const int32_t* Z_off, const int64_t* Z_starts, int32_t nz,
+                                    diagpu_complex64* Z_vals, void* stream)
+{
+    using diagpu::cf32;
+    return diagpu::axpby_launch<cf32>(
+        n, X_off, X_starts, nx, reinterpret_cast<const cf32*>(X_vals), cf32{alpha.re, alpha.im},
+        Y_off, Y_starts, ny, reinterpret_cast<const cf32*>(Y_vals), cf32{beta.re, beta.im}, Z_off,
+        Z_starts, nz, reinterpret_cast<cf32*>(Z_vals), stream, "diagpu_dia_axpby_c64");
 }
 
 }  // extern "C"

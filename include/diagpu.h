@@ -270,6 +270,36 @@ DIAGPU_API int diagpu_dia_axpby_f32(int32_t n, const int32_t* X_off, const int64
                                     const int64_t* Z_starts, int32_t nz, float* Z_vals,
                                     void* stream);
 
+/* Complex64 variant of diagpu_dia_axpby_f32 with complex factors (a zero
+ * factor, both parts 0, means its operand is not read).  Used by the complex
+ * Taylor chain that builds exp(-i t H); no reference counterpart. */
+DIAGPU_API int diagpu_dia_axpby_c64(int32_t n, const int32_t* X_off, const int64_t* X_starts,
+                                    int32_t nx, const diagpu_complex64* X_vals,
+                                    diagpu_complex64 alpha, const int32_t* Y_off,
+                                    const int64_t* Y_starts, int32_t ny,
+                                    const diagpu_complex64* Y_vals, diagpu_complex64 beta,
+                                    const int32_t* Z_off, const int64_t* Z_starts, int32_t nz,
+                                    diagpu_complex64* Z_vals, void* stream);
+
+/* ======================================================================
+ * HM -> Recon on the device
+ * ====================================================================== */
+
+/* build_recon (spmv/src/dia_reconstruct.cuh:77-107) for a square n x n HM
+ * matrix already on the device (for square matrices the HM layout is the
+ * reference's compact DIA layout): recon_offsets[k] = offsets[ndiag-1-k]
+ * (HM offsets ascending, as the SpGEMM symbolic phase produces them, give the
+ * descending Recon order), recon_values[k * n + c] = the diagonal's element
+ * in column c for c in [max(d,0), max(d,0) + n - |d|), 0 elsewhere.  Lets a
+ * SpGEMM product be applied by the SpMV kernels without a host copy. */
+DIAGPU_API int diagpu_hm_to_recon_f32(int32_t n, const int32_t* offsets, const int64_t* starts,
+                                      int32_t ndiag, const float* values, int32_t* recon_offsets,
+                                      float* recon_values, void* stream);
+DIAGPU_API int diagpu_hm_to_recon_c64(int32_t n, const int32_t* offsets, const int64_t* starts,
+                                      int32_t ndiag, const diagpu_complex64* values,
+                                      int32_t* recon_offsets, diagpu_complex64* recon_values,
+                                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif
