@@ -37,11 +37,20 @@
 // issues all 2K loads straight-line.
 //
 // Edge tiles.  A tile whose rows or columns leave the matrix for some
-// diagonal runs the same ring with per-element loads at clamped (always
-// valid) columns and masked accumulation: no branch around a load, so the
-// loads pipeline like the interior ones.  An edge tile is also dispatched
-// early (odd XCDs walk their row range from the end), since the slowest tile
-// sets the kernel's end.
+// diagonal runs the same ring, still with 16-byte runs, each loaded at its
+// start column clamped into [0, lim - R] (always a valid run), and masked
+// accumulation: no branch around a load, so the loads pipeline like the
+// interior ones.  A lane whose run straddles column 0 or lim finds its
+// in-range elements inside the clamped run, shifted by (start - clamped
+// start), and picks them out with selects; lanes wholly out of range all load
+// the same clamped run (one cache line per wave) and mask every term.  This
+// keeps an edge tile about as fast as an interior one, which matters when
+// the offset spread is a sizeable part of n (a propagator with hundreds of
+// diagonals spread over +-10^5 rows has a fifth of its tiles at the edges,
+// all on the XCDs that own the first and last rows).  Only a matrix
+// narrower than one run (lim < R) falls back to per-element loads at
+// clamped columns.  An edge tile is also dispatched early (odd XCDs walk
+// their row range from the end).
 //
 // XCD awareness: workgroup b runs on XCD b mod 8; tiles are remapped so each
 // XCD owns one contiguous eighth of the rows.  x[c] is used by rows c - d_k
@@ -71,7 +80,7 @@ template <typename TV, typename TX> struct Shape {
     static constexpr int R = (int)(16 / sizeof(TV));
     static constexpr bool wide_x = R * sizeof(TX) > 16;   // 32-byte x runs
     static constexpr int W = wide_x ? 4 : 6;              // interior ring
-    static constexpr int WE = wide_x ? 2 : 5;             // edge ring
+    static constexpr int WR = wide_x ? 2 : 4;             // edge ring
     static constexpr int TILE = kBlock * R;
 };
 
@@ -105,16 +114,19 @@ inline __device__ void wave_minmax(int v, int& lo, int& hi)
     hi = __builtin_amdgcn_readfirstlane(b);
 }
 
+// How a group's loads treat columns outside [0, lim).
+enum EdgeMode {
+    kInterior = 0,   // the whole tile is in range: plain 16-byte runs
+    kEdgeRun = 1,    // 16-byte runs at clamped starts, shifted and masked
+};
+
 // One group of gn <= 64 diagonals (offsets in `ov`, lane l = d_{g0+l};
 // values `vg` = Recon row g0) accumulated into `acc` for the lane's R rows
 // starting at row `r`.  W diagonals' loads in flight; every index is clamped
 // to the group so all loads are valid, and the slots past the group are
-// masked.
-//
-// EDGE = false: the whole tile is in range (rows < `rows`, every column in
-// [0, lim)); 16-byte vector loads.  EDGE = true: per-element loads at columns
-// clamped into [0, lim), terms whose column is outside masked.
-template <typename TV, typename TX, int W, bool EDGE>
+// masked.  kEdgeRun needs lim >= R and masks every term whose column is
+// outside [0, lim).
+template <typename TV, typename TX, int W, int MODE>
 __device__ __forceinline__ void ring_group(int64_t r, int64_t cols, int64_t lim, int gn, int ov,
                                            const TV* __restrict__ vg, const TX* __restrict__ x,
                                            Run<TX, Shape<TV, TX>::R>& acc)
@@ -122,37 +134,46 @@ __device__ __forceinline__ void ring_group(int64_t r, int64_t cols, int64_t lim,
     constexpr int R = Shape<TV, TX>::R;
     Run<TV, R> a[W];
     Run<TX, R> b[W];
-    // EDGE: the lane's first column for the slot's diagonal, clamped to
-    // [-R, lim] (a column outside that range is as out of range as its clamp)
-    int32_t c0[W];
-    (void)c0;
+    // a run start clamped to a valid run, [0, lim - R] (kEdgeRun)
+    auto clamp_run = [&](int64_t c) -> int64_t {
+        const int64_t hi = lim - R;
+        return c < 0 ? 0 : (c > hi ? hi : c);
+    };
     auto issue = [&](int j, int k) {
         const int d = __builtin_amdgcn_readlane(ov, k);
-        if constexpr (!EDGE) {
-            a[j] = load_run<TV, R, true>(vg + (int64_t)k * cols + r + d);
+        const TV* vk = vg + (int64_t)k * cols;
+        if constexpr (MODE == kInterior) {
+            a[j] = load_run<TV, R, true>(vk + r + d);
             b[j] = load_run<TX, R, false>(x + r + d);
         } else {
-            const int64_t c = r + d;
-            c0[j] = (int32_t)(c < -R ? -R : (c > lim ? lim : c));
-            const TV* vk = vg + (int64_t)k * cols;
-#pragma unroll
-            for (int e = 0; e < R; ++e) {
-                int64_t cc = c + e;
-                cc = cc < 0 ? 0 : (cc >= lim ? lim - 1 : cc);   // always a valid address
-                a[j].v[e] = load_elem<TV, true>(vk + (uint32_t)cc);
-                b[j].v[e] = load_elem<TX, false>(x + (uint32_t)cc);
-            }
+            const uint32_t cc = (uint32_t)clamp_run(r + d);
+            a[j] = load_run<TV, R, true>(vk + cc);
+            b[j] = load_run<TX, R, false>(x + cc);
         }
     };
-    auto consume = [&](int j, bool on) {
+    // slot j holds diagonal k (k uniform); `on` = the slot is part of the group
+    auto consume = [&](int j, int k, bool on) {
+        if constexpr (MODE == kInterior) {
 #pragma unroll
-        for (int e = 0; e < R; ++e) {
-            bool ok = on;
-            if constexpr (EDGE) {
-                const int64_t c = (int64_t)c0[j] + e;
-                ok = ok && c >= 0 && c < lim;
+            for (int e = 0; e < R; ++e)
+                acc.v[e] = sel(on, mad(acc.v[e], a[j].v[e], b[j].v[e]), acc.v[e]);
+        } else {
+            const int64_t c = r + __builtin_amdgcn_readlane(ov, k);
+            // element e of the run sits at index e + s of what was loaded
+            const int s = (int)(c - clamp_run(c));
+#pragma unroll
+            for (int e = 0; e < R; ++e) {
+                const bool ok = on && (uint64_t)(c + e) < (uint64_t)lim;
+                TV av = a[j].v[0];
+                TX bv = b[j].v[0];
+#pragma unroll
+                for (int i = 1; i < R; ++i) {
+                    const bool m = e + s == i;
+                    av = sel(m, a[j].v[i], av);
+                    bv = sel(m, b[j].v[i], bv);
+                }
+                acc.v[e] = sel(ok, mad(acc.v[e], av, bv), acc.v[e]);
             }
-            acc.v[e] = sel(ok, mad(acc.v[e], a[j].v[e], b[j].v[e]), acc.v[e]);
         }
     };
 
@@ -163,7 +184,7 @@ __device__ __forceinline__ void ring_group(int64_t r, int64_t cols, int64_t lim,
     while (k0 + 2 * W <= gn) {   // every refill of this round is in range
 #pragma unroll
         for (int j = 0; j < W; ++j) {
-            consume(j, true);
+            consume(j, k0 + j, true);
             __builtin_amdgcn_sched_barrier(0);
             issue(j, k0 + W + j);
             __builtin_amdgcn_sched_barrier(0);
@@ -174,14 +195,28 @@ __device__ __forceinline__ void ring_group(int64_t r, int64_t cols, int64_t lim,
     // copies); refills are clamped the same way.
 #pragma unroll
     for (int j = 0; j < W; ++j) {
-        consume(j, k0 + j < gn);
+        const int kc = k0 + j;
+        consume(j, kc < gn ? kc : gn - 1, kc < gn);
         __builtin_amdgcn_sched_barrier(0);
         const int kn = k0 + W + j;
         issue(j, kn < gn ? kn : gn - 1);
         __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int j = 0; j < W - 1; ++j) consume(j, k0 + W + j < gn);
+    for (int j = 0; j < W - 1; ++j) {
+        const int kc = k0 + W + j;
+        consume(j, kc < gn ? kc : gn - 1, kc < gn);
+    }
+}
+
+// A non-interior tile (lim >= R: the host sends narrower matrices to
+// spmv_narrow_kernel).
+template <typename TV, typename TX>
+__device__ __forceinline__ void edge_group(int64_t r, int64_t cols, int64_t lim, int gn, int ov,
+                                           const TV* __restrict__ vg, const TX* __restrict__ x,
+                                           Run<TX, Shape<TV, TX>::R>& acc)
+{
+    ring_group<TV, TX, Shape<TV, TX>::WR, kEdgeRun>(r, cols, lim, gn, ov, vg, x, acc);
 }
 
 template <typename TX, int R>
@@ -259,18 +294,18 @@ __global__ __launch_bounds__(kBlock) void spmv_ring_kernel(
     for (int e = 0; e < R; ++e) acc.v[e] = zero_of<TX>();
     if constexpr (!MULTI) {
         if (interior)
-            ring_group<TV, TX, S::W, false>(r, cols, lim, K, ov0, vals, x, acc);
+            ring_group<TV, TX, S::W, kInterior>(r, cols, lim, K, ov0, vals, x, acc);
         else
-            ring_group<TV, TX, S::WE, true>(r, cols, lim, K, ov0, vals, x, acc);
+            edge_group<TV, TX>(r, cols, lim, K, ov0, vals, x, acc);
     } else {
         for (int g0 = 0; g0 < K; g0 += 64) {
             const int gn = (K - g0) < 64 ? (K - g0) : 64;
             const int ov = g0 == 0 ? ov0 : offs[g0 + (lane < gn ? lane : gn - 1)];
             const TV* vg = vals + (int64_t)g0 * cols;
             if (interior)
-                ring_group<TV, TX, S::W, false>(r, cols, lim, gn, ov, vg, x, acc);
+                ring_group<TV, TX, S::W, kInterior>(r, cols, lim, gn, ov, vg, x, acc);
             else
-                ring_group<TV, TX, S::WE, true>(r, cols, lim, gn, ov, vg, x, acc);
+                edge_group<TV, TX>(r, cols, lim, gn, ov, vg, x, acc);
         }
     }
     store_rows<TX, R>(y, r, rows, acc, interior);
@@ -322,11 +357,39 @@ __global__ __launch_bounds__(kBlock) void spmv_short_kernel(
         } else {
             const int lane = (int)threadIdx.x & 63;
             const int ov = offs[lane < KF ? lane : KF - 1];
-            ring_group<TV, TX, S::WE, true>(r, cols, lim, KF, ov, vals, x, acc);
+            edge_group<TV, TX>(r, cols, lim, KF, ov, vals, x, acc);
         }
     }
     store_rows<TX, R>(y, r, rows, acc, interior);
     if constexpr (DOT) dot_epilogue<TX, R>(acc, x, r, rows, interior, tile, tiles, da);
+}
+
+// lim < R (fewer than R columns of x in range): no 16-byte run fits, so
+// every term is a per-element load behind its bounds check.  Same tiles and
+// epilogues as the other kernels.
+template <typename TV, typename TX, bool DOT>
+__global__ __launch_bounds__(kBlock) void spmv_narrow_kernel(
+    int32_t rows, int32_t cols, int64_t lim, int32_t K, const int32_t* __restrict__ offs,
+    const TV* __restrict__ vals, const TX* __restrict__ x, TX* __restrict__ y, int32_t tiles,
+    int32_t per_xcd, DotArgs da)
+{
+    typedef Shape<TV, TX> S;
+    constexpr int R = S::R;
+    const int tile = tile_of_block(per_xcd);
+    if (tile >= tiles) return;
+    const int64_t r = (int64_t)tile * S::TILE + (int64_t)threadIdx.x * R;
+    Run<TX, R> acc;
+#pragma unroll
+    for (int e = 0; e < R; ++e) acc.v[e] = zero_of<TX>();
+    for (int k = 0; k < K; ++k) {
+        const int64_t c = r + offs[k];
+        const TV* vk = vals + (int64_t)k * cols;
+#pragma unroll
+        for (int e = 0; e < R; ++e)
+            if ((uint64_t)(c + e) < (uint64_t)lim) acc.v[e] = mad(acc.v[e], vk[c + e], x[c + e]);
+    }
+    store_rows<TX, R>(y, r, rows, acc, false);
+    if constexpr (DOT) dot_epilogue<TX, R>(acc, x, r, rows, false, tile, tiles, da);
 }
 
 template <typename TV, typename TX>
@@ -334,8 +397,9 @@ using SpmvKernel = void (*)(int32_t, int32_t, int64_t, int32_t, const int32_t*, 
                             const TX*, TX*, int32_t, int32_t, DotArgs);
 
 template <typename TV, typename TX, bool DOT>
-SpmvKernel<TV, TX> pick_kernel(int K)
+SpmvKernel<TV, TX> pick_kernel(int K, int64_t lim)
 {
+    if (K > 0 && lim < Shape<TV, TX>::R) return spmv_narrow_kernel<TV, TX, DOT>;
     switch (K) {
     case 0: return spmv_short_kernel<TV, TX, 0, DOT>;
     case 1: return spmv_short_kernel<TV, TX, 1, DOT>;
@@ -382,7 +446,7 @@ int spmv_run(int32_t rows, int32_t cols, int32_t num_diags, const int32_t* offs,
     const int32_t tiles = spmv_tiles<TV, TX>(rows);
     const int32_t per_xcd = ceil_div<int32_t>(tiles, kNumXcd);
     const DotArgs da = dot ? *dot : DotArgs{nullptr, nullptr};
-    hipLaunchKernelGGL((dot ? pick_kernel<TV, TX, true>(K) : pick_kernel<TV, TX, false>(K)),
+    hipLaunchKernelGGL((dot ? pick_kernel<TV, TX, true>(K, lim) : pick_kernel<TV, TX, false>(K, lim)),
                        dim3(per_xcd * kNumXcd), dim3(kBlock), 0, as_stream(stream), rows, cols,
                        lim, K, offs, vals, x, y, tiles, per_xcd, da);
     const int st = check_launch(name);

@@ -56,6 +56,24 @@ def test_complex_spmv_every_path(dev, oracle, K, mat):
         assert (err <= 1e-5 * absum + 1e-30).all(), float(err.max())
 
 
+@pytest.mark.parametrize("mat,cols", [("c64", 1), ("f32", 1), ("f32", 3)])
+def test_complex_spmv_narrow(dev, oracle, mat, cols):
+    """min(cols, x_size) below one 16-byte run of matrix elements: the
+    per-element kernel for complex and real-matrix/complex-state operands."""
+    rng = np.random.default_rng(cols + 10 * (mat == "f32"))
+    rows = 2049
+    offs = np.array([-1500, -2, -1, 0, 1, 2, 700], np.int32)
+    vals = (_cx(rng, len(offs) * cols) if mat == "c64"
+            else rng.uniform(-1, 1, len(offs) * cols).astype(np.float32))
+    x = _cx(rng, cols)
+    y = spmv_recon(torch.as_tensor(offs, device=dev), torch.as_tensor(vals, device=dev),
+                   rows, cols, torch.as_tensor(x, device=dev)).cpu().numpy()
+    want, absum = oracle.spmv_recon_complex_ref(rows, cols, offs, vals, x)
+    for part in (np.real, np.imag):
+        err = np.abs(part(y).astype(np.float64) - part(want))
+        assert (err <= 1e-5 * absum + 1e-30).all(), float(err.max())
+
+
 @pytest.mark.parametrize("K", [2, 5, 9, 40, 70])
 def test_real_matrix_complex_state_equals_real_kernel_per_part(dev, K):
     """H (real) applied to x = a + ib is H a + i H b with the real kernel's
@@ -166,6 +184,24 @@ def test_propagator_breakdown_is_exact(dev):
     want = np.exp(-1j * t * d.astype(np.float64)) * psi0
     got = res.psi.cpu().numpy()
     assert np.abs(got - want).max() <= 2e-6 * np.abs(psi0).max()
+
+
+@pytest.mark.parametrize("n", [1, 2, 3])
+@pytest.mark.parametrize("complex_values", [True, False])
+def test_propagator_tiny_n(dev, n, complex_values):
+    """n below one 16-byte run (the per-element SpMV with its dot epilogue):
+    Lanczos reaches the whole space in <= n steps and is exact there."""
+    import scipy.linalg as sl
+    rng = np.random.default_rng(20 + n + 5 * complex_values)
+    offs, vals, H = _hermitian_band(rng, n, list(range(n)), complex_values)
+    psi0 = _cx(rng, n)
+    t = 0.9
+    res = expm_krylov(torch.as_tensor(offs, device=dev), torch.as_tensor(vals.reshape(-1), device=dev),
+                      n, torch.as_tensor(psi0, device=dev), t, 8)
+    want = sl.expm(-1j * t * H) @ psi0.astype(np.complex128)
+    got = res.psi.cpu().numpy().astype(np.complex128)
+    nrm = np.linalg.norm(psi0.astype(np.complex128))
+    assert res.steps <= n and np.linalg.norm(got - want) <= 1e-5 * nrm
 
 
 def test_propagator_zero_time_and_zero_state(dev):

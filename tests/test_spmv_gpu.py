@@ -205,3 +205,24 @@ def test_every_kernel_variant(dev, oracle, K, dtype):
     y64, absum = oracle.spmv_recon_ref64(rows, cols, offs, np.nan_to_num(vals).reshape(-1), x)
     assert not np.isnan(y).any()
     check_bound(y, y64, absum, TOL32 if dtype == np.float32 else TOL64)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("cols,xlen", [(1, 1), (2, 2), (3, 3), (3000, 1), (3000, 3)])
+def test_narrow_matrix(dev, oracle, dtype, cols, xlen):
+    """Fewer columns of x in range than one 16-byte run holds (min(cols,
+    x_size) < 16 / element size): the per-element kernel, any K, with rows
+    far beyond the columns so most rows see no in-range term.  (f64 with
+    two columns is the boundary min(cols, x_size) == 16 / element size of
+    the clamped-run kernels instead.)"""
+    R = 16 // np.dtype(dtype).itemsize
+    rng = np.random.default_rng(cols * 7 + xlen + R)
+    rows = 3001
+    for offs in ([0], [2, 0, -1], [-2999, -5, -1, 0, 1, 2, 3, 2999], list(range(-40, 30))):
+        r_off = np.array(offs, np.int32)
+        r_val = rng.uniform(-1, 1, size=len(offs) * cols).astype(dtype)
+        x = rng.standard_normal(xlen).astype(dtype)
+        y = gpu_spmv(dev, r_off, r_val, rows, cols, x, y_init=np.full(rows, np.nan, dtype))
+        y64, absum = oracle.spmv_recon_ref64(rows, cols, r_off, r_val, x)
+        assert not np.isnan(y).any()
+        check_bound(y, y64, absum, TOL32 if dtype == np.float32 else TOL64)
