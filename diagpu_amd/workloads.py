@@ -177,8 +177,30 @@ def hm_stencil7(nx: int, ny: int, nz: int, device="cuda") -> HM:
     return hm_from_values(n, offs, torch.cat(parts), device)
 
 
+def recon_to_hm(R: Recon) -> HM:
+    """HM compact DIA of a square Recon matrix (the inverse of build_recon,
+    spmv/src/dia_reconstruct.cuh:77-107): diagonal d, ascending, holds Recon
+    row k's columns [max(d, 0), max(d, 0) + n - |d|).  Offsets must be
+    distinct and inside (-n, n)."""
+    if R.rows != R.cols:
+        raise ValueError("recon_to_hm needs a square matrix")
+    n = R.rows
+    offs = R.offsets.cpu().tolist()
+    if len(set(offs)) != len(offs) or any(abs(d) >= n for d in offs):
+        raise ValueError("offsets must be distinct and inside (-n, n)")
+    order = sorted(range(len(offs)), key=lambda k: offs[k])
+    parts = [R.values[k * n + max(offs[k], 0): k * n + max(offs[k], 0) + n - abs(offs[k])]
+             for k in order]
+    vals = torch.cat(parts).contiguous() if parts else R.values.new_empty(0)
+    return hm_from_values(n, [offs[k] for k in order], vals, R.values.device)
+
+
 def spgemm_config(cfg: int, seed: int = 0, device="cuda") -> tuple[HM, HM]:
-    """BASELINE.json SpGEMM configs 4 and 5."""
+    """BASELINE.json SpGEMM configs 4 and 5; for configs 1-3 (SpMV matrices)
+    the product H H of that config's matrix."""
+    if cfg in (1, 2, 3):
+        H = recon_to_hm(spmv_config(cfg, seed, device))
+        return H, H
     if cfg == 4:
         n = 1 << 20
         A = hm_random(n, range(-4, 5), seed, device)

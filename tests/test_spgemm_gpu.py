@@ -245,3 +245,34 @@ def test_capacity_and_empty(dev):
     F = _hm_dev(dev, n, [60, 63])
     p3 = SpgemmPlan(F, _hm_dev(dev, n, [10, 20]))
     assert p3.info.c_ndiag == 0
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3])
+def test_square_of_spmv_configs(dev, oracle, cfg):
+    """H H for the SpMV configs' matrices (full size): plan exact; values to
+    the bound on every C diagonal (configs 1, 2) or on a sample of them
+    (config 3, about 1400 C diagonals of 4.2M values), and all of C through
+    C 1 = H (H 1)."""
+    A, B = workloads.spgemm_config(cfg, seed=cfg, device=dev)
+    plan = SpgemmPlan(A, B)
+    c_off, c_len, c_st, nnz, ptr, pairs = check_plan(oracle, plan, A, B)
+    Cv = plan.multiply(A.values, B.values)
+    torch.cuda.synchronize()
+    Av, Bv = A.values.cpu().numpy(), B.values.cpu().numpy()
+    if cfg < 3:
+        want, ab = oracle.spgemm_pairs_f64(Av, Bv, c_len, c_st, ptr, pairs, 0, len(c_off))
+        check_values(Cv.cpu().numpy(), want, ab)
+        return
+    rng = np.random.default_rng(3)
+    counts = np.diff(ptr)
+    ks = sorted({0, len(c_off) - 1, int(np.argmax(counts)), *rng.choice(len(c_off), 24).tolist()})
+    for k in ks:
+        want, ab = oracle.spgemm_pairs_f64(Av, Bv, c_len, c_st, ptr, pairs, k, k + 1)
+        got = Cv[int(c_st[k]):int(c_st[k]) + int(c_len[k])].cpu().numpy()
+        check_values(got, want, ab)
+    n = A.n
+    rs = _row_sums_gpu(plan, Cv, n)
+    b1, b1a = _hm_matvec(n, host(B), np.ones(n))
+    ab1, _ = _hm_matvec(n, host(A), b1)
+    _, bound = _hm_matvec(n, host(A), b1a)
+    assert np.all(np.abs(rs - ab1) <= TOL * bound + 1e-300)
