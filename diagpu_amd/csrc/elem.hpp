@@ -67,24 +67,31 @@ __device__ __forceinline__ T load_elem(const T* p)
     return r;
 }
 
-// A lane's run of R consecutive elements (16 or 32 bytes), moved as 16-byte
-// vectors.
+// A lane's run of R consecutive elements (8, 16 or 32 bytes), moved as one
+// 8-byte or whole 16-byte vectors.
 template <typename T, int R> struct Run { T v[R]; };
 
 typedef float f4dw __attribute__((ext_vector_type(4), aligned(4)));
+typedef float f2dw __attribute__((ext_vector_type(2), aligned(4)));
 
 template <typename T, int R, bool NT>
 __device__ __forceinline__ Run<T, R> load_run(const T* p)
 {
-    static_assert((R * sizeof(T)) % 16 == 0, "runs are whole 16-byte vectors");
-    constexpr int NQ = (int)(R * sizeof(T) / 16);
-    f4dw q[NQ];
-#pragma unroll
-    for (int i = 0; i < NQ; ++i)
-        q[i] = NT ? __builtin_nontemporal_load(reinterpret_cast<const f4dw*>(p) + i)
-                  : reinterpret_cast<const f4dw*>(p)[i];
     Run<T, R> r;
-    __builtin_memcpy(&r, q, sizeof(r));
+    if constexpr (R * sizeof(T) == 8) {
+        const f2dw q = NT ? __builtin_nontemporal_load(reinterpret_cast<const f2dw*>(p))
+                          : *reinterpret_cast<const f2dw*>(p);
+        __builtin_memcpy(&r, &q, sizeof(r));
+    } else {
+        static_assert((R * sizeof(T)) % 16 == 0, "runs are 8 bytes or whole 16-byte vectors");
+        constexpr int NQ = (int)(R * sizeof(T) / 16);
+        f4dw q[NQ];
+#pragma unroll
+        for (int i = 0; i < NQ; ++i)
+            q[i] = NT ? __builtin_nontemporal_load(reinterpret_cast<const f4dw*>(p) + i)
+                      : reinterpret_cast<const f4dw*>(p)[i];
+        __builtin_memcpy(&r, q, sizeof(r));
+    }
     return r;
 }
 

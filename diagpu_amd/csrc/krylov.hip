@@ -213,7 +213,13 @@ struct Layout {
 Layout layout(int64_t n, int m)
 {
     Layout L;
-    const int64_t tiles = (n + 511) / 512;   // >= every launch's tile count (R >= 2)
+    // one partial per workgroup of the largest launch: either SpMV (real or
+    // complex matrix) or the vector kernels
+    int64_t tiles = spmv_tiles<float, cf32>((int32_t)n);
+    const int64_t tc = spmv_tiles<cf32, cf32>((int32_t)n);
+    const int64_t tv = (n + kVTile - 1) / kVTile;
+    tiles = tc > tiles ? tc : tiles;
+    tiles = tv > tiles ? tv : tiles;
     size_t off = 0;
     L.vecs = off;
     off += align256((size_t)m * (size_t)n * sizeof(cf32));

@@ -12,9 +12,10 @@
 // Element types.  One kernel family serves real fp32 and fp64, complex64
 // matrices with complex64 vectors, and real fp32 matrices with complex64
 // vectors (a real Hamiltonian applied to a complex state: the matrix is read
-// once for both parts of x).  A lane owns R rows with R * sizeof(matrix
-// element) = 16 bytes; its x run and y run are R vector elements (16 or 32
-// bytes).
+// once for both parts of x).  A lane owns R rows, R times the wider of the
+// two elements being 16 bytes: its x and y runs are 16 bytes, its value run
+// 16 bytes (8 for a real matrix with complex vectors, where 32-byte x runs
+// would leave every 16-byte x load half coalesced).
 //
 // Mapping.  A workgroup of 256 lanes owns a tile of 256 x R consecutive rows.
 // For diagonal k the lane needs Recon[k][r+d_k ..] and x[r+d_k ..]: runs at
@@ -77,10 +78,12 @@ constexpr int kShortMax = 5;   // K <= kShortMax: straight-line kernel
 // Per (matrix element, vector element) pair: rows per lane and ring depths,
 // chosen so the kernels stay within 64 VGPRs (8 waves per SIMD).
 template <typename TV, typename TX> struct Shape {
-    static constexpr int R = (int)(16 / sizeof(TV));
-    static constexpr bool wide_x = R * sizeof(TX) > 16;   // 32-byte x runs
-    static constexpr int W = wide_x ? 4 : 6;              // interior ring
-    static constexpr int WR = wide_x ? 2 : 4;             // edge ring
+    // 16 bytes of the wider of the two elements: a real matrix applied to a
+    // complex vector takes 2 rows per lane (8-byte value runs), so that every
+    // x load and y store is a fully coalesced 16-byte run.
+    static constexpr int R = (int)(16 / (sizeof(TV) > sizeof(TX) ? sizeof(TV) : sizeof(TX)));
+    static constexpr int W = 6;    // interior ring
+    static constexpr int WR = 4;   // edge ring
     static constexpr int TILE = kBlock * R;
 };
 
