@@ -2,7 +2,7 @@
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--extras | --no-extras]
 
-Prints ONE JSON line.  The headline is BASELINE.json's config 2: DIA SpMV of
+Prints ONE JSON line.  The headline is benchmark config 2: DIA SpMV of
 the 2-D 5-point Poisson stencil on a 2048 x 2048 grid (n = 4,194,304, fp32);
 one step = one SpMV y = H x.  `value` is achieved algorithmic HBM bandwidth
 
@@ -11,7 +11,7 @@ one step = one SpMV y = H x.  `value` is achieved algorithmic HBM bandwidth
 divided by the step time measured with HIP events on the launch stream over
 exactly K steps.  Each step uses the next of `--sets` independent buffer sets
 (>= 512 MiB in total, twice the 256 MiB MALL), so no step finds its operands
-in the Infinity Cache.  The "extras" object times the other BASELINE configs
+in the Infinity Cache.  The "extras" object times the other benchmark configs
 the same way (SpMV configs 1-3, SpGEMM configs 4-5 when built).
 """
 from __future__ import annotations

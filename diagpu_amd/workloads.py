@@ -1,4 +1,4 @@
-"""Seeded synthetic inputs of the BASELINE.json configurations, built on the
+"""Seeded synthetic inputs of the five benchmark configurations, built on the
 device with torch (plain tensor fills: they are inputs, not the product).
 
 Recon matrices follow spmv/src/dia_reconstruct.cuh:9-17 (column-indexed,
@@ -71,7 +71,7 @@ def recon_random(n: int, offsets, seed: int, device="cuda", dtype=torch.float32,
 
 
 def recon_poisson5(side: int, seed: int, device="cuda", dtype=torch.float32) -> Recon:
-    """2-D 5-point Poisson stencil on a side x side grid:
+    """2-D 5-point Poisson stencil on a side x side grid (benchmark config 2):
     offsets {side, 1, 0, -1, -side}, diagonal 4, off-diagonals -1, the +-1
     entries that wrap across a grid row zeroed, x ~ N(0, 1)."""
     n = side * side
@@ -98,7 +98,8 @@ def random_band_offsets(count: int, half_width: int, seed: int) -> list[int]:
 
 
 def spmv_config(cfg: int, seed: int = 0, device="cuda", dtype=torch.float32) -> Recon:
-    """BASELINE.json SpMV configs 1-3 (1-based numbering of BASELINE.md)."""
+    """Benchmark SpMV configs 1-3: the tridiagonal n = 2^20 band, the
+    2048 x 2048 Poisson stencil, and the random 64-diagonal band."""
     if cfg == 1:
         return recon_random(1 << 20, [-1, 0, 1], seed, device, dtype, x_dist="uniform")
     if cfg == 2:
@@ -196,7 +197,7 @@ def recon_to_hm(R: Recon) -> HM:
 
 
 def spgemm_config(cfg: int, seed: int = 0, device="cuda") -> tuple[HM, HM]:
-    """BASELINE.json SpGEMM configs 4 and 5; for configs 1-3 (SpMV matrices)
+    """Benchmark SpGEMM configs 4 and 5; for configs 1-3 (SpMV matrices)
     the product H H of that config's matrix."""
     if cfg in (1, 2, 3):
         H = recon_to_hm(spmv_config(cfg, seed, device))

@@ -99,7 +99,7 @@ DIAGPU_API int diagpu_spmv_recon_f32(const diagpu_recon_view_f32* R, const float
                                      int64_t x_size, float* y, void* stream);
 
 /* fp64 variant of diagpu_spmv_recon_f32 (no reference counterpart: the
- * reference is fp32/TF32 only; BASELINE config 2 asks for fp64). */
+ * reference is fp32/TF32 only; benchmark config 2 asks for fp64). */
 DIAGPU_API int diagpu_spmv_recon_f64(const diagpu_recon_view_f64* R, const double* x,
                                      int64_t x_size, double* y, void* stream);
 

@@ -58,8 +58,10 @@ def test_complex_spmv_every_path(dev, oracle, K, mat):
 
 @pytest.mark.parametrize("mat,cols", [("c64", 1), ("f32", 1), ("f32", 3)])
 def test_complex_spmv_narrow(dev, oracle, mat, cols):
-    """min(cols, x_size) below one 16-byte run of matrix elements: the
-    per-element kernel for complex and real-matrix/complex-state operands."""
+    """One column: below one run (2 rows per lane for both pairs), so the
+    per-element kernel for complex and real-matrix/complex-state operands.
+    Three columns: just above one run, so every tile is an edge tile of the
+    clamped-run ring with lim barely past R."""
     rng = np.random.default_rng(cols + 10 * (mat == "f32"))
     rows = 2049
     offs = np.array([-1500, -2, -1, 0, 1, 2, 700], np.int32)
@@ -90,7 +92,7 @@ def test_real_matrix_complex_state_equals_real_kernel_per_part(dev, K):
 
 
 def test_complex_spmv_full_size_poisson(dev, oracle):
-    """BASELINE config 2's stencil with complex values (i times the real
+    """Benchmark config 2's stencil with complex values (i times the real
     stencil) and a complex state: y = i H x, checked over every row."""
     R = workloads.spmv_config(2, seed=3, device=dev, dtype=torch.float32)
     cv = (1j * R.values.to(torch.complex64)).contiguous()
