@@ -17,7 +17,9 @@
 // (SpMV+dot, update+norm), z is written into u_{j+1}'s slot and updated in
 // place, and every scalar stays on the device.  Each reduction is one fp64
 // partial per workgroup plus a one-workgroup fixed-order sum (reduce.hpp,
-// sum_partials): deterministic, and free of device-scope fences.
+// sum_partials): deterministic, and free of device-scope fences.  q_j is
+// not needed before step j+1's update, so its sum shares one launch with
+// step j+1's d sum (sum_partials2): three launches per step.
 //
 // After m steps the host reads alpha and beta (the only synchronisation),
 // forms T_m = tridiag(beta, alpha, beta), diagonalises it (cyclic Jacobi,
@@ -207,7 +209,7 @@ void jacobi_eig(int m, std::vector<double>& a, std::vector<double>& Q, std::vect
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 struct Layout {
-    size_t vecs, partials, d, q, total;
+    size_t vecs, pd, pq, d, q, total;   // pd: SpMV dot partials, pq: norm partials
 };
 
 Layout layout(int64_t n, int m)
@@ -223,7 +225,9 @@ Layout layout(int64_t n, int m)
     size_t off = 0;
     L.vecs = off;
     off += align256((size_t)m * (size_t)n * sizeof(cf32));
-    L.partials = off;
+    L.pd = off;
+    off += align256((size_t)tiles * sizeof(double));
+    L.pq = off;
     off += align256((size_t)tiles * sizeof(double));
     L.d = off;
     off += align256((size_t)m * sizeof(double));
@@ -254,7 +258,8 @@ int expm_krylov(int32_t rows, int32_t cols, int32_t K, const int32_t* offs, cons
                     L.total);
     char* ws = static_cast<char*>(workspace);
     cf32* vecs = reinterpret_cast<cf32*>(ws + L.vecs);
-    double* partials = reinterpret_cast<double*>(ws + L.partials);
+    double* pd = reinterpret_cast<double*>(ws + L.pd);
+    double* pq = reinterpret_cast<double*>(ws + L.pq);
     double* d = reinterpret_cast<double*>(ws + L.d);
     double* q = reinterpret_cast<double*>(ws + L.q);
     hipStream_t s = as_stream(stream);
@@ -264,22 +269,26 @@ int expm_krylov(int32_t rows, int32_t cols, int32_t K, const int32_t* offs, cons
     const int vper = (vtiles + kNumXcd - 1) / kNumXcd;
     const dim3 vgrid((unsigned)(vper * kNumXcd));
 
-    hipLaunchKernelGGL(k_norm2, vgrid, dim3(kVB), 0, s, psi0, n, vtiles, vper, partials);
+    const int stiles = spmv_tiles<TV, cf32>(rows);
+
+    // pq holds the partials of q[j-1] when step j starts (||psi_0||^2 for j = 1)
+    hipLaunchKernelGGL(k_norm2, vgrid, dim3(kVB), 0, s, psi0, n, vtiles, vper, pq);
     int st = check_launch(fn);
-    if (!st) st = sum_partials(partials, vtiles, q, stream);
     if (st) return st;
     for (int j = 1; j <= m; ++j) {
         const cf32* uj = j == 1 ? psi0 : slot(j);
         const cf32* ujm1 = j == 1 ? nullptr : (j == 2 ? psi0 : slot(j - 1));
-        DotArgs da{partials, d + (j - 1)};
+        DotArgs da{pd, nullptr};
         st = spmv_run<TV, cf32>(rows, cols, K, offs, vals, uj, n, slot(j + 1), &da, stream, fn);
+        if (!st) st = sum_partials2(pd, stiles, d + (j - 1), pq, vtiles, q + (j - 1), stream);
         if (st) return st;
         hipLaunchKernelGGL(k_lanczos_update, vgrid, dim3(kVB), 0, s, slot(j + 1), uj, ujm1, n, j,
-                           d, q, vtiles, vper, partials);
+                           d, q, vtiles, vper, pq);
         st = check_launch(fn);
-        if (!st) st = sum_partials(partials, vtiles, q + j, stream);
         if (st) return st;
     }
+    st = sum_partials(pq, vtiles, q + m, stream);
+    if (st) return st;
     std::vector<double> hd(m), hq(m + 1);
     st = check_hip(hipMemcpyAsync(hd.data(), d, sizeof(double) * m, hipMemcpyDeviceToHost, s), fn);
     if (!st)

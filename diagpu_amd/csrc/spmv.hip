@@ -442,7 +442,7 @@ int spmv_run(int32_t rows, int32_t cols, int32_t num_diags, const int32_t* offs,
         if (cols > 0 && !vals) return fail(DIAGPU_ERR_ARG, "%s: values is NULL", name);
         if (lim > 0 && !x) return fail(DIAGPU_ERR_ARG, "%s: x is NULL", name);
     }
-    if (dot && (x_size < rows || !x || !dot->partials || !dot->out))
+    if (dot && (x_size < rows || !x || !dot->partials))
         return fail(DIAGPU_ERR_ARG, "%s: the dot epilogue needs x_size >= rows and its buffers",
                     name);
     if (lim == 0) K = 0;   // no column in range: y = 0 without touching values or x
@@ -453,7 +453,7 @@ int spmv_run(int32_t rows, int32_t cols, int32_t num_diags, const int32_t* offs,
                        dim3(per_xcd * kNumXcd), dim3(kBlock), 0, as_stream(stream), rows, cols,
                        lim, K, offs, vals, x, y, tiles, per_xcd, da);
     const int st = check_launch(name);
-    if (st || !dot) return st;
+    if (st || !dot || !dot->out) return st;
     return sum_partials(dot->partials, tiles, dot->out, stream);
 }
 
@@ -461,12 +461,20 @@ namespace {
 constexpr int kSumBlock = 1024;
 constexpr int kSumUnroll = 8;
 
-// Lane l adds partials l, l + 1024, l + 2048, ... in that order (loads of a
-// batch of 8 issued before their adds), then a fixed tree: deterministic, and
-// up to 8192 partials cost one memory round trip.
-__global__ __launch_bounds__(kSumBlock) void k_sum_partials(const double* __restrict__ partials,
-                                                            int32_t n, double* __restrict__ out)
+struct SumJob {
+    const double* partials;
+    int32_t n;
+    double* out;
+};
+
+// Workgroup b sums job b.  Lane l adds partials l, l + 1024, l + 2048, ... in
+// that order (loads of a batch of 8 issued before their adds), then a fixed
+// tree: deterministic, and up to 8192 partials cost one memory round trip.
+__global__ __launch_bounds__(kSumBlock) void k_sum_partials(SumJob j0, SumJob j1)
 {
+    const SumJob job = blockIdx.x == 0 ? j0 : j1;
+    const double* __restrict__ partials = job.partials;
+    const int32_t n = job.n;
     double t = 0.0;
     int i = (int)threadIdx.x;
     for (; i + (kSumUnroll - 1) * kSumBlock < n; i += kSumUnroll * kSumBlock) {
@@ -478,15 +486,23 @@ __global__ __launch_bounds__(kSumBlock) void k_sum_partials(const double* __rest
     }
     for (; i < n; i += kSumBlock) t += partials[i];
     t = block_sum<kSumBlock>(t);
-    if (threadIdx.x == 0) *out = t;
+    if (threadIdx.x == 0) *job.out = t;
 }
 }  // namespace
 
 int sum_partials(const double* partials, int32_t n, double* out, void* stream)
 {
-    hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(kSumBlock), 0, as_stream(stream), partials,
-                       n, out);
+    const SumJob j0{partials, n, out};
+    hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(kSumBlock), 0, as_stream(stream), j0, j0);
     return check_launch("sum_partials");
+}
+
+int sum_partials2(const double* p0, int32_t n0, double* out0, const double* p1, int32_t n1,
+                  double* out1, void* stream)
+{
+    hipLaunchKernelGGL(k_sum_partials, dim3(2), dim3(kSumBlock), 0, as_stream(stream),
+                       SumJob{p0, n0, out0}, SumJob{p1, n1, out1});
+    return check_launch("sum_partials2");
 }
 
 #define DIAGPU_SPMV_INSTANCE(TV, TX)                                                          \

@@ -16,12 +16,16 @@ struct cf32 {
 // one-workgroup kernel on the same stream adds them in tile order into *out
 // (deterministic).  `partials` holds spmv_tiles<TV, TX>(rows) doubles.
 struct DotArgs {
-    double* partials;
-    double* out;
+    double* partials;   // one per row tile (spmv_tiles)
+    double* out;        // the sum, or NULL: the caller adds the partials itself
 };
 
 // *out = sum of partials[0 .. n) in index order (one workgroup, async).
 int sum_partials(const double* partials, int32_t n, double* out, void* stream);
+
+// Two such sums in one launch (one workgroup each), each in index order.
+int sum_partials2(const double* p0, int32_t n0, double* out0, const double* p1, int32_t n1,
+                  double* out1, void* stream);
 
 // Number of row tiles (= workgroups doing work) of an SpMV launch.
 template <typename TV, typename TX>
