@@ -109,6 +109,7 @@ PROTOTYPES: dict[str, tuple] = {
         _vp, _vp, _i32, _vp, _vp]),
     "diagpu_hm_to_recon_f32": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp]),
     "diagpu_hm_to_recon_c64": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp]),
+    "diagpu_promote_f32_c64": (C.c_int, [_i64, _vp, _vp, _vp]),
 }
 
 _lib: C.CDLL | None = None

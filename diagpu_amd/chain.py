@@ -48,11 +48,16 @@ def identity(n: int, device, dtype=torch.float32) -> HM:
     return I
 
 
-def as_complex(M: HM) -> HM:
-    """The same matrix with complex64 values (a copy; M itself if already complex)."""
+def as_complex(M: HM, stream=None) -> HM:
+    """The same matrix with complex64 values (a copy made on the device by
+    diagpu_promote_f32_c64; M itself if already complex)."""
     if M.values.dtype == torch.complex64:
         return M
-    return HM(M.n, M.offsets, M.lengths, M.starts, M.values.to(torch.complex64))
+    _check_dev(M.values, torch.float32, "values")
+    out = torch.empty(M.values.numel(), dtype=torch.complex64, device=M.values.device)
+    _lib.call("diagpu_promote_f32_c64", M.values.numel(), M.values.data_ptr(), out.data_ptr(),
+              _stream_handle(stream))
+    return HM(M.n, M.offsets, M.lengths, M.starts, out)
 
 
 def _c64(z) -> "_lib.Complex64":

@@ -9,7 +9,8 @@
 // columns [max(d, 0), max(d, 0) + n - |d|), zero elsewhere.  It lets a product
 // built by SpGEMM (a propagator, a matrix power) be applied by the SpMV path
 // without a trip through host memory.  One streaming pass: every Recon value
-// written once, every HM value read once.
+// written once, every HM value read once.  Also the real -> complex64
+// promotion of a value array (diagpu_promote_f32_c64).
 #include "common.hpp"
 #include "elem.hpp"
 
@@ -62,10 +63,44 @@ int hm_to_recon(int32_t n, const int32_t* off, const int64_t* starts, int32_t K,
     return check_launch(fn);
 }
 
+// dst[i] = (src[i], 0): a real operator's values as complex64.  Grid-stride,
+// 16-byte stores.
+__global__ __launch_bounds__(kBlock) void k_promote(int64_t count, const float* __restrict__ src,
+                                                   cf32* __restrict__ dst)
+{
+    const int64_t stride = (int64_t)gridDim.x * kBlock * 2;
+    for (int64_t i = ((int64_t)blockIdx.x * kBlock + threadIdx.x) * 2; i < count; i += stride) {
+        if (i + 2 <= count) {
+            const float a = src[i], b = src[i + 1];
+            const f4dw q = {a, 0.f, b, 0.f};
+            *reinterpret_cast<f4dw*>(dst + i) = q;
+        } else {
+            dst[i] = cf32{src[i], 0.f};
+        }
+    }
+}
+
 }  // namespace
 }  // namespace diagpu
 
 extern "C" {
+
+DIAGPU_API int diagpu_promote_f32_c64(int64_t count, const float* src, diagpu_complex64* dst,
+                                      void* stream)
+{
+    const char* fn = "diagpu_promote_f32_c64";
+    if (count < 0) return diagpu::fail(DIAGPU_ERR_ARG, "%s: negative count", fn);
+    if (count == 0) return DIAGPU_OK;
+    if (!src || !dst) return diagpu::fail(DIAGPU_ERR_ARG, "%s: a pointer is NULL", fn);
+    using diagpu::cf32;
+    const int64_t pairs = (count + 1) / 2;
+    int64_t grid = diagpu::ceil_div<int64_t>(pairs, diagpu::kBlock);
+    const int64_t cap = (int64_t)diagpu::cu_count() * 16;
+    if (grid > cap) grid = cap;
+    hipLaunchKernelGGL(diagpu::k_promote, dim3((unsigned)grid), dim3(diagpu::kBlock), 0,
+                       diagpu::as_stream(stream), count, src, reinterpret_cast<cf32*>(dst));
+    return diagpu::check_launch(fn);
+}
 
 DIAGPU_API int diagpu_hm_to_recon_f32(int32_t n, const int32_t* offsets, const int64_t* starts,
                                       int32_t ndiag, const float* values, int32_t* recon_offsets,

@@ -300,6 +300,13 @@ DIAGPU_API int diagpu_hm_to_recon_c64(int32_t n, const int32_t* offsets, const i
                                       int32_t* recon_offsets, diagpu_complex64* recon_values,
                                       void* stream);
 
+/* dst[i] = (src[i], 0) for i < count, on the device: a real operator's
+ * values (any layout) as complex64, e.g. to start a complex chain such as
+ * the propagator exp(-i dt H) from a real H.  No counterpart in the
+ * reference (its kernels are real only). */
+DIAGPU_API int diagpu_promote_f32_c64(int64_t count, const float* src, diagpu_complex64* dst,
+                                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -267,6 +267,15 @@ public:
                                         info_.max_pairs, dC_vals, stream));
     }
 
+    // The same product with complex64 operands and C (same plan).
+    void numeric(const diagpu_complex64* dA_vals, const diagpu_complex64* dB_vals,
+                 diagpu_complex64* dC_vals, hipStream_t stream = 0) const
+    {
+        check(diagpu_spgemm_numeric_c64(n_, dA_vals, dB_vals, C_off_.data(), C_len_.data(),
+                                        C_starts_.data(), info_.c_ndiag, ptr_.data(), pairs_.data(),
+                                        info_.max_pairs, dC_vals, stream));
+    }
+
     const diagpu_spgemm_info& info() const { return info_; }
     const int* c_offsets() const { return C_off_.data(); }
     const int* c_lengths() const { return C_len_.data(); }

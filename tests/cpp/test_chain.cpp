@@ -2,10 +2,15 @@
 // Taylor series built by the device-planned SpGEMM chain, checked against
 // dense float64 products on the host:
 //   |P - P64| <= 1e-5 * k * (|H|^k)  elementwise (k products of fp32 sums),
-// and the result's diagonal set equals the sumset of H's offsets.
+// and the result's diagonal set equals the sumset of H's offsets.  The
+// complex propagator U = exp(-i dt H) against a complex128 series on the
+// host (|U - U64| <= 1e-5 * order * expm(dt |H|) + the truncation bound),
+// U U^H = I, and U in the Recon layout (to_recon) applied by the complex
+// SpMV against the dense product and against the Lanczos propagator.
 #include <unistd.h>
 
 #include <cmath>
+#include <complex>
 #include <cstdio>
 #include <random>
 #include <set>
@@ -159,6 +164,218 @@ static void test_axpby()
     report("axpby on the union of diagonals", ok, det);
 }
 
+// ---- complex propagator ----------------------------------------------------
+
+using cd = std::complex<double>;
+using DenseC = std::vector<cd>;
+
+// Hermitian band: diagonal +d random, -d its conjugate at the same positions,
+// main diagonal real.  Offsets ascending; values back to back.
+static void hermitian_band(int n, const std::vector<int>& pos, bool cplx, unsigned seed,
+                           std::vector<int>& offs, std::vector<diagpu_complex64>& vals, DenseC& D)
+{
+    std::mt19937 rng(seed);
+    std::uniform_real_distribution<float> U(-1.0f, 1.0f);
+    std::set<int> all;
+    for (int d : pos) { all.insert(d); all.insert(-d); }
+    offs.assign(all.begin(), all.end());
+    std::vector<std::vector<diagpu_complex64>> diag(offs.size());
+    for (size_t k = 0; k < offs.size(); ++k) diag[k].resize(static_cast<size_t>(n - std::abs(offs[k])));
+    auto index = [&](int d) { return static_cast<size_t>(std::lower_bound(offs.begin(), offs.end(), d) - offs.begin()); };
+    for (int d : pos) {
+        auto& up = diag[index(d)];
+        auto& lo = diag[index(-d)];
+        for (auto& v : up) v = diagpu_complex64{U(rng), (cplx && d != 0) ? U(rng) : 0.0f};
+        for (size_t p = 0; p < up.size(); ++p) lo[p] = diagpu_complex64{up[p].re, -up[p].im};
+    }
+    vals.clear();
+    D.assign(static_cast<size_t>(n) * n, cd(0.0));
+    for (size_t k = 0; k < offs.size(); ++k) {
+        const int d = offs[k];
+        for (size_t p = 0; p < diag[k].size(); ++p) {
+            const int r = static_cast<int>(p) - std::min(d, 0);
+            D[static_cast<size_t>(r) * n + r + d] = cd(diag[k][p].re, diag[k][p].im);
+            vals.push_back(diag[k][p]);
+        }
+    }
+}
+
+static DenseC matmul_c(const DenseC& A, const DenseC& B, int n)
+{
+    DenseC C(static_cast<size_t>(n) * n, cd(0.0));
+    for (int i = 0; i < n; ++i)
+        for (int k = 0; k < n; ++k) {
+            const cd a = A[static_cast<size_t>(i) * n + k];
+            if (a == cd(0.0)) continue;
+            for (int j = 0; j < n; ++j) C[static_cast<size_t>(i) * n + j] += a * B[static_cast<size_t>(k) * n + j];
+        }
+    return C;
+}
+
+// sum_{k<terms} (s M)^k / k! in complex128 (||s M|| small)
+static DenseC series(const DenseC& M, cd s, int n, int terms)
+{
+    DenseC S(static_cast<size_t>(n) * n, cd(0.0)), P(S);
+    for (int i = 0; i < n; ++i) S[static_cast<size_t>(i) * n + i] = P[static_cast<size_t>(i) * n + i] = cd(1.0);
+    for (int k = 1; k < terms; ++k) {
+        P = matmul_c(P, M, n);
+        for (auto& v : P) v *= s / static_cast<double>(k);
+        for (size_t i = 0; i < S.size(); ++i) S[i] += P[i];
+    }
+    return S;
+}
+
+static DenseC hm_to_dense_c(const diagpu::DeviceHMC& M)
+{
+    const int n = M.n;
+    const std::vector<diagpu_complex64> v = M.download_values();
+    DenseC D(static_cast<size_t>(n) * n, cd(0.0));
+    size_t q = 0;
+    for (int d : M.offsets)
+        for (int p = 0; p < n - std::abs(d); ++p, ++q) {
+            const int r = p - std::min(d, 0);
+            D[static_cast<size_t>(r) * n + r + d] = cd(v[q].re, v[q].im);
+        }
+    return D;
+}
+
+static void test_propagator(const char* name, int n, const std::vector<int>& pos, bool cplx,
+                            float dt, int order)
+{
+    std::vector<int> offs;
+    std::vector<diagpu_complex64> vals;
+    DenseC Hd;
+    hermitian_band(n, pos, cplx, 77u + n, offs, vals, Hd);
+    diagpu::DeviceHMC U;
+    if (cplx) {
+        U = diagpu::propagator(diagpu::DeviceHMC::upload(n, offs, vals), dt, order);
+    } else {   // a real H: promoted on the device
+        std::vector<float> rv(vals.size());
+        for (size_t i = 0; i < vals.size(); ++i) rv[i] = vals[i].re;
+        U = diagpu::propagator(diagpu::DeviceHM::upload(n, offs, rv), dt, order);
+    }
+    const DenseC Ud = hm_to_dense_c(U);
+    const DenseC want = series(Hd, cd(0.0, -dt), n, 40);
+    DenseC Ha(Hd.size());
+    double nrm = 0.0;   // ||dt H||_inf
+    for (int i = 0; i < n; ++i) {
+        double row = 0.0;
+        for (int j = 0; j < n; ++j) {
+            Ha[static_cast<size_t>(i) * n + j] = cd(std::abs(Hd[static_cast<size_t>(i) * n + j]));
+            row += std::abs(Hd[static_cast<size_t>(i) * n + j]);
+        }
+        nrm = std::max(nrm, row * dt);
+    }
+    const DenseC bound = series(Ha, cd(dt, 0.0), n, 40);   // expm(dt |H|)
+    double fact = 1.0;
+    for (int k = 2; k <= order + 1; ++k) fact *= k;
+    const double trunc = std::pow(nrm, order + 1) / fact * std::exp(nrm);
+    double worst = 0.0;
+    for (size_t i = 0; i < Ud.size(); ++i)
+        worst = std::max(worst, std::abs(Ud[i] - want[i]) / (1e-5 * order * bound[i].real() + trunc + 1e-30));
+    // unitarity
+    double uni = 0.0;
+    for (int i = 0; i < n; ++i)
+        for (int j = 0; j < n; ++j) {
+            cd s(0.0);
+            for (int k = 0; k < n; ++k)
+                s += Ud[static_cast<size_t>(i) * n + k] * std::conj(Ud[static_cast<size_t>(j) * n + k]);
+            uni = std::max(uni, std::abs(s - cd(i == j ? 1.0 : 0.0)));
+        }
+    char det[96];
+    std::snprintf(det, sizeof det, "max err/tol %.3f, |UU^H - I| %.1e", worst, uni);
+    report(name, worst <= 1.0 && uni <= 1e-5, det);
+}
+
+// U in the Recon layout applied by the complex SpMV: against the dense
+// product, and against the Lanczos propagator of the same H.
+static void test_propagator_applied()
+{
+    const int n = 3000;   // H only as HM (no dense copy at this size)
+    const float dt = 0.05f;
+    const std::vector<int> pos = {0, 1, 2, 57};
+    std::vector<int> offs;
+    std::vector<diagpu_complex64> vals;
+    {
+        std::set<int> all;
+        for (int d : pos) { all.insert(d); all.insert(-d); }
+        offs.assign(all.begin(), all.end());
+        std::mt19937 rng(11);
+        std::uniform_real_distribution<float> U(-1.0f, 1.0f);
+        std::vector<std::vector<diagpu_complex64>> diag(offs.size());
+        for (size_t k = 0; k < offs.size(); ++k) diag[k].resize(static_cast<size_t>(n - std::abs(offs[k])));
+        auto index = [&](int d) { return static_cast<size_t>(std::lower_bound(offs.begin(), offs.end(), d) - offs.begin()); };
+        for (int d : pos) {
+            auto& up = diag[index(d)];
+            auto& lo = diag[index(-d)];
+            for (auto& v : up) v = diagpu_complex64{U(rng), d ? U(rng) : 0.0f};
+            for (size_t p = 0; p < up.size(); ++p) lo[p] = diagpu_complex64{up[p].re, -up[p].im};
+        }
+        for (auto& d : diag) vals.insert(vals.end(), d.begin(), d.end());
+    }
+    const diagpu::DeviceHMC H = diagpu::DeviceHMC::upload(n, offs, vals);
+    const diagpu::DeviceHMC U = diagpu::propagator(H, dt, 8);
+    const auto UR = diagpu::to_recon(U);
+    const auto HR = diagpu::to_recon(H);
+    // Recon layout: offsets descending, Recon[k][c] = U[c - d][c], zero padding
+    const std::vector<int> ro = UR.offsets.download();
+    const std::vector<diagpu_complex64> rv = UR.values.download();
+    const std::vector<diagpu_complex64> uv = U.download_values();
+    bool layout_ok = static_cast<int>(ro.size()) == U.ndiag();
+    size_t q = 0;
+    std::vector<size_t> start(U.offsets.size());
+    for (size_t k = 0; k < U.offsets.size(); ++k) { start[k] = q; q += static_cast<size_t>(n - std::abs(U.offsets[k])); }
+    for (int k = 0; layout_ok && k < U.ndiag(); ++k) {
+        const int ks = U.ndiag() - 1 - k;
+        const int d = U.offsets[ks];
+        layout_ok = ro[k] == d;
+        for (int c = 0; layout_ok && c < n; ++c) {
+            const diagpu_complex64 g = rv[static_cast<size_t>(k) * n + c];
+            const int r = c - d;
+            diagpu_complex64 w{0.0f, 0.0f};
+            if (r >= 0 && r < n) w = uv[start[ks] + static_cast<size_t>(std::min(r, c))];
+            layout_ok = g.re == w.re && g.im == w.im;
+        }
+    }
+    report("to_recon(U): build_recon layout, exact", layout_ok);
+
+    std::mt19937 rng(3);
+    std::normal_distribution<float> N(0.0f, 1.0f);
+    std::vector<std::complex<float>> psi(static_cast<size_t>(n));
+    for (auto& v : psi) v = {N(rng), N(rng)};
+    diagpu::DeviceArray<std::complex<float>> dpsi(psi), dy(static_cast<size_t>(n)), dk(static_cast<size_t>(n));
+    const diagpu_recon_view_c64 uview = diagpu::view(UR);
+    diagpu::check(diagpu_spmv_recon_c64(&uview, reinterpret_cast<const diagpu_complex64*>(dpsi.data()), n,
+                                        reinterpret_cast<diagpu_complex64*>(dy.data()), nullptr));
+    diagpu::KrylovPropagator prop(n, 20);
+    const diagpu::KrylovResult kr = prop.run(diagpu::view(HR), dpsi.data(), dt, dk.data());
+    const std::vector<std::complex<float>> y = dy.download(), yk = dk.download();
+    // U psi on the host from U's own values (fp64)
+    std::vector<cd> yh(static_cast<size_t>(n), cd(0.0));
+    for (size_t k = 0; k < U.offsets.size(); ++k) {
+        const int d = U.offsets[k];
+        for (int p = 0; p < n - std::abs(d); ++p) {
+            const int r = p - std::min(d, 0);
+            const diagpu_complex64 u = uv[start[k] + static_cast<size_t>(p)];
+            yh[static_cast<size_t>(r)] += cd(u.re, u.im) * cd(psi[static_cast<size_t>(r + d)]);
+        }
+    }
+    double e1 = 0.0, e2 = 0.0, np = 0.0, ny = 0.0;
+    for (int i = 0; i < n; ++i) {
+        e1 += std::norm(cd(y[i]) - yh[i]);
+        e2 += std::norm(cd(y[i]) - cd(yk[i]));
+        np += std::norm(cd(psi[i]));
+        ny += std::norm(cd(y[i]));
+    }
+    e1 = std::sqrt(e1 / np);
+    e2 = std::sqrt(e2 / np);
+    const double unit = std::fabs(std::sqrt(ny / np) - 1.0);
+    char det[128];
+    std::snprintf(det, sizeof det, "vs U psi (fp64) %.1e, vs Lanczos %.1e, | ||U psi||/||psi|| - 1 | %.1e",
+                  e1, e2, unit);
+    report("U psi by the complex SpMV", e1 <= 1e-6 && e2 <= 2e-5 && unit <= 2e-5 && kr.steps > 0, det);
+}
+
 int main()
 {
     std::setvbuf(stdout, nullptr, _IONBF, 0);
@@ -171,6 +388,9 @@ int main()
         test_taylor("exp(0.2 H), order 10", 240, {-3, -1, 0, 1, 4}, 0.2f, 10);
         test_taylor("exp(0.5 H), order 8, no main diagonal", 180, {-2, 1}, 0.5f, 8);
         test_taylor("order 0 is the identity", 64, {-1, 1}, 1.0f, 0);
+        test_propagator("exp(-i 0.05 H), complex Hermitian, order 10", 120, {0, 1, 3, 17}, true, 0.05f, 10);
+        test_propagator("exp(-i 0.1 H), real H promoted, order 12", 96, {0, 2, 5}, false, 0.1f, 12);
+        test_propagator_applied();
     } catch (const std::exception& e) {
         std::printf("  exception: %s\n", e.what());
         g_all = false;

@@ -152,3 +152,6 @@ def test_complex_and_krylov_argument_errors():
     assert b"workspace" in _lib.load().diagpu_last_error()
     assert _status("diagpu_expm_krylov_f32", None, fake, 1.0, 10, fake, fake, b.value, None,
                    None, C.byref(info), None) == _lib.ERR_ARG
+    assert _status("diagpu_promote_f32_c64", -1, fake, fake, None) == _lib.ERR_ARG
+    assert _status("diagpu_promote_f32_c64", 5, None, fake, None) == _lib.ERR_ARG
+    assert _status("diagpu_promote_f32_c64", 0, None, None, None) == _lib.OK

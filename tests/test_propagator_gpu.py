@@ -73,6 +73,21 @@ def test_hm_to_recon_matches_reference_build_recon(dev, oracle):
         assert np.allclose(y, chain.hm_matvec64(M, x.astype(np.complex128)), rtol=0, atol=1e-4)
 
 
+@pytest.mark.parametrize("count", [1, 2, 7, 1 << 20, (1 << 20) + 3])
+def test_promote_f32_c64(dev, count):
+    """diagpu_promote_f32_c64: dst = (src, 0), exactly, for odd and even
+    counts and with a one-element offset (unaligned) destination."""
+    from diagpu_amd import _lib
+    g = torch.Generator(device=dev).manual_seed(count)
+    src = torch.randn(count, device=dev, generator=g)
+    buf = torch.full((count + 1,), complex("nan+nanj"), dtype=torch.complex64, device=dev)
+    _lib.call("diagpu_promote_f32_c64", count, src.data_ptr(), buf[1:].data_ptr(),
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.isnan(buf[0].real)
+    assert torch.equal(buf[1:].real, src) and torch.equal(buf[1:].imag, torch.zeros_like(src))
+
+
 def test_complex_axpby(dev):
     n = 300
     X = _complex_hm(n, [-4, 0, 9], 1, dev)
