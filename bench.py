@@ -47,7 +47,7 @@ def parse_args(argv=None):
     ap.add_argument("--only", default="",
                     help="profiling aid: run just one workload (spmv2, spmv2d, spmv2c, "
                          "spmv2rc, spmv1, spmv3, spgemm4, spgemm5, spgemm4c, spgemm5c, taylor, krylov, "
-                         "propagator, copy) "
+                         "propagator, propagator2d, copy) "
                          "and print its line")
     return ap.parse_args(argv)
 
@@ -346,17 +346,27 @@ def time_taylor(order: int = 6, t: float = 0.05):
             "steps": steps}
 
 
-def time_propagator(order: int = 6, dt: float = 0.02, m: int = 12, reps: int = 20):
-    """The two propagation workflows of slides/transcript.md:10-18 on the
-    7-point stencil of SpGEMM config 4 (n = 2^20): build U = exp(-i dt H)
-    once (complex Taylor chain + device HM->Recon) and apply it by the
-    complex SpMV, against one Lanczos call per time step on H itself.
-    Break-even = the number of steps after which building U has paid off."""
+def time_propagator(grid: str = "3d", order: int = 6, dt: float = 0.02, m: int = 12,
+                    reps: int = 20):
+    """The two propagation workflows of slides/transcript.md:10-18: build
+    U = exp(-i dt H) once (complex Taylor chain + device HM->Recon) and apply
+    it by the complex SpMV, against one Lanczos call per time step on H
+    itself.  grid "3d": the 7-point stencil of SpGEMM config 4 (n = 2^20;
+    U has 377 diagonals at order 6); "2d": config 2's 5-point stencil
+    (n = 2^22; 85 diagonals).  Break-even = the number of steps after which
+    building U has paid off."""
     import torch
     from diagpu_amd import chain, workloads
     from diagpu_amd.krylov import expm_krylov, KrylovWorkspace
     from diagpu_amd.spmv import spmv_recon
-    H = workloads.hm_stencil7(128, 128, 64, device="cuda")
+    if grid == "3d":
+        H = workloads.hm_stencil7(128, 128, 64, device="cuda")
+        name = "propagator_stencil7_cfg4"
+    elif grid == "2d":
+        H = workloads.recon_to_hm(workloads.spmv_config(2, seed=1, device="cuda"))
+        name = "propagator_poisson5_cfg2"
+    else:
+        raise ValueError(f"unknown grid {grid}")
     n = H.n
     chain.to_recon(chain.propagator(H, dt, order))          # warm-up (plans, allocator)
     torch.cuda.synchronize()
@@ -393,7 +403,7 @@ def time_propagator(order: int = 6, dt: float = 0.02, m: int = 12, reps: int = 2
     kry_ms = (time.perf_counter() - t0) * 1e3 / reps
     nrm = torch.linalg.vector_norm(psi.to(torch.complex128)).item()
     rel = torch.linalg.vector_norm((y - out).to(torch.complex128)).item() / nrm
-    return {"workload": "propagator_stencil7_cfg4", "n": n, "order": order, "dt": dt,
+    return {"workload": name, "n": n, "order": order, "dt": dt,
             "U_diags": K, "U_bytes": 8 * K * n, "build_ms": round(build_ms, 3),
             "apply_ms": round(apply_ms, 4),
             "apply_GBs": round(apply_bytes / (apply_ms * 1e6), 1),
@@ -459,7 +469,9 @@ def main(argv=None) -> int:
         elif w == "taylor":
             print(json.dumps(time_taylor()), flush=True)
         elif w == "propagator":
-            print(json.dumps(time_propagator()), flush=True)
+            print(json.dumps(time_propagator("3d")), flush=True)
+        elif w == "propagator2d":
+            print(json.dumps(time_propagator("2d")), flush=True)
         else:
             raise SystemExit(f"unknown --only {w}")
         return 0
@@ -528,14 +540,15 @@ def main(argv=None) -> int:
             torch.cuda.empty_cache()
         except Exception as e:
             extras["taylor_chain"] = {"error": repr(e)}
-        try:
-            rec = time_propagator()
-            extras["propagator"] = rec
-            log(f"extra propagator: build {rec['build_ms']} ms, apply {rec['apply_ms']} ms, "
-                f"krylov {rec['krylov_ms']} ms")
+        for grid in ("3d", "2d"):
+            try:
+                rec = time_propagator(grid)
+                extras[rec["workload"]] = rec
+                log(f"extra {rec['workload']}: build {rec['build_ms']} ms, apply {rec['apply_ms']} ms, "
+                    f"krylov {rec['krylov_ms']} ms")
+            except Exception as e:
+                extras[f"propagator_{grid}"] = {"error": repr(e)}
             torch.cuda.empty_cache()
-        except Exception as e:
-            extras["propagator"] = {"error": repr(e)}
 
     traffic = load_traffic("spmv_cfg2_f32")
     line = {

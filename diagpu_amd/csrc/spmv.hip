@@ -31,11 +31,13 @@
 // the ring kernel keeps W diagonals' loads in flight per lane at all times --
 // step j consumes slot j and refills it with the diagonal W ahead, and
 // sched_barrier pins that order so the compiler emits a steady vmcnt window
-// instead of hoisting or sinking the loads.  Offsets travel 64 at a time in
-// one VGPR (lane l holds d_{g0+l}) and are broadcast with readlane, which
-// needs no memory wait.  For K <= 5 the short kernel takes the offsets with
-// scalar loads (the scalar cache does not queue behind the HBM stream) and
-// issues all 2K loads straight-line.
+// instead of hoisting or sinking the loads.  Offsets come through the scalar
+// cache (the compiler batches them into s_load_dwordx4/x2), which does not
+// queue behind the HBM stream, so one ring runs over all K diagonals with no
+// drain anywhere (measured against 64 offsets per VGPR broadcast by
+// readlane, with a refill of that VGPR every 64 diagonals: 1.7 points of
+// 8 TB/s on config 3's 64 diagonals, about 1 point at 85 and 377).  For
+// K <= 5 the short kernel issues all 2K loads straight-line.
 //
 // Edge tiles.  A tile whose rows or columns leave the matrix for some
 // diagonal runs the same ring, still with 16-byte runs, each loaded at its
@@ -123,14 +125,15 @@ enum EdgeMode {
     kEdgeRun = 1,    // 16-byte runs at clamped starts, shifted and masked
 };
 
-// One group of gn <= 64 diagonals (offsets in `ov`, lane l = d_{g0+l};
-// values `vg` = Recon row g0) accumulated into `acc` for the lane's R rows
-// starting at row `r`.  W diagonals' loads in flight; every index is clamped
-// to the group so all loads are valid, and the slots past the group are
+// The gn diagonals with offsets `offs` (read with uniform indices: scalar
+// loads) and values `vg` (Recon rows) accumulated into `acc` for the lane's R
+// rows starting at row `r`.  W diagonals' loads in flight; every index is
+// clamped to [0, gn) so all loads are valid, and the slots past the end are
 // masked.  kEdgeRun needs lim >= R and masks every term whose column is
 // outside [0, lim).
 template <typename TV, typename TX, int W, int MODE>
-__device__ __forceinline__ void ring_group(int64_t r, int64_t cols, int64_t lim, int gn, int ov,
+__device__ __forceinline__ void ring_group(int64_t r, int64_t cols, int64_t lim, int gn,
+                                           const int32_t* __restrict__ offs,
                                            const TV* __restrict__ vg, const TX* __restrict__ x,
                                            Run<TX, Shape<TV, TX>::R>& acc)
 {
@@ -143,7 +146,7 @@ __device__ __forceinline__ void ring_group(int64_t r, int64_t cols, int64_t lim,
         return c < 0 ? 0 : (c > hi ? hi : c);
     };
     auto issue = [&](int j, int k) {
-        const int d = __builtin_amdgcn_readlane(ov, k);
+        const int d = offs[k];
         const TV* vk = vg + (int64_t)k * cols;
         if constexpr (MODE == kInterior) {
             a[j] = load_run<TV, R, true>(vk + r + d);
@@ -161,7 +164,7 @@ __device__ __forceinline__ void ring_group(int64_t r, int64_t cols, int64_t lim,
             for (int e = 0; e < R; ++e)
                 acc.v[e] = sel(on, mad(acc.v[e], a[j].v[e], b[j].v[e]), acc.v[e]);
         } else {
-            const int64_t c = r + __builtin_amdgcn_readlane(ov, k);
+            const int64_t c = r + offs[k];
             // element e of the run sits at index e + s of what was loaded
             const int s = (int)(c - clamp_run(c));
 #pragma unroll
@@ -215,11 +218,12 @@ __device__ __forceinline__ void ring_group(int64_t r, int64_t cols, int64_t lim,
 // A non-interior tile (lim >= R: the host sends narrower matrices to
 // spmv_narrow_kernel).
 template <typename TV, typename TX>
-__device__ __forceinline__ void edge_group(int64_t r, int64_t cols, int64_t lim, int gn, int ov,
+__device__ __forceinline__ void edge_group(int64_t r, int64_t cols, int64_t lim, int gn,
+                                           const int32_t* __restrict__ offs,
                                            const TV* __restrict__ vg, const TX* __restrict__ x,
                                            Run<TX, Shape<TV, TX>::R>& acc)
 {
-    ring_group<TV, TX, Shape<TV, TX>::WR, kEdgeRun>(r, cols, lim, gn, ov, vg, x, acc);
+    ring_group<TV, TX, Shape<TV, TX>::WR, kEdgeRun>(r, cols, lim, gn, offs, vg, x, acc);
 }
 
 template <typename TX, int R>
@@ -259,9 +263,8 @@ __device__ __forceinline__ void dot_epilogue(const Run<TX, R>& acc, const TX* __
 // Kernels
 // ---------------------------------------------------------------------------
 
-// General K: groups of 64 diagonals, each through the ring (MULTI = false:
-// K <= 64, one group, the offsets VGPR loaded once).
-template <typename TV, typename TX, bool MULTI, bool DOT>
+// K > kShortMax: one ring over all K diagonals.
+template <typename TV, typename TX, bool DOT>
 __global__ __launch_bounds__(kBlock) void spmv_ring_kernel(
     int32_t rows, int32_t cols, int64_t lim, int32_t K, const int32_t* __restrict__ offs,
     const TV* __restrict__ vals, const TX* __restrict__ x, TX* __restrict__ y, int32_t tiles,
@@ -275,19 +278,14 @@ __global__ __launch_bounds__(kBlock) void spmv_ring_kernel(
     const int64_t r0 = (int64_t)tile * S::TILE;
     const int64_t r = r0 + (int64_t)threadIdx.x * R;
 
-    // offset range over all groups (one vector load per 64 offsets)
-    const int g0n = K < 64 ? K : 64;
-    const int ov0 = offs[lane < g0n ? lane : g0n - 1];
-    int dmin, dmax;
-    wave_minmax(ov0, dmin, dmax);
-    if constexpr (MULTI) {
-        for (int g0 = 64; g0 < K; g0 += 64) {
-            const int gn = (K - g0) < 64 ? (K - g0) : 64;
-            int lo, hi;
-            wave_minmax(offs[g0 + (lane < gn ? lane : gn - 1)], lo, hi);
-            dmin = lo < dmin ? lo : dmin;
-            dmax = hi > dmax ? hi : dmax;
-        }
+    // offset range (one vector load per 64 offsets, reduced across the wave)
+    int dmin = INT_MAX, dmax = INT_MIN;
+    for (int g0 = 0; g0 < K; g0 += 64) {
+        const int gn = (K - g0) < 64 ? (K - g0) : 64;
+        int lo, hi;
+        wave_minmax(offs[g0 + (lane < gn ? lane : gn - 1)], lo, hi);
+        dmin = lo < dmin ? lo : dmin;
+        dmax = hi > dmax ? hi : dmax;
     }
     const bool interior =
         r0 + S::TILE <= rows && r0 + dmin >= 0 && r0 + S::TILE + (int64_t)dmax <= lim;
@@ -295,22 +293,10 @@ __global__ __launch_bounds__(kBlock) void spmv_ring_kernel(
     Run<TX, R> acc;
 #pragma unroll
     for (int e = 0; e < R; ++e) acc.v[e] = zero_of<TX>();
-    if constexpr (!MULTI) {
-        if (interior)
-            ring_group<TV, TX, S::W, kInterior>(r, cols, lim, K, ov0, vals, x, acc);
-        else
-            edge_group<TV, TX>(r, cols, lim, K, ov0, vals, x, acc);
-    } else {
-        for (int g0 = 0; g0 < K; g0 += 64) {
-            const int gn = (K - g0) < 64 ? (K - g0) : 64;
-            const int ov = g0 == 0 ? ov0 : offs[g0 + (lane < gn ? lane : gn - 1)];
-            const TV* vg = vals + (int64_t)g0 * cols;
-            if (interior)
-                ring_group<TV, TX, S::W, kInterior>(r, cols, lim, gn, ov, vg, x, acc);
-            else
-                edge_group<TV, TX>(r, cols, lim, gn, ov, vg, x, acc);
-        }
-    }
+    if (interior)
+        ring_group<TV, TX, S::W, kInterior>(r, cols, lim, K, offs, vals, x, acc);
+    else
+        edge_group<TV, TX>(r, cols, lim, K, offs, vals, x, acc);
     store_rows<TX, R>(y, r, rows, acc, interior);
     if constexpr (DOT) dot_epilogue<TX, R>(acc, x, r, rows, interior, tile, tiles, da);
 }
@@ -358,9 +344,7 @@ __global__ __launch_bounds__(kBlock) void spmv_short_kernel(
 #pragma unroll
                 for (int e = 0; e < R; ++e) acc.v[e] = mad(acc.v[e], a[k].v[e], b[k].v[e]);
         } else {
-            const int lane = (int)threadIdx.x & 63;
-            const int ov = offs[lane < KF ? lane : KF - 1];
-            edge_group<TV, TX>(r, cols, lim, KF, ov, vals, x, acc);
+            edge_group<TV, TX>(r, cols, lim, KF, offs, vals, x, acc);
         }
     }
     store_rows<TX, R>(y, r, rows, acc, interior);
@@ -410,8 +394,7 @@ SpmvKernel<TV, TX> pick_kernel(int K, int64_t lim)
     case 3: return spmv_short_kernel<TV, TX, 3, DOT>;
     case 4: return spmv_short_kernel<TV, TX, 4, DOT>;
     case 5: return spmv_short_kernel<TV, TX, 5, DOT>;
-    default:
-        return K <= 64 ? spmv_ring_kernel<TV, TX, false, DOT> : spmv_ring_kernel<TV, TX, true, DOT>;
+    default: return spmv_ring_kernel<TV, TX, DOT>;
     }
 }
 static_assert(kShortMax == 5, "pick_kernel covers K = 0..5");
