@@ -75,9 +75,9 @@ PROTOTYPES: dict[str, tuple] = {
     "diagpu_spmv_recon_f32_c64": (C.c_int, [C.POINTER(ReconViewF32), _vp, _i64, _vp, _vp]),
     "diagpu_expm_krylov_workspace": (C.c_int, [_i32, _i32, C.POINTER(_sz)]),
     "diagpu_expm_krylov_c64": (C.c_int, [C.POINTER(ReconViewC64), _vp, C.c_double, _i32, _vp,
-                                         _vp, _sz, _vp, _vp, C.POINTER(KrylovInfo), _vp]),
+                                         _vp, _sz, _vp, _vp, _vp, C.POINTER(KrylovInfo), _vp]),
     "diagpu_expm_krylov_f32": (C.c_int, [C.POINTER(ReconViewF32), _vp, C.c_double, _i32, _vp,
-                                         _vp, _sz, _vp, _vp, C.POINTER(KrylovInfo), _vp]),
+                                         _vp, _sz, _vp, _vp, _vp, C.POINTER(KrylovInfo), _vp]),
     "diagpu_spgemm_symbolic_workspace": (C.c_int, [_i32, _i32, _i32, C.POINTER(_sz)]),
     "diagpu_spgemm_symbolic": (C.c_int, [
         _i32,

@@ -29,13 +29,15 @@ class KrylovResult:
 
 
 class KrylovWorkspace:
-    """Device workspace for n x n operators and up to m steps (reusable)."""
+    """Device workspace for n x n operators and up to m steps (reusable), and
+    the pinned host buffer (2m+1 doubles) that T_m's entries come back in."""
 
     def __init__(self, n: int, m: int, device="cuda"):
         b = C.c_size_t(0)
         _lib.call("diagpu_expm_krylov_workspace", n, m, C.byref(b))
         self.n, self.m = n, m
         self.buf = torch.empty(b.value, dtype=torch.uint8, device=device)
+        self.host = torch.empty(2 * m + 1, dtype=torch.float64, pin_memory=True)
 
 
 def expm_krylov(offsets: torch.Tensor, values: torch.Tensor, n: int, psi0: torch.Tensor,
@@ -58,7 +60,7 @@ def expm_krylov(offsets: torch.Tensor, values: torch.Tensor, n: int, psi0: torch
     beta = np.zeros(m, np.float64)
     info = _lib.KrylovInfo()
     _lib.call(name, C.byref(view), psi0.data_ptr(), float(t), int(m), out.data_ptr(),
-              workspace.buf.data_ptr(), workspace.buf.numel(),
+              workspace.buf.data_ptr(), workspace.buf.numel(), workspace.host.data_ptr(),
               alpha.ctypes.data_as(C.c_void_p), beta.ctypes.data_as(C.c_void_p),
               C.byref(info), _stream_handle(stream))
     return KrylovResult(out, info.steps, bool(info.breakdown), info.psi0_norm,

@@ -143,6 +143,9 @@ DIAGPU_API int diagpu_expm_krylov_workspace(int32_t n, int32_t m, size_t* bytes)
  * deterministic fp64 reductions, scalars kept on the device; one stream
  * synchronisation after the m steps to read alpha and beta, then exp(-i t T_m)
  * e_1 on the host in fp64 and one combine kernel (async on `stream`).
+ * host_scratch (optional) is a pinned host buffer (hipHostMalloc) of at least
+ * 2m+1 doubles for that readback; with NULL the copy goes through pageable
+ * memory, which the HIP runtime stages (tens of microseconds more per call).
  * alpha and beta (host, m entries each, optional) receive T_m's diagonal and
  * off-diagonal (zero past info->steps).  psi_t must not overlap psi_0 or the
  * workspace.
@@ -151,13 +154,15 @@ DIAGPU_API int diagpu_expm_krylov_workspace(int32_t n, int32_t m, size_t* bytes)
 DIAGPU_API int diagpu_expm_krylov_c64(const diagpu_recon_view_c64* H,
                                       const diagpu_complex64* psi0, double t, int32_t m,
                                       diagpu_complex64* psi_t, void* workspace,
-                                      size_t workspace_bytes, double* alpha, double* beta,
-                                      diagpu_krylov_info* info, void* stream);
+                                      size_t workspace_bytes, double* host_scratch,
+                                      double* alpha, double* beta, diagpu_krylov_info* info,
+                                      void* stream);
 DIAGPU_API int diagpu_expm_krylov_f32(const diagpu_recon_view_f32* H,
                                       const diagpu_complex64* psi0, double t, int32_t m,
                                       diagpu_complex64* psi_t, void* workspace,
-                                      size_t workspace_bytes, double* alpha, double* beta,
-                                      diagpu_krylov_info* info, void* stream);
+                                      size_t workspace_bytes, double* host_scratch,
+                                      double* alpha, double* beta, diagpu_krylov_info* info,
+                                      void* stream);
 
 /* ======================================================================
  * DIA x DIA SpGEMM, HM layout: C = A * B

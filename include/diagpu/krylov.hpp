@@ -13,6 +13,7 @@
 #pragma once
 
 #include <complex>
+#include <memory>
 #include <vector>
 
 #include "common.hpp"
@@ -35,6 +36,10 @@ public:
         size_t bytes = 0;
         check(diagpu_expm_krylov_workspace(n, max_steps, &bytes));
         ws_.resize(bytes);
+        double* h = nullptr;   // pinned: T_m's entries come back without a staged copy
+        check_hip(hipHostMalloc(reinterpret_cast<void**>(&h), (2 * static_cast<size_t>(max_steps) + 1) * sizeof(double)),
+                  "hipHostMalloc");
+        host_.reset(h);
     }
 
     int32_t n() const { return n_; }
@@ -45,7 +50,7 @@ public:
     {
         return finish(m, [&](int32_t mm, double* a, double* b, diagpu_krylov_info* info) {
             return diagpu_expm_krylov_c64(&H, as_c(d_psi0), t, mm, as_c(d_psi_t), ws_.data(),
-                                          ws_.size(), a, b, info, stream);
+                                          ws_.size(), host_.get(), a, b, info, stream);
         });
     }
 
@@ -58,7 +63,7 @@ public:
         return finish(m, [&](int32_t mm, double* a, double* b, diagpu_krylov_info* info) {
             return diagpu_expm_krylov_f32(reinterpret_cast<const diagpu_recon_view_f32*>(&H),
                                           as_c(d_psi0), t, mm, as_c(d_psi_t), ws_.data(),
-                                          ws_.size(), a, b, info, stream);
+                                          ws_.size(), host_.get(), a, b, info, stream);
         });
     }
 
@@ -91,8 +96,13 @@ private:
         return r;
     }
 
+    struct PinnedFree {
+        void operator()(double* p) const { (void)hipHostFree(p); }
+    };
+
     int32_t n_, m_;
     DeviceArray<unsigned char> ws_;
+    std::unique_ptr<double, PinnedFree> host_;
 };
 
 }  // namespace diagpu

@@ -144,14 +144,14 @@ def test_complex_and_krylov_argument_errors():
     rect = V(1000, 999, 1, fake.value, fake.value)
     call = lambda view, m, ws_bytes, t=1.0: _status(
         "diagpu_expm_krylov_c64", C.byref(view), fake, t, m, fake, fake, ws_bytes, None, None,
-        C.byref(info), None)
+        None, C.byref(info), None)
     assert call(rect, 10, b.value) == _lib.ERR_ARG                 # not square
     assert call(sq, 0, b.value) == _lib.ERR_ARG                    # m out of range
     assert call(sq, 10, b.value, float("nan")) == _lib.ERR_ARG     # t not finite
     assert call(sq, 10, b.value - 1) == _lib.ERR_CAPACITY          # workspace too small
     assert b"workspace" in _lib.load().diagpu_last_error()
     assert _status("diagpu_expm_krylov_f32", None, fake, 1.0, 10, fake, fake, b.value, None,
-                   None, C.byref(info), None) == _lib.ERR_ARG
+                   None, None, C.byref(info), None) == _lib.ERR_ARG
     assert _status("diagpu_promote_f32_c64", -1, fake, fake, None) == _lib.ERR_ARG
     assert _status("diagpu_promote_f32_c64", 5, None, fake, None) == _lib.ERR_ARG
     assert _status("diagpu_promote_f32_c64", 0, None, None, None) == _lib.OK

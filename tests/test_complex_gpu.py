@@ -206,6 +206,32 @@ def test_propagator_tiny_n(dev, n, complex_values):
     assert res.steps <= n and np.linalg.norm(got - want) <= 1e-5 * nrm
 
 
+def test_propagator_pageable_readback(dev):
+    """host_scratch = NULL (T_m's entries read back through pageable memory)
+    gives the same result, bit for bit, as the pinned buffer the Python
+    workspace passes."""
+    import ctypes as C
+    from diagpu_amd import _lib
+    from diagpu_amd.spmv import recon_view
+    rng = np.random.default_rng(31)
+    n, m, t = 3000, 16, 0.7
+    offs, vals, _ = _hermitian_band(rng, n, [0, 1, 9], True)
+    d_off = torch.as_tensor(offs, device=dev)
+    d_val = torch.as_tensor(vals.reshape(-1), device=dev)
+    psi0 = torch.as_tensor(_cx(rng, n), device=dev)
+    ws = KrylovWorkspace(n, m, dev)
+    pinned = expm_krylov(d_off, d_val, n, psi0, t, m, workspace=ws)
+    out = torch.empty_like(psi0)
+    info = _lib.KrylovInfo()
+    view = recon_view(d_off, d_val, n, n)
+    _lib.call("diagpu_expm_krylov_c64", C.byref(view), psi0.data_ptr(), t, m, out.data_ptr(),
+              ws.buf.data_ptr(), ws.buf.numel(), None, None, None, C.byref(info),
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert info.steps == pinned.steps and info.err_estimate == pinned.err_estimate
+    assert torch.equal(out, pinned.psi)
+
+
 def test_propagator_zero_time_and_zero_state(dev):
     rng = np.random.default_rng(9)
     n = 4097
