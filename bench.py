@@ -47,7 +47,7 @@ def parse_args(argv=None):
     ap.add_argument("--only", default="",
                     help="profiling aid: run just one workload (spmv2, spmv2d, spmv2c, "
                          "spmv2rc, spmv1, spmv3, spgemm4, spgemm5, spgemm4c, spgemm5c, taylor, krylov, "
-                         "propagator, propagator2d, copy) "
+                         "propagator, propagator2d, gemmdiag, gemmdiag20, copy) "
                          "and print its line")
     return ap.parse_args(argv)
 
@@ -414,6 +414,55 @@ def time_propagator(grid: str = "3d", order: int = 6, dt: float = 0.02, m: int =
                                  if kry_ms > apply_ms else None)}
 
 
+def time_gemm_diag(n: int = 4096, hb: int = 10, reps: int = 100):
+    """gemm_diag on row-packed operands (gemm_diag/gemm_diag.cu:9-15) with the
+    reference driver's default shape (n = 4096, offsets -hb..hb, values
+    U(0.5, 1.5), gemm_diag.cu:467-486): the plan once, then `reps` timed
+    numeric phases.  The reference kernel has no tensor-core instructions
+    (products in shared memory, a sequential reduction and atomicAdd); here
+    the product runs on the SpGEMM gather kernel, so MFMA utilisation is 0:
+    at <= 0.84 flop/B every config is HBM-bound, and fp32 MFMA peak equals
+    the fp32 vector peak on MI355X."""
+    import torch
+    from diagpu_amd.spgemm import gemm_diag
+    offs = list(range(-hb, hb + 1))
+    g = torch.Generator(device="cuda").manual_seed(42)
+
+    def packed():
+        D = torch.rand(len(offs), n, generator=g, device="cuda") + 0.5
+        t = torch.arange(n, device="cuda")
+        for i, d in enumerate(offs):       # zero where the row t + d leaves the matrix
+            D[i].masked_fill_((t + d < 0) | (t + d >= n), 0)
+        return D.reshape(-1).contiguous()
+    off = torch.tensor(offs, dtype=torch.int32, device="cuda")
+    DA, DB = packed(), packed()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    plan, C = gemm_diag(n, off, DA, off, DB)
+    torch.cuda.synchronize()
+    first_ms = (time.perf_counter() - t0) * 1e3
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for _ in range(3):
+        plan.numeric(DA, DB, C)
+    e0.record(stream)
+    for _ in range(reps):
+        plan.numeric(DA, DB, C)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    nnz = sum(n - abs(d) for d in offs)
+    alg = 4 * (2 * nnz + plan.info.c_nnz)
+    flops = plan.info.useful_flops
+    return {"workload": f"gemm_diag_n{n}_hb{hb}", "n": n, "A_diags": len(offs),
+            "B_diags": len(offs), "C_diags": plan.info.c_ndiag, "numeric_ms": round(ms, 5),
+            "first_call_ms": round(first_ms, 3), "GFLOPs": round(flops / (ms * 1e6), 1),
+            "GBs": round(alg / (ms * 1e6), 1), "frac_hbm": round(alg / (ms * 1e6) / HBM_PEAK_GBS, 4),
+            "alg_bytes": alg, "mfma_utilisation": 0.0,
+            "mfma_note": "no dense tile contraction: banded products at <= 0.84 flop/B are HBM-bound, "
+                         "and the reference kernel uses no tensor-core instructions"}
+
+
 def copy_calibration(steps: int):
     """A plain device copy of known size, for scaling rocprof FETCH/WRITE counters."""
     import torch
@@ -472,6 +521,10 @@ def main(argv=None) -> int:
             print(json.dumps(time_propagator("3d")), flush=True)
         elif w == "propagator2d":
             print(json.dumps(time_propagator("2d")), flush=True)
+        elif w == "gemmdiag":
+            print(json.dumps(time_gemm_diag()), flush=True)
+        elif w == "gemmdiag20":
+            print(json.dumps(time_gemm_diag(1 << 20, 10, 20)), flush=True)
         else:
             raise SystemExit(f"unknown --only {w}")
         return 0
@@ -540,6 +593,13 @@ def main(argv=None) -> int:
             torch.cuda.empty_cache()
         except Exception as e:
             extras["taylor_chain"] = {"error": repr(e)}
+        for n_gd, reps_gd in ((4096, 100), (1 << 20, 20)):
+            try:
+                rec = time_gemm_diag(n_gd, 10, reps_gd)
+                extras[rec["workload"]] = rec
+                log(f"extra {rec['workload']}: {rec['numeric_ms']} ms, {rec['GFLOPs']} GFLOP/s")
+            except Exception as e:
+                extras[f"gemm_diag_n{n_gd}"] = {"error": repr(e)}
         for grid in ("3d", "2d"):
             try:
                 rec = time_propagator(grid)

@@ -18,7 +18,8 @@
 // 16-byte aligned).  Each lane owns E consecutive positions: one aligned
 // 128-bit streaming store of C and, per plan entry, one 128-bit load each of A
 // and B (dword aligned).  A workgroup
-// takes a batch of 16 consecutive C diagonals of one row block: their
+// takes a batch of up to 16 consecutive C diagonals of one row block (fewer
+// when a small problem would otherwise leave CUs idle): their
 // metadata and plan entries (1.7 per diagonal on average) are resolved once
 // into LDS, then the flattened entry list is walked in chunks whose loads are
 // all in flight together, across C-diagonal boundaries.  The C stores are
@@ -34,6 +35,8 @@
 // owns the row blocks [x * nbx, (x + 1) * nbx) and its workgroups stride
 // through that range's items in order, so each XCD's L2 streams one
 // contiguous band of rows.  Each workgroup's item loop ends at a fixed count.
+#include <algorithm>
+
 #include "common.hpp"
 #include "elem.hpp"
 
@@ -69,13 +72,24 @@ struct PairRec {
     int32_t cover;    // 1: covers the whole item, 0: part of it, -1: none of it
 };
 
+// Item enumeration: XCD-partitioned (workgroup b on XCD b mod 8 strides
+// through that XCD's row blocks) or, for problems with few row blocks, flat
+// (workgroup b strides through all items).  `batch` (<= kBatch) C diagonals
+// per item.
+struct ItemSpace {
+    int32_t NB;           // row blocks
+    int32_t nb_per_xcd;   // XCD-partitioned: row blocks per XCD
+    int32_t wg_per_xcd;   // XCD-partitioned: workgroups per XCD
+    int32_t flat;         // 1: flat enumeration over gridDim.x workgroups
+    int32_t batch;        // C diagonals per item, 1..kBatch
+};
+
 template <typename T, int PC>
 __global__ __launch_bounds__(kBlock) void k_gather(
     const T* __restrict__ Av, const T* __restrict__ Bv,
     const int32_t* __restrict__ C_off, const int32_t* __restrict__ C_len,
     const int64_t* __restrict__ C_starts, int32_t nC, const int64_t* __restrict__ pair_ptr,
-    const diagpu_gpair* __restrict__ pairs, T* __restrict__ Cv, int32_t NB,
-    int32_t nb_per_xcd, int32_t wg_per_xcd)
+    const diagpu_gpair* __restrict__ pairs, T* __restrict__ Cv, ItemSpace is)
 {
     constexpr int E = epl<T>();
     constexpr int TB = item_positions<T>();
@@ -84,20 +98,30 @@ __global__ __launch_bounds__(kBlock) void k_gather(
     __shared__ int64_t ptr_s[kBatch + 1];
     __shared__ PairRec prec[kBlock];
 
-    const int xcd = (int)(blockIdx.x % kNumXcd);
-    const int l = (int)(blockIdx.x / kNumXcd);
-    const int rb0 = xcd * nb_per_xcd;
-    const int rb_end = (rb0 + nb_per_xcd) < NB ? (rb0 + nb_per_xcd) : NB;
+    int rb0, rb_end, l, stride;
+    if (is.flat) {
+        rb0 = 0;
+        rb_end = is.NB;
+        l = (int)blockIdx.x;
+        stride = (int)gridDim.x;
+    } else {
+        const int xcd = (int)(blockIdx.x % kNumXcd);
+        rb0 = xcd * is.nb_per_xcd;
+        rb_end = (rb0 + is.nb_per_xcd) < is.NB ? (rb0 + is.nb_per_xcd) : is.NB;
+        l = (int)(blockIdx.x / kNumXcd);
+        stride = is.wg_per_xcd;
+    }
     if (rb0 >= rb_end || nC <= 0) return;
-    const int nbat = (nC + kBatch - 1) / kBatch;
+    const int batch = is.batch;
+    const int nbat = (nC + batch - 1) / batch;
     const int t = (int)threadIdx.x;
     const int64_t p_lane = (int64_t)t * E;
     const int64_t nwork = (int64_t)(rb_end - rb0) * nbat;
 
-    for (int64_t j = l; j < nwork; j += wg_per_xcd) {
+    for (int64_t j = l; j < nwork; j += stride) {
         const int rb = rb0 + (int)(j / nbat);
-        const int kb = (int)(j % nbat) * kBatch;
-        const int gv = (nC - kb) < kBatch ? (nC - kb) : kBatch;
+        const int kb = (int)(j % nbat) * batch;
+        const int gv = (nC - kb) < batch ? (nC - kb) : batch;
 
         __syncthreads();   // previous batch done with drec/ptr_s/prec
         if (t <= gv) ptr_s[t] = pair_ptr[kb + t];
@@ -242,23 +266,47 @@ int numeric_launch(int32_t n, const T* A_vals, const T* B_vals, const int32_t* C
         return fail(DIAGPU_ERR_ARG, "%s: pairs or operand values are NULL", fn);
 
     constexpr int TB = item_positions<T>();
-    const int32_t NB = (int32_t)ceil_div<int64_t>((int64_t)n + epl<T>() - 1, TB);
-    const int32_t nb_per_xcd = ceil_div<int32_t>(NB, kNumXcd);
+    ItemSpace is;
+    is.NB = (int32_t)ceil_div<int64_t>((int64_t)n + epl<T>() - 1, TB);
+    is.nb_per_xcd = ceil_div<int32_t>(is.NB, kNumXcd);
     // Many C diagonals (wide operands): 4-entry chunks, 4 workgroups per CU;
     // few: 8-entry chunks and 8 workgroups per CU for more loads in flight.
     const bool wide = c_ndiag >= 1024;
-    const int64_t batches_per_xcd = (int64_t)nb_per_xcd * ceil_div<int64_t>(c_ndiag, kBatch);
-    int64_t wg = (int64_t)(cu_count() / kNumXcd) * (wide ? 4 : 8);
-    if (wg > batches_per_xcd) wg = batches_per_xcd;
-    if (wg < 1) wg = 1;
+    const int per_cu = wide ? 4 : 8;
+    const int64_t slots = (int64_t)cu_count() * per_cu;
+    // Small problems with heavy items: fewer C diagonals per item until the
+    // items can fill the GPU (a batch's entries are walked by one workgroup,
+    // chunk after chunk, so an item of many entries is a long serial chain;
+    // light items -- at most two chunks -- are left whole, their prologue
+    // being the larger cost), and flat item enumeration when there are too
+    // few row blocks to give every XCD a share.
+    const int pc = wide ? 4 : 8;
+    is.batch = kBatch;
+    while (is.batch > 1 && (int64_t)is.NB * ceil_div<int64_t>(c_ndiag, is.batch) < slots &&
+           std::min<int64_t>(is.batch, c_ndiag) * max_pairs > 2 * pc)
+        is.batch /= 2;
+    is.flat = is.NB < 4 * kNumXcd ? 1 : 0;
+    int64_t grid;
+    if (is.flat) {
+        grid = (int64_t)is.NB * ceil_div<int64_t>(c_ndiag, is.batch);
+        if (grid > slots) grid = slots;
+        is.wg_per_xcd = 0;
+    } else {
+        const int64_t items_per_xcd = (int64_t)is.nb_per_xcd * ceil_div<int64_t>(c_ndiag, is.batch);
+        int64_t wg = (int64_t)(cu_count() / kNumXcd) * per_cu;
+        if (wg > items_per_xcd) wg = items_per_xcd;
+        if (wg < 1) wg = 1;
+        is.wg_per_xcd = (int32_t)wg;
+        grid = wg * kNumXcd;
+    }
     if (wide)
-        hipLaunchKernelGGL((k_gather<T, 4>), dim3((unsigned)(wg * kNumXcd)), dim3(kBlock), 0,
+        hipLaunchKernelGGL((k_gather<T, 4>), dim3((unsigned)grid), dim3(kBlock), 0,
                            as_stream(stream), A_vals, B_vals, C_off, C_len, C_starts,
-                           (int32_t)c_ndiag, pair_ptr, pairs, C_vals, NB, nb_per_xcd, (int32_t)wg);
+                           (int32_t)c_ndiag, pair_ptr, pairs, C_vals, is);
     else
-        hipLaunchKernelGGL((k_gather<T, 8>), dim3((unsigned)(wg * kNumXcd)), dim3(kBlock), 0,
+        hipLaunchKernelGGL((k_gather<T, 8>), dim3((unsigned)grid), dim3(kBlock), 0,
                            as_stream(stream), A_vals, B_vals, C_off, C_len, C_starts,
-                           (int32_t)c_ndiag, pair_ptr, pairs, C_vals, NB, nb_per_xcd, (int32_t)wg);
+                           (int32_t)c_ndiag, pair_ptr, pairs, C_vals, is);
     return check_launch(fn);
 }
 
