@@ -57,6 +57,12 @@ class GPair(C.Structure):
                 ("bsh", C.c_int32), ("al", C.c_int32), ("bl", C.c_int32)]
 
 
+class BandInfo(C.Structure):
+    _fields_ = [("a_off_min", C.c_int32), ("a_off_max", C.c_int32),
+                ("rows_per_block", C.c_int32), ("eligible", C.c_int32),
+                ("lds_bytes", C.c_int64), ("n_pairs", C.c_int64)]
+
+
 class SpgemmInfo(C.Structure):
     _fields_ = [("c_ndiag", C.c_int64), ("c_nnz", C.c_int64), ("n_pairs", C.c_int64),
                 ("max_pairs", C.c_int64), ("useful_flops", C.c_int64)]
@@ -110,6 +116,11 @@ PROTOTYPES: dict[str, tuple] = {
     "diagpu_hm_to_recon_f32": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp]),
     "diagpu_hm_to_recon_c64": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp]),
     "diagpu_promote_f32_c64": (C.c_int, [_i64, _vp, _vp, _vp]),
+    "diagpu_spgemm_band_prepare": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _i32, _vp, _i64, _vp,
+                                             C.POINTER(BandInfo), _vp]),
+    "diagpu_spgemm_numeric_band_f32": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp,
+                                                 _vp, _vp, _i64, _vp, _vp, C.POINTER(BandInfo),
+                                                 _vp, _vp]),
 }
 
 _lib: C.CDLL | None = None

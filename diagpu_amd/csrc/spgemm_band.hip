@@ -1,0 +1,327 @@
+// DIA x DIA SpGEMM numeric phase for narrow bands, with the operands staged
+// in LDS: the LDS-tiled accumulation for products where each operand run is
+// used by many plan entries (contiguous bands such as gemm_diag's defaults,
+// gemm_diag/gemm_diag.cu:467-486: 21 x 21 diagonals, 10.8 entries per C
+// diagonal).  The gather kernel (spgemm_numeric.hip) re-reads both operand
+// runs from L2 for every entry; here a workgroup stages, for its block of
+// kRB rows i,
+//   A(i, i + da)          for every A diagonal          nA x kRB values
+//   B(w, w + db)          for every B diagonal and       nB x (kRB + span)
+//                         w in [i0 + min da, i0 + kRB + max da)
+// once, then evaluates every C diagonal's entries from LDS:
+//   C(i, i + dc) = sum over the plan entries (da, db) of dc
+//                  A(i, i + da) * B(i + da, i + dc).
+// Entries are taken in plan order (the pair order of
+// spmspm/gather_flat.cuh:231-255) with one fused multiply-add each, and a
+// term whose A element does not exist (row i + da outside [0, n)) is skipped
+// -- the gather kernel's exact sequence of roundings, so both kernels return
+// the same bits.  Row i's C element is written if column i + dc exists.
+//
+// Each plan entry becomes an int4 {A row's LDS offset, B window's LDS
+// offset + the entry's shift, da, 0} (diagpu_spgemm_band_prepare, once per
+// plan); the workgroup copies the table into LDS with the operands and reads
+// it with uniform addresses (as global loads the compiler kept the entries
+// in the vector memory queue, behind the staging loads).  The LDS footprint
+// is 4 (nA kRB + nB WB) + 16 n_pairs bytes, WB = kRB + span rounded up to a
+// multiple of 4, span = max da - min da.
+#include <algorithm>
+#include <type_traits>
+
+#include "common.hpp"
+
+namespace diagpu {
+namespace {
+
+constexpr int kRB = 256;                       // rows per workgroup (one per lane)
+constexpr int64_t kLdsBudget = 64 * 1024;      // keeps two workgroups per CU
+
+// Rows of one B diagonal's window in LDS: kRB + span, padded to a multiple
+// of 4 (keeps the entry table after the windows 16-byte aligned).
+__host__ __device__ constexpr int window_rows(int span) { return (kRB + span + 3) & ~3; }
+
+// LDS bytes of one workgroup: A rows, B windows, the plan's entries.
+int64_t band_lds_bytes(int32_t nA, int32_t nB, int64_t span, int64_t n_pairs)
+{
+    const int64_t wb = span > (int64_t)1 << 20 ? (int64_t)1 << 40 : window_rows((int)span);
+    return 4 * ((int64_t)nA * kRB + (int64_t)nB * wb) + 16 * n_pairs;
+}
+
+// entries[g] = {a kRB, b WB + (da - min da), da, 0}, a and b the indices of
+// pairs[g].ab in A_starts and of pairs[g].bb in B_starts (binary search: the
+// starts ascend), WB = window_rows(span).  span[0..1] = min, max da (k_span, which
+// runs first on the stream); span[2] is set if an entry matches no diagonal.
+__global__ __launch_bounds__(256) void k_band_prepare(const diagpu_gpair* __restrict__ pairs,
+                                                      int64_t n_pairs,
+                                                      const int32_t* __restrict__ A_off,
+                                                      const int64_t* __restrict__ A_starts,
+                                                      int32_t nA,
+                                                      const int64_t* __restrict__ B_starts,
+                                                      int32_t nB, int4* __restrict__ entries,
+                                                      int32_t* __restrict__ span)
+{
+    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (g >= n_pairs) return;
+    auto find = [](const int64_t* s, int32_t cnt, int64_t v) -> int {
+        int lo = 0, hi = cnt - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (s[mid] <= v) lo = mid; else hi = mid - 1;
+        }
+        return s[lo] == v ? lo : -1;
+    };
+    const diagpu_gpair p = pairs[g];
+    const int a = find(A_starts, nA, (int64_t)p.ab);
+    const int b = find(B_starts, nB, (int64_t)p.bb);
+    if (a < 0 || b < 0) {
+        span[2] = 1;   // every writer stores the same value
+        entries[g] = int4{0, 0, 0, 0};
+        return;
+    }
+    const int lo = span[0], wb = window_rows(span[1] - span[0]);
+    const int da = A_off[a];
+    entries[g] = int4{a * kRB, b * wb + (da - lo), da, 0};
+}
+
+// min and max of A's offsets, one workgroup
+__global__ __launch_bounds__(256) void k_span(const int32_t* __restrict__ off, int32_t cnt,
+                                              int32_t* __restrict__ out)
+{
+    __shared__ int lo_s[256], hi_s[256];
+    int lo = 0x7fffffff, hi = -0x7fffffff - 1;
+    for (int i = threadIdx.x; i < cnt; i += 256) {
+        lo = off[i] < lo ? off[i] : lo;
+        hi = off[i] > hi ? off[i] : hi;
+    }
+    lo_s[threadIdx.x] = lo;
+    hi_s[threadIdx.x] = hi;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) {
+            lo_s[threadIdx.x] = lo_s[threadIdx.x + s] < lo_s[threadIdx.x] ? lo_s[threadIdx.x + s] : lo_s[threadIdx.x];
+            hi_s[threadIdx.x] = hi_s[threadIdx.x + s] > hi_s[threadIdx.x] ? hi_s[threadIdx.x + s] : hi_s[threadIdx.x];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        out[0] = lo_s[0];
+        out[1] = hi_s[0];
+        out[2] = 0;   // bad-entry flag, set by k_band_prepare (launched next)
+    }
+}
+
+// Workgroup b on XCD b mod 8: each XCD owns a contiguous range of row
+// blocks, so neighbouring blocks (whose B windows overlap) share its L2.
+inline __device__ int block_of(int per_xcd)
+{
+    const int x = (int)(blockIdx.x % kNumXcd);
+    const int l = (int)(blockIdx.x / kNumXcd);
+    return x * per_xcd + l;
+}
+
+__global__ __launch_bounds__(kRB) void k_band(
+    int32_t n, const int32_t* __restrict__ A_off, const int64_t* __restrict__ A_starts, int32_t nA,
+    const float* __restrict__ Av, const int32_t* __restrict__ B_off,
+    const int64_t* __restrict__ B_starts, int32_t nB, const float* __restrict__ Bv,
+    const int32_t* __restrict__ C_off, const int64_t* __restrict__ C_starts, int32_t nC,
+    const int64_t* __restrict__ pair_ptr, const int4* __restrict__ entries, int32_t n_pairs,
+    float* __restrict__ Cv, int32_t a_min, int32_t a_max, int32_t blocks, int32_t per_xcd)
+{
+    extern __shared__ float lds[];
+    const int blk = block_of(per_xcd);
+    if (blk >= blocks) return;
+    const int WB = window_rows(a_max - a_min);      // B window rows
+    float* A_l = lds;                               // [nA][kRB]
+    float* B_l = lds + (int64_t)nA * kRB;           // [nB][WB]
+    int4* E_l = reinterpret_cast<int4*>(B_l + (int64_t)nB * WB);   // [n_pairs] plan entries
+    const int r = (int)threadIdx.x;
+    const int64_t i0 = (int64_t)blk * kRB;
+    const int64_t i = i0 + r;
+
+    // Staging, kS loads in flight per lane: diagonals are taken kS at a time
+    // (a uniform index, so their offsets and starts come from scalar loads),
+    // each lane loads its row of each from an always-valid address (the HM
+    // position clamped into the diagonal) and stores 0 where the element
+    // does not exist, so no load waits behind another or sits behind a
+    // branch.
+    constexpr int kS = 8;
+    auto stage = [&](const int32_t* __restrict__ off, const int64_t* __restrict__ starts,
+                     int cnt, const float* __restrict__ vals, float* dst, int pitch,
+                     int64_t row0, int q) {
+        const int64_t w = row0 + q;                 // this lane's row
+        for (int d0 = 0; d0 < cnt; d0 += kS) {
+            float v[kS];
+            bool ok[kS];
+#pragma unroll
+            for (int u = 0; u < kS; ++u) {
+                const int d = d0 + u < cnt ? d0 + u : cnt - 1;
+                const int o = off[d];
+                const int64_t len = (int64_t)n - (o < 0 ? -o : o);
+                int64_t pos = w + (o < 0 ? o : 0);     // HM position of (w, w + o)
+                ok[u] = d0 + u < cnt && w >= 0 && w < n && w + o >= 0 && w + o < n;
+                pos = pos < 0 ? 0 : (pos >= len ? len - 1 : pos);
+                v[u] = vals[starts[d] + pos];
+            }
+#pragma unroll
+            for (int u = 0; u < kS; ++u)
+                if (d0 + u < cnt) dst[(d0 + u) * pitch + q] = ok[u] ? v[u] : 0.f;
+        }
+    };
+    stage(A_off, A_starts, nA, Av, A_l, kRB, i0, r);                  // A: rows i0 + r
+    for (int q = r; q < WB; q += kRB)                                  // B: rows i0 + a_min + q
+        stage(B_off, B_starts, nB, Bv, B_l, WB, i0 + a_min, q);
+    // the plan's entries: read below with uniform LDS addresses (as global
+    // loads the compiler keeps them in the vector memory queue)
+    for (int g = r; g < n_pairs; g += kRB) E_l[g] = entries[g];
+    __syncthreads();
+
+    // every A element of this block exists, for every diagonal: no predicate
+    const bool interior =
+        i0 + kRB <= n && i0 + a_min >= 0 && i0 + kRB + (int64_t)a_max <= n;
+    // Wave w evaluates C diagonals w, w + 4, ... over all kRB rows, kR rows
+    // per lane (lane l: rows l, l + 64, ...): each entry's lookup then feeds
+    // kR independent pairs of LDS reads.
+    constexpr int kWaves = kRB / 64, kR = kRB / 64;
+    const int wave = r >> 6, lane = r & 63;
+    const int row0 = (int)i0 + lane;                 // n <= 2^30: rows fit int32
+    auto evaluate = [&](auto interior_tag) {
+        constexpr bool kInt = decltype(interior_tag)::value;
+        for (int kc = wave; kc < nC; kc += kWaves) {
+            const int dc = C_off[kc];
+            const int g0 = (int)pair_ptr[kc], g1 = (int)pair_ptr[kc + 1];
+            float acc[kR];
+#pragma unroll
+            for (int j = 0; j < kR; ++j) acc[j] = 0.f;
+            // entries in batches of kU: their LDS reads issued together,
+            // then the multiply-adds in plan order
+            constexpr int kU = 2;
+            auto step = [&](const int4& e, const float (&a)[kR], const float (&b)[kR]) {
+#pragma unroll
+                for (int j = 0; j < kR; ++j) {
+                    const float t = __builtin_fmaf(a[j], b[j], acc[j]);
+                    if constexpr (kInt) {
+                        acc[j] = t;
+                    } else {
+                        const int ra = row0 + 64 * j + e.z;   // column of the A element
+                        acc[j] = (ra >= 0 && ra < n) ? t : acc[j];
+                    }
+                }
+            };
+            int g = g0;
+            for (; g + kU <= g1; g += kU) {
+                int4 e[kU];
+                float a[kU][kR], b[kU][kR];
+#pragma unroll
+                for (int u = 0; u < kU; ++u) e[u] = E_l[g + u];
+#pragma unroll
+                for (int u = 0; u < kU; ++u)
+#pragma unroll
+                    for (int j = 0; j < kR; ++j) {
+                        a[u][j] = A_l[e[u].x + lane + 64 * j];
+                        b[u][j] = B_l[e[u].y + lane + 64 * j];
+                    }
+#pragma unroll
+                for (int u = 0; u < kU; ++u) step(e[u], a[u], b[u]);
+            }
+            for (; g < g1; ++g) {
+                const int4 e = E_l[g];
+                float a[kR], b[kR];
+#pragma unroll
+                for (int j = 0; j < kR; ++j) {
+                    a[j] = A_l[e.x + lane + 64 * j];
+                    b[j] = B_l[e.y + lane + 64 * j];
+                }
+                step(e, a, b);
+            }
+            float* __restrict__ cp = Cv + C_starts[kc] + (dc < 0 ? dc : 0);
+#pragma unroll
+            for (int j = 0; j < kR; ++j) {
+                const int ii = row0 + 64 * j;
+                if (ii < n && ii + dc >= 0 && ii + dc < n) __builtin_nontemporal_store(acc[j], cp + ii);
+            }
+        }
+    };
+    if (interior)
+        evaluate(std::true_type{});
+    else
+        evaluate(std::false_type{});
+}
+
+}  // namespace
+}  // namespace diagpu
+
+extern "C" {
+
+DIAGPU_API int diagpu_spgemm_band_prepare(int32_t n, const int32_t* A_off,
+                                          const int64_t* A_starts, int32_t nA,
+                                          const int64_t* B_starts, int32_t nB,
+                                          const diagpu_gpair* pairs, int64_t n_pairs,
+                                          int32_t* entries, diagpu_band_info* info, void* stream)
+{
+    using namespace diagpu;
+    const char* fn = "diagpu_spgemm_band_prepare";
+    if (!info) return fail(DIAGPU_ERR_ARG, "%s: info is NULL", fn);
+    *info = diagpu_band_info{};
+    if (n < 1 || nA < 1 || nB < 1 || n_pairs < 0)
+        return fail(DIAGPU_ERR_ARG, "%s: need n, nA, nB >= 1 and n_pairs >= 0", fn);
+    if (nA > 65535 || nB > 32767)
+        return fail(DIAGPU_ERR_ARG, "%s: at most 65535 A and 32767 B diagonals", fn);
+    if (!A_off || !A_starts || !B_starts || !entries || (n_pairs > 0 && !pairs))
+        return fail(DIAGPU_ERR_ARG, "%s: a pointer is NULL", fn);
+    hipStream_t s = as_stream(stream);
+    int32_t* dev = entries + 4 * n_pairs;   // caller's 4 scratch ints: A span, bad-entry flag
+    int32_t host[3] = {0, 0, 0};
+    hipLaunchKernelGGL(k_span, dim3(1), dim3(256), 0, s, A_off, nA, dev);
+    int st = check_launch(fn);
+    if (!st && n_pairs > 0) {
+        hipLaunchKernelGGL(k_band_prepare, dim3((unsigned)ceil_div<int64_t>(n_pairs, 256)),
+                           dim3(256), 0, s, pairs, n_pairs, A_off, A_starts, nA, B_starts, nB,
+                           reinterpret_cast<int4*>(entries), dev);
+        st = check_launch(fn);
+    }
+    if (!st) st = check_hip(hipMemcpyAsync(host, dev, sizeof(host), hipMemcpyDeviceToHost, s), fn);
+    if (!st) st = check_hip(hipStreamSynchronize(s), fn);
+    if (st) return st;
+    if (host[2]) return fail(DIAGPU_ERR_ARG, "%s: a plan entry's start is not an operand diagonal's start", fn);
+    info->a_off_min = host[0];
+    info->a_off_max = host[1];
+    info->rows_per_block = kRB;
+    info->n_pairs = n_pairs;
+    info->lds_bytes = band_lds_bytes(nA, nB, host[1] - host[0], n_pairs);
+    info->eligible = info->lds_bytes <= kLdsBudget && n_pairs <= 0x7fffffff ? 1 : 0;
+    return DIAGPU_OK;
+}
+
+DIAGPU_API int diagpu_spgemm_numeric_band_f32(
+    int32_t n, const int32_t* A_off, const int64_t* A_starts, int32_t nA, const float* A_vals,
+    const int32_t* B_off, const int64_t* B_starts, int32_t nB, const float* B_vals,
+    const int32_t* C_off, const int64_t* C_starts, int64_t c_ndiag, const int64_t* pair_ptr,
+    const int32_t* entries, const diagpu_band_info* info, float* C_vals, void* stream)
+{
+    using namespace diagpu;
+    const char* fn = "diagpu_spgemm_numeric_band_f32";
+    if (!info) return fail(DIAGPU_ERR_ARG, "%s: info is NULL", fn);
+    if (n < 1 || nA < 1 || nB < 1 || c_ndiag < 0 || c_ndiag > 2 * (int64_t)n - 1)
+        return fail(DIAGPU_ERR_ARG, "%s: bad sizes (n=%d nA=%d nB=%d c_ndiag=%lld)", fn, n, nA,
+                    nB, (long long)c_ndiag);
+    if (!info->eligible || info->rows_per_block != kRB || info->a_off_max < info->a_off_min ||
+        info->n_pairs < 0 || info->lds_bytes > kLdsBudget ||
+        info->lds_bytes != band_lds_bytes(nA, nB, (int64_t)info->a_off_max - info->a_off_min,
+                                          info->n_pairs))
+        return fail(DIAGPU_ERR_CAPACITY, "%s: info is not an eligible band_prepare result for "
+                    "these operands", fn);
+    const int64_t n_pairs = info->n_pairs;
+    if (c_ndiag == 0) return DIAGPU_OK;
+    if (!A_off || !A_starts || !A_vals || !B_off || !B_starts || !B_vals || !C_off ||
+        !C_starts || !pair_ptr || !entries || !C_vals)
+        return fail(DIAGPU_ERR_ARG, "%s: a pointer is NULL", fn);
+    const int32_t blocks = (int32_t)ceil_div<int64_t>(n, kRB);
+    const int32_t per_xcd = ceil_div<int32_t>(blocks, kNumXcd);
+    hipLaunchKernelGGL(k_band, dim3((unsigned)(per_xcd * kNumXcd)), dim3(kRB),
+                       (size_t)info->lds_bytes, as_stream(stream), n, A_off, A_starts, nA, A_vals,
+                       B_off, B_starts, nB, B_vals, C_off, C_starts, (int32_t)c_ndiag, pair_ptr,
+                       reinterpret_cast<const int4*>(entries), (int32_t)n_pairs, C_vals,
+                       info->a_off_min, info->a_off_max, blocks, per_xcd);
+    return check_launch(fn);
+}
+
+}  // extern "C"

@@ -55,10 +55,12 @@ class SpgemmPlan:
         self.lookup = (torch.empty(2 * self.n - 1, dtype=torch.int32, device=dev)
                        if want_lookup else None)
         self.info = _lib.SpgemmInfo()
+        self._band = None
         self.symbolic()
 
     def symbolic(self) -> None:
         A, B = self.A, self.B
+        self._band = None
         _lib.call("diagpu_spgemm_symbolic", self.n,
                   A.offsets.data_ptr(), A.lengths.data_ptr(), A.starts.data_ptr(),
                   A.offsets.numel(),
@@ -88,19 +90,62 @@ class SpgemmPlan:
         return raw.view(GPAIR_DTYPE)
 
     # numeric ---------------------------------------------------------------
-    def numeric(self, A_vals: torch.Tensor, B_vals: torch.Tensor, C_vals: torch.Tensor) -> None:
+    def band_info(self):
+        """(entries, BandInfo) of diagpu_spgemm_band_prepare for this plan
+        (computed once; one stream sync); entries int32 [4 n_pairs + 4]."""
+        if self._band is None:
+            A, B = self.A, self.B
+            pab = torch.empty(4 * self.info.n_pairs + 4, dtype=torch.int32,
+                              device=self.C_off.device)
+            info = _lib.BandInfo()
+            _lib.call("diagpu_spgemm_band_prepare", self.n, A.offsets.data_ptr(),
+                      A.starts.data_ptr(), A.offsets.numel(), B.starts.data_ptr(),
+                      B.offsets.numel(), self.pairs.data_ptr(), self.info.n_pairs,
+                      pab.data_ptr(), C.byref(info), _stream_handle(self.stream))
+            self._band = (pab, info)
+        return self._band
+
+    def uses_band(self, dtype=torch.float32) -> bool:
+        """The automatic choice: the LDS-staged band kernel for fp32 plans
+        whose staged operands fit, whose C diagonals average >= 3 entries
+        (each operand run then feeds several entries) and that have at least
+        1024 row blocks of 256 (one workgroup each: fewer leave CUs idle,
+        where the gather splits its work finer), else the gather."""
+        na, nb = self.A.offsets.numel(), self.B.offsets.numel()
+        if (dtype != torch.float32 or self.info.c_ndiag == 0 or na > 65535 or nb > 32767
+                or self.info.n_pairs < 3 * self.info.c_ndiag or self.n < 1024 * 256):
+            return False
+        return bool(self.band_info()[1].eligible)
+
+    def numeric(self, A_vals: torch.Tensor, B_vals: torch.Tensor, C_vals: torch.Tensor,
+                kernel: str = "auto") -> None:
         """C values for the plan's structure; float32 or complex64 (all three
-        tensors the same dtype)."""
+        tensors the same dtype).  kernel: "auto", "gather" (any plan) or
+        "band" (fp32, narrow bands; the same bits as the gather)."""
         dt = A_vals.dtype
         name = {torch.float32: "diagpu_spgemm_numeric_f32",
                 torch.complex64: "diagpu_spgemm_numeric_c64"}.get(dt)
         if name is None:
             raise TypeError(f"unsupported value dtype {dt}")
+        if kernel not in ("auto", "gather", "band"):
+            raise ValueError(f"unknown kernel {kernel!r}")
         _check_dev(A_vals, dt, "A_vals")
         _check_dev(B_vals, dt, "B_vals")
         _check_dev(C_vals, dt, "C_vals")
         if C_vals.numel() < self.info.c_nnz:
             raise ValueError(f"C_vals has {C_vals.numel()} elements, needs {self.info.c_nnz}")
+        if kernel == "band" or (kernel == "auto" and self.uses_band(dt)):
+            if dt != torch.float32:
+                raise TypeError("the band kernel is fp32")
+            pab, info = self.band_info()
+            A, B = self.A, self.B
+            _lib.call("diagpu_spgemm_numeric_band_f32", self.n, A.offsets.data_ptr(),
+                      A.starts.data_ptr(), A.offsets.numel(), A_vals.data_ptr(),
+                      B.offsets.data_ptr(), B.starts.data_ptr(), B.offsets.numel(),
+                      B_vals.data_ptr(), self.C_off.data_ptr(), self.C_starts.data_ptr(),
+                      self.info.c_ndiag, self.ptr.data_ptr(), pab.data_ptr(), C.byref(info),
+                      C_vals.data_ptr(), _stream_handle(self.stream))
+            return
         st = getattr(_lib.load(), name)(
             self.n, A_vals.data_ptr(), B_vals.data_ptr(), self.C_off.data_ptr(),
             self.C_len.data_ptr(), self.C_starts.data_ptr(), self.info.c_ndiag,
@@ -109,9 +154,10 @@ class SpgemmPlan:
         if st:
             _lib.check(st)
 
-    def multiply(self, A_vals: torch.Tensor, B_vals: torch.Tensor) -> torch.Tensor:
+    def multiply(self, A_vals: torch.Tensor, B_vals: torch.Tensor,
+                 kernel: str = "auto") -> torch.Tensor:
         Cv = torch.empty(max(1, self.info.c_nnz), dtype=A_vals.dtype, device=A_vals.device)
-        self.numeric(A_vals, B_vals, Cv)
+        self.numeric(A_vals, B_vals, Cv, kernel)
         return Cv[: self.info.c_nnz]
 
 

@@ -240,6 +240,46 @@ DIAGPU_API int diagpu_spgemm_numeric_c64(
     const int64_t* pair_ptr, const diagpu_gpair* pairs, int64_t max_pairs,
     diagpu_complex64* C_vals, void* stream);
 
+/* ----------------------------------------------------------------------
+ * Narrow bands: the numeric phase with the operands staged in LDS
+ * ---------------------------------------------------------------------- */
+
+/* What diagpu_spgemm_band_prepare found out about a plan. */
+typedef struct diagpu_band_info {
+    int32_t a_off_min, a_off_max;   /* smallest and largest A offset          */
+    int32_t rows_per_block;         /* rows one workgroup stages (rpb)         */
+    int32_t eligible;               /* 1: the staged operands fit in LDS       */
+    int64_t lds_bytes;              /* per workgroup: 4 (nA rpb + nB wb) +     */
+                                    /* 16 n_pairs, wb = rpb + span rounded up  */
+                                    /* to a multiple of 4                      */
+    int64_t n_pairs;                /* plan entries                            */
+} diagpu_band_info;
+
+/* For the band kernel, per plan (once): entries[4g .. 4g+3] = {a rpb,
+ * b wb + (da - min da), da, 0} for plan entry g, a and b the
+ * indices of its A and B diagonals (looked up from the entry's starts), and
+ * A's offset span in *info.  entries holds 4 n_pairs + 4 int32 (the last 4
+ * are scratch).  One stream synchronisation (to return *info).  No
+ * reference counterpart: the LDS-tiled form of the numeric phase below. */
+DIAGPU_API int diagpu_spgemm_band_prepare(int32_t n, const int32_t* A_off,
+                                          const int64_t* A_starts, int32_t nA,
+                                          const int64_t* B_starts, int32_t nB,
+                                          const diagpu_gpair* pairs, int64_t n_pairs,
+                                          int32_t* entries, diagpu_band_info* info,
+                                          void* stream);
+
+/* The numeric phase of diagpu_spgemm_numeric_f32 (same C, bit for bit) with
+ * each workgroup staging a block of A rows and the matching window of B rows
+ * in LDS and evaluating every C diagonal's plan entries from there: for
+ * products whose operand runs are used by many entries (narrow bands, e.g.
+ * gemm_diag's contiguous offsets).  info must be an eligible band_prepare
+ * result for these operands (else DIAGPU_ERR_CAPACITY). */
+DIAGPU_API int diagpu_spgemm_numeric_band_f32(
+    int32_t n, const int32_t* A_off, const int64_t* A_starts, int32_t nA, const float* A_vals,
+    const int32_t* B_off, const int64_t* B_starts, int32_t nB, const float* B_vals,
+    const int32_t* C_off, const int64_t* C_starts, int64_t c_ndiag, const int64_t* pair_ptr,
+    const int32_t* entries, const diagpu_band_info* info, float* C_vals, void* stream);
+
 /* ======================================================================
  * gemm_diag: row-packed operands, HM-layout C
  * ====================================================================== */

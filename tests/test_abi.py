@@ -155,3 +155,18 @@ def test_complex_and_krylov_argument_errors():
     assert _status("diagpu_promote_f32_c64", -1, fake, fake, None) == _lib.ERR_ARG
     assert _status("diagpu_promote_f32_c64", 5, None, fake, None) == _lib.ERR_ARG
     assert _status("diagpu_promote_f32_c64", 0, None, None, None) == _lib.OK
+    band = _lib.BandInfo()
+    assert _status("diagpu_spgemm_band_prepare", 0, fake, fake, 1, fake, 1, fake, 1, fake,
+                   C.byref(band), None) == _lib.ERR_ARG
+    assert _status("diagpu_spgemm_band_prepare", 100, fake, fake, 70000, fake, 1, fake, 1, fake,
+                   C.byref(band), None) == _lib.ERR_ARG
+    assert _status("diagpu_spgemm_band_prepare", 100, None, fake, 1, fake, 1, fake, 1, fake,
+                   C.byref(band), None) == _lib.ERR_ARG
+    # numeric_band needs an eligible, consistent info (validated before any launch)
+    band = _lib.BandInfo(0, 4, 256, 1, 4 * (3 * 256 + 2 * 260) + 16 * 7, 7)
+    call = lambda nA, info: _status("diagpu_spgemm_numeric_band_f32", 100, fake, fake, nA, fake,
+                                    fake, fake, 2, fake, fake, fake, 5, fake, fake, C.byref(info),
+                                    fake, None)
+    assert call(4, band) == _lib.ERR_CAPACITY    # lds_bytes does not match nA
+    band.eligible = 0
+    assert call(3, band) == _lib.ERR_CAPACITY

@@ -276,3 +276,62 @@ def test_square_of_spmv_configs(dev, oracle, cfg):
     ab1, _ = _hm_matvec(n, host(A), b1)
     _, bound = _hm_matvec(n, host(A), b1a)
     assert np.all(np.abs(rs - ab1) <= TOL * bound + 1e-300)
+
+
+@pytest.mark.parametrize("n,offs_a,offs_b", [
+    (4096, list(range(-10, 11)), list(range(-10, 11))),       # gemm_diag.cu:467-486 defaults
+    (37, [-36, -3, 0, 2, 36], [-30, -1, 0, 5, 36]),            # smaller than one block, edges
+    (1000, list(range(-40, 41, 3)), [-999, -7, 0, 1, 998]),    # narrow A, B spanning the matrix
+    (70001, list(range(-12, 13)), [-65000, -3, 0, 4, 65000]),  # ragged last block
+])
+def test_band_kernel_same_bits_as_gather(dev, oracle, n, offs_a, offs_b):
+    """The LDS-staged band kernel returns the gather kernel's C bit for bit
+    (same plan order, same fused multiply-adds, same skipped terms), and its
+    entries point every plan entry at its operand diagonals' LDS rows."""
+    A = workloads.hm_random(n, offs_a, 11, dev)
+    B = workloads.hm_random(n, offs_b, 12, dev)
+    plan = SpgemmPlan(A, B)
+    pab, info = plan.band_info()
+    assert info.eligible and info.a_off_min == min(offs_a) and info.a_off_max == max(offs_a)
+    pairs = plan.pairs_numpy()
+    a_st, b_st = A.starts.cpu().numpy(), B.starts.cpu().numpy()
+    a_idx = np.searchsorted(a_st, pairs["ab"].astype(np.int64))
+    b_idx = np.searchsorted(b_st, pairs["bb"].astype(np.int64))
+    da = np.asarray(offs_a)[a_idx]
+    wb = (256 + max(offs_a) - min(offs_a) + 3) // 4 * 4
+    got = pab[: 4 * plan.info.n_pairs].cpu().numpy().reshape(-1, 4)
+    assert np.array_equal(got[:, 0], a_idx * 256)
+    assert np.array_equal(got[:, 1], b_idx * wb + da - min(offs_a))
+    assert np.array_equal(got[:, 2], da) and not got[:, 3].any()
+    Cg = plan.multiply(A.values, B.values, kernel="gather")
+    Cb = plan.multiply(A.values, B.values, kernel="band")
+    assert torch.equal(Cg.view(torch.int32), Cb.view(torch.int32))
+    if n <= 5000:
+        ptr, c_len, c_st = plan.pair_ptr().cpu().numpy(), plan.c_lengths().cpu().numpy(), plan.c_starts().cpu().numpy()
+        want, ab = oracle.spgemm_pairs_f64(A.values.cpu().numpy(), B.values.cpu().numpy(), c_len,
+                                           c_st, ptr, pairs, 0, plan.info.c_ndiag)
+        check_values(Cb.cpu().numpy(), want, ab)
+
+
+def test_band_kernel_choice_and_capacity(dev):
+    """auto picks the band kernel for gemm_diag's contiguous bands and the
+    gather for config 4 (1.3 entries per C diagonal); a plan whose staged
+    operands exceed the LDS budget is refused with DIAGPU_ERR_CAPACITY."""
+    n = 1 << 18
+    A = workloads.hm_random(n, range(-10, 11), 1, dev)
+    assert SpgemmPlan(A, A).uses_band()
+    small = workloads.hm_random(8192, range(-10, 11), 1, dev)     # 32 row blocks: the gather
+    assert not SpgemmPlan(small, small).uses_band()
+    A4, B4 = workloads.spgemm_config(4, seed=4, device=dev)
+    p4 = SpgemmPlan(A4, B4)
+    assert not p4.uses_band()
+    Cg = p4.multiply(A4.values, B4.values, kernel="gather")
+    Cb = p4.multiply(A4.values, B4.values, kernel="band")      # eligible, just not chosen
+    assert torch.equal(Cg.view(torch.int32), Cb.view(torch.int32))
+    wide = workloads.hm_random(n, [-8000, 0, 8000], 3, dev)      # span 16000: B window too big
+    narrow = workloads.hm_random(n, range(-8, 9), 4, dev)
+    pw = SpgemmPlan(wide, narrow)
+    assert not pw.band_info()[1].eligible and not pw.uses_band()
+    with pytest.raises(_lib.DiagpuError) as e:                    # refused before any launch
+        pw.multiply(wide.values, narrow.values, kernel="band")
+    assert e.value.status == _lib.ERR_CAPACITY
