@@ -32,7 +32,7 @@
 namespace diagpu {
 namespace {
 
-constexpr int kRB = 256;                       // rows per workgroup (one per lane)
+constexpr int kRB = 256;                       // rows per block (one per lane)
 constexpr int64_t kLdsBudget = 64 * 1024;      // keeps two workgroups per CU
 
 // Rows of one B diagonal's window in LDS: kRB + span, padded to a multiple
@@ -44,6 +44,12 @@ int64_t band_lds_bytes(int32_t nA, int32_t nB, int64_t span, int64_t n_pairs)
 {
     const int64_t wb = span > (int64_t)1 << 20 ? (int64_t)1 << 40 : window_rows((int)span);
     return 4 * ((int64_t)nA * kRB + (int64_t)nB * wb) + 16 * n_pairs;
+}
+
+// The band kernel takes the plan: its LDS footprint fits the budget.
+bool band_fits(int64_t lds_bytes, int64_t n_pairs)
+{
+    return lds_bytes <= kLdsBudget && n_pairs <= 0x7fffffff;
 }
 
 // entries[g] = {a kRB, b WB + (da - min da), da, 0}, a and b the indices of
@@ -109,141 +115,172 @@ __global__ __launch_bounds__(256) void k_span(const int32_t* __restrict__ off, i
     }
 }
 
-// Workgroup b on XCD b mod 8: each XCD owns a contiguous range of row
-// blocks, so neighbouring blocks (whose B windows overlap) share its L2.
-inline __device__ int block_of(int per_xcd)
-{
-    const int x = (int)(blockIdx.x % kNumXcd);
-    const int l = (int)(blockIdx.x / kNumXcd);
-    return x * per_xcd + l;
-}
-
+// The persistent evaluation.  XCD x (workgroups b with b mod 8 == x) owns
+// the row blocks [x per_xcd, (x + 1) per_xcd) and its L workgroups take
+// blocks l, l + L, ... of that range in step, so the blocks in flight on one
+// XCD are neighbours whose B windows overlap in its L2.  Per block a
+// workgroup stages the operands with direct global-to-LDS loads (no
+// registers, so every load of the block is in flight at once and one wait
+// covers them all), then evaluates the block's C values from LDS.
+//
+// Staged elements that do not exist (rows outside [0, n), or columns
+// outside it) hold whatever the clamped load brought: a term reads B(i + da,
+// i + dc) only where C(i, i + dc) is written (so column i + dc exists) and
+// A(i, i + da) exists (so row i + da does), and the evaluation skips every
+// term whose A element is missing, so no such value reaches a C element.
 __global__ __launch_bounds__(kRB) void k_band(
     int32_t n, const int32_t* __restrict__ A_off, const int64_t* __restrict__ A_starts, int32_t nA,
     const float* __restrict__ Av, const int32_t* __restrict__ B_off,
     const int64_t* __restrict__ B_starts, int32_t nB, const float* __restrict__ Bv,
     const int32_t* __restrict__ C_off, const int64_t* __restrict__ C_starts, int32_t nC,
     const int64_t* __restrict__ pair_ptr, const int4* __restrict__ entries, int32_t n_pairs,
-    float* __restrict__ Cv, int32_t a_min, int32_t a_max, int32_t blocks, int32_t per_xcd)
+    float* __restrict__ Cv, int32_t a_min, int32_t a_max, int32_t blocks, int32_t per_xcd,
+    int32_t wg_per_xcd)
 {
     extern __shared__ float lds[];
-    const int blk = block_of(per_xcd);
-    if (blk >= blocks) return;
+    const int xcd = (int)(blockIdx.x % kNumXcd);
+    const int blk_end = (xcd + 1) * per_xcd < blocks ? (xcd + 1) * per_xcd : blocks;
+    int blk = xcd * per_xcd + (int)(blockIdx.x / kNumXcd);
+    if (blk >= blk_end) return;
     const int WB = window_rows(a_max - a_min);      // B window rows
     float* A_l = lds;                               // [nA][kRB]
     float* B_l = lds + (int64_t)nA * kRB;           // [nB][WB]
     int4* E_l = reinterpret_cast<int4*>(B_l + (int64_t)nB * WB);   // [n_pairs] plan entries
     const int r = (int)threadIdx.x;
-    const int64_t i0 = (int64_t)blk * kRB;
-    const int64_t i = i0 + r;
+    const int wave = __builtin_amdgcn_readfirstlane(r >> 6), lane = r & 63;
 
-    // Staging, kS loads in flight per lane: diagonals are taken kS at a time
-    // (a uniform index, so their offsets and starts come from scalar loads),
-    // each lane loads its row of each from an always-valid address (the HM
-    // position clamped into the diagonal) and stores 0 where the element
-    // does not exist, so no load waits behind another or sits behind a
-    // branch.
+    // the plan's entries, once per workgroup: read below with uniform LDS
+    // addresses (as global loads the compiler kept them in the vector memory
+    // queue, behind the staging loads)
+    for (int g = r; g < n_pairs; g += kRB) E_l[g] = entries[g];
+
+    // One wave's 64 rows of one diagonal: lane l loads the element of row
+    // w (its HM position clamped into the diagonal, so the address is
+    // always valid) into dst[l].  Positions and rows fit int32 (n <= 2^30).
+    auto load_row = [&](const float* __restrict__ vals, int64_t st, int o, int w, float* dst) {
+        const int len = n - (o < 0 ? -o : o);
+        const int pos = min(max(w + (o < 0 ? o : 0), 0), len - 1);   // HM position of (w, w + o)
+        __builtin_amdgcn_global_load_lds(vals + st + pos, dst, 4, 0, 0);
+    };
+    // Diagonals kS at a time: their offsets and starts are read (scalar
+    // loads, all in flight together) before any of their row loads is
+    // issued -- the compiler does not move a scalar load across a direct
+    // LDS load, so a load interleaved with them waits alone.
     constexpr int kS = 8;
-    auto stage = [&](const int32_t* __restrict__ off, const int64_t* __restrict__ starts,
-                     int cnt, const float* __restrict__ vals, float* dst, int pitch,
-                     int64_t row0, int q) {
-        const int64_t w = row0 + q;                 // this lane's row
-        for (int d0 = 0; d0 < cnt; d0 += kS) {
-            float v[kS];
-            bool ok[kS];
+    const int slots = (WB + kRB - 1) / kRB;         // kRB-row slots of a B window
+    auto stage = [&](int i0) {
+        for (int d0 = 0; d0 < nA; d0 += kS) {       // A: rows i0 + r
+            int o[kS];
+            int64_t st[kS];
 #pragma unroll
             for (int u = 0; u < kS; ++u) {
-                const int d = d0 + u < cnt ? d0 + u : cnt - 1;
-                const int o = off[d];
-                const int64_t len = (int64_t)n - (o < 0 ? -o : o);
-                int64_t pos = w + (o < 0 ? o : 0);     // HM position of (w, w + o)
-                ok[u] = d0 + u < cnt && w >= 0 && w < n && w + o >= 0 && w + o < n;
-                pos = pos < 0 ? 0 : (pos >= len ? len - 1 : pos);
-                v[u] = vals[starts[d] + pos];
+                const int d = d0 + u < nA ? d0 + u : nA - 1;
+                o[u] = A_off[d];
+                st[u] = A_starts[d];
             }
 #pragma unroll
             for (int u = 0; u < kS; ++u)
-                if (d0 + u < cnt) dst[(d0 + u) * pitch + q] = ok[u] ? v[u] : 0.f;
+                if (d0 + u < nA) load_row(Av, st[u], o[u], i0 + r, A_l + (d0 + u) * kRB + wave * 64);
+        }
+        for (int d0 = 0; d0 < nB; d0 += kS) {       // B: window rows i0 + a_min + q
+            int o[kS];
+            int64_t st[kS];
+#pragma unroll
+            for (int u = 0; u < kS; ++u) {
+                const int d = d0 + u < nB ? d0 + u : nB - 1;
+                o[u] = B_off[d];
+                st[u] = B_starts[d];
+            }
+            for (int sl = 0; sl < slots; ++sl) {
+                const int q = r + kRB * sl;
+                if (q < WB) {
+#pragma unroll
+                    for (int u = 0; u < kS; ++u)
+                        if (d0 + u < nB)
+                            load_row(Bv, st[u], o[u], i0 + a_min + q,
+                                     B_l + (d0 + u) * WB + kRB * sl + wave * 64);
+                }
+            }
         }
     };
-    stage(A_off, A_starts, nA, Av, A_l, kRB, i0, r);                  // A: rows i0 + r
-    for (int q = r; q < WB; q += kRB)                                  // B: rows i0 + a_min + q
-        stage(B_off, B_starts, nB, Bv, B_l, WB, i0 + a_min, q);
-    // the plan's entries: read below with uniform LDS addresses (as global
-    // loads the compiler keeps them in the vector memory queue)
-    for (int g = r; g < n_pairs; g += kRB) E_l[g] = entries[g];
-    __syncthreads();
 
-    // every A element of this block exists, for every diagonal: no predicate
-    const bool interior =
-        i0 + kRB <= n && i0 + a_min >= 0 && i0 + kRB + (int64_t)a_max <= n;
-    // Wave w evaluates C diagonals w, w + 4, ... over all kRB rows, kR rows
-    // per lane (lane l: rows l, l + 64, ...): each entry's lookup then feeds
-    // kR independent pairs of LDS reads.
     constexpr int kWaves = kRB / 64, kR = kRB / 64;
-    const int wave = r >> 6, lane = r & 63;
-    const int row0 = (int)i0 + lane;                 // n <= 2^30: rows fit int32
-    auto evaluate = [&](auto interior_tag) {
-        constexpr bool kInt = decltype(interior_tag)::value;
-        for (int kc = wave; kc < nC; kc += kWaves) {
-            const int dc = C_off[kc];
-            const int g0 = (int)pair_ptr[kc], g1 = (int)pair_ptr[kc + 1];
-            float acc[kR];
+    for (; blk < blk_end; blk += wg_per_xcd) {
+        const int64_t i0 = (int64_t)blk * kRB;
+        __syncthreads();                 // every wave is done with the previous block's LDS
+        stage((int)i0);
+        __builtin_amdgcn_s_waitcnt(0);   // this wave's direct loads have landed in LDS
+        __syncthreads();
+
+        // every A element of this block exists, for every diagonal: no predicate
+        const bool interior =
+            i0 + kRB <= n && i0 + a_min >= 0 && i0 + kRB + (int64_t)a_max <= n;
+        const int row0 = (int)i0 + lane;             // n <= 2^30: rows fit int32
+        // Wave w evaluates C diagonals w, w + 4, ... over all kRB rows, kR
+        // rows per lane (lane l: rows l, l + 64, ...): each entry's lookup
+        // then feeds kR independent pairs of LDS reads.
+        auto evaluate = [&](auto interior_tag) {
+            constexpr bool kInt = decltype(interior_tag)::value;
+            for (int kc = wave; kc < nC; kc += kWaves) {
+                const int dc = C_off[kc];
+                const int g0 = (int)pair_ptr[kc], g1 = (int)pair_ptr[kc + 1];
+                float acc[kR];
 #pragma unroll
-            for (int j = 0; j < kR; ++j) acc[j] = 0.f;
-            // entries in batches of kU: their LDS reads issued together,
-            // then the multiply-adds in plan order
-            constexpr int kU = 2;
-            auto step = [&](const int4& e, const float (&a)[kR], const float (&b)[kR]) {
-#pragma unroll
-                for (int j = 0; j < kR; ++j) {
-                    const float t = __builtin_fmaf(a[j], b[j], acc[j]);
-                    if constexpr (kInt) {
-                        acc[j] = t;
-                    } else {
-                        const int ra = row0 + 64 * j + e.z;   // column of the A element
-                        acc[j] = (ra >= 0 && ra < n) ? t : acc[j];
-                    }
-                }
-            };
-            int g = g0;
-            for (; g + kU <= g1; g += kU) {
-                int4 e[kU];
-                float a[kU][kR], b[kU][kR];
-#pragma unroll
-                for (int u = 0; u < kU; ++u) e[u] = E_l[g + u];
-#pragma unroll
-                for (int u = 0; u < kU; ++u)
+                for (int j = 0; j < kR; ++j) acc[j] = 0.f;
+                // entries in batches of kU: their LDS reads issued together,
+                // then the multiply-adds in plan order
+                constexpr int kU = 2;
+                auto step = [&](const int4& e, const float (&a)[kR], const float (&b)[kR]) {
 #pragma unroll
                     for (int j = 0; j < kR; ++j) {
-                        a[u][j] = A_l[e[u].x + lane + 64 * j];
-                        b[u][j] = B_l[e[u].y + lane + 64 * j];
+                        const float t = __builtin_fmaf(a[j], b[j], acc[j]);
+                        if constexpr (kInt) {
+                            acc[j] = t;
+                        } else {
+                            const int ra = row0 + 64 * j + e.z;   // column of the A element
+                            acc[j] = (ra >= 0 && ra < n) ? t : acc[j];
+                        }
                     }
+                };
+                int g = g0;
+                for (; g + kU <= g1; g += kU) {
+                    int4 e[kU];
+                    float a[kU][kR], b[kU][kR];
 #pragma unroll
-                for (int u = 0; u < kU; ++u) step(e[u], a[u], b[u]);
-            }
-            for (; g < g1; ++g) {
-                const int4 e = E_l[g];
-                float a[kR], b[kR];
+                    for (int u = 0; u < kU; ++u) e[u] = E_l[g + u];
+#pragma unroll
+                    for (int u = 0; u < kU; ++u)
+#pragma unroll
+                        for (int j = 0; j < kR; ++j) {
+                            a[u][j] = A_l[e[u].x + lane + 64 * j];
+                            b[u][j] = B_l[e[u].y + lane + 64 * j];
+                        }
+#pragma unroll
+                    for (int u = 0; u < kU; ++u) step(e[u], a[u], b[u]);
+                }
+                for (; g < g1; ++g) {
+                    const int4 e = E_l[g];
+                    float a[kR], b[kR];
+#pragma unroll
+                    for (int j = 0; j < kR; ++j) {
+                        a[j] = A_l[e.x + lane + 64 * j];
+                        b[j] = B_l[e.y + lane + 64 * j];
+                    }
+                    step(e, a, b);
+                }
+                float* __restrict__ cp = Cv + C_starts[kc] + (dc < 0 ? dc : 0);
 #pragma unroll
                 for (int j = 0; j < kR; ++j) {
-                    a[j] = A_l[e.x + lane + 64 * j];
-                    b[j] = B_l[e.y + lane + 64 * j];
+                    const int ii = row0 + 64 * j;
+                    if (ii < n && ii + dc >= 0 && ii + dc < n) __builtin_nontemporal_store(acc[j], cp + ii);
                 }
-                step(e, a, b);
             }
-            float* __restrict__ cp = Cv + C_starts[kc] + (dc < 0 ? dc : 0);
-#pragma unroll
-            for (int j = 0; j < kR; ++j) {
-                const int ii = row0 + 64 * j;
-                if (ii < n && ii + dc >= 0 && ii + dc < n) __builtin_nontemporal_store(acc[j], cp + ii);
-            }
-        }
-    };
-    if (interior)
-        evaluate(std::true_type{});
-    else
-        evaluate(std::false_type{});
+        };
+        if (interior)
+            evaluate(std::true_type{});
+        else
+            evaluate(std::false_type{});
+    }
 }
 
 }  // namespace
@@ -282,12 +319,14 @@ DIAGPU_API int diagpu_spgemm_band_prepare(int32_t n, const int32_t* A_off,
     if (!st) st = check_hip(hipStreamSynchronize(s), fn);
     if (st) return st;
     if (host[2]) return fail(DIAGPU_ERR_ARG, "%s: a plan entry's start is not an operand diagonal's start", fn);
+    if (host[0] <= -n || host[1] >= n)
+        return fail(DIAGPU_ERR_OFFSET, "%s: an A offset is outside (-n, n)", fn);
     info->a_off_min = host[0];
     info->a_off_max = host[1];
     info->rows_per_block = kRB;
     info->n_pairs = n_pairs;
     info->lds_bytes = band_lds_bytes(nA, nB, host[1] - host[0], n_pairs);
-    info->eligible = info->lds_bytes <= kLdsBudget && n_pairs <= 0x7fffffff ? 1 : 0;
+    info->eligible = band_fits(info->lds_bytes, n_pairs) ? 1 : 0;
     return DIAGPU_OK;
 }
 
@@ -303,10 +342,11 @@ DIAGPU_API int diagpu_spgemm_numeric_band_f32(
     if (n < 1 || nA < 1 || nB < 1 || c_ndiag < 0 || c_ndiag > 2 * (int64_t)n - 1)
         return fail(DIAGPU_ERR_ARG, "%s: bad sizes (n=%d nA=%d nB=%d c_ndiag=%lld)", fn, n, nA,
                     nB, (long long)c_ndiag);
-    if (!info->eligible || info->rows_per_block != kRB || info->a_off_max < info->a_off_min ||
-        info->n_pairs < 0 || info->lds_bytes > kLdsBudget ||
-        info->lds_bytes != band_lds_bytes(nA, nB, (int64_t)info->a_off_max - info->a_off_min,
-                                          info->n_pairs))
+    const int64_t span = (int64_t)info->a_off_max - info->a_off_min;
+    if (!info->eligible || info->rows_per_block != kRB || span < 0 || info->a_off_min <= -n ||
+        info->a_off_max >= n || info->n_pairs < 0 ||
+        info->lds_bytes != band_lds_bytes(nA, nB, span, info->n_pairs) ||
+        !band_fits(info->lds_bytes, info->n_pairs))
         return fail(DIAGPU_ERR_CAPACITY, "%s: info is not an eligible band_prepare result for "
                     "these operands", fn);
     const int64_t n_pairs = info->n_pairs;
@@ -316,11 +356,19 @@ DIAGPU_API int diagpu_spgemm_numeric_band_f32(
         return fail(DIAGPU_ERR_ARG, "%s: a pointer is NULL", fn);
     const int32_t blocks = (int32_t)ceil_div<int64_t>(n, kRB);
     const int32_t per_xcd = ceil_div<int32_t>(blocks, kNumXcd);
-    hipLaunchKernelGGL(k_band, dim3((unsigned)(per_xcd * kNumXcd)), dim3(kRB),
-                       (size_t)info->lds_bytes, as_stream(stream), n, A_off, A_starts, nA, A_vals,
-                       B_off, B_starts, nB, B_vals, C_off, C_starts, (int32_t)c_ndiag, pair_ptr,
+    // persistent: as many workgroups per XCD as fit at once, at most one
+    // per row block of its range
+    int per_cu = 0;
+    int st = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_band, kRB,
+                                                                    (size_t)info->lds_bytes), fn);
+    if (st) return st;
+    int64_t wg = (int64_t)(cu_count() / kNumXcd) * (per_cu > 0 ? per_cu : 1);
+    if (wg > per_xcd) wg = per_xcd;
+    hipLaunchKernelGGL(k_band, dim3((unsigned)(wg * kNumXcd)), dim3(kRB), (size_t)info->lds_bytes,
+                       as_stream(stream), n, A_off, A_starts, nA, A_vals, B_off, B_starts, nB,
+                       B_vals, C_off, C_starts, (int32_t)c_ndiag, pair_ptr,
                        reinterpret_cast<const int4*>(entries), (int32_t)n_pairs, C_vals,
-                       info->a_off_min, info->a_off_max, blocks, per_xcd);
+                       info->a_off_min, info->a_off_max, blocks, per_xcd, (int32_t)wg);
     return check_launch(fn);
 }
 

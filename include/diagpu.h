@@ -249,6 +249,7 @@ typedef struct diagpu_band_info {
     int32_t a_off_min, a_off_max;   /* smallest and largest A offset          */
     int32_t rows_per_block;         /* rows one workgroup stages (rpb)         */
     int32_t eligible;               /* 1: the staged operands fit in LDS       */
+                                    /* (lds_bytes <= 64 KiB)                   */
     int64_t lds_bytes;              /* per workgroup: 4 (nA rpb + nB wb) +     */
                                     /* 16 n_pairs, wb = rpb + span rounded up  */
                                     /* to a multiple of 4                      */
@@ -259,8 +260,9 @@ typedef struct diagpu_band_info {
  * b wb + (da - min da), da, 0} for plan entry g, a and b the
  * indices of its A and B diagonals (looked up from the entry's starts), and
  * A's offset span in *info.  entries holds 4 n_pairs + 4 int32 (the last 4
- * are scratch).  One stream synchronisation (to return *info).  No
- * reference counterpart: the LDS-tiled form of the numeric phase below. */
+ * are scratch).  One stream synchronisation (to return *info).
+ * DIAGPU_ERR_OFFSET if an A offset lies outside (-n, n).  No reference
+ * counterpart: the LDS-tiled form of the numeric phase below. */
 DIAGPU_API int diagpu_spgemm_band_prepare(int32_t n, const int32_t* A_off,
                                           const int64_t* A_starts, int32_t nA,
                                           const int64_t* B_starts, int32_t nB,

@@ -61,9 +61,10 @@ public:
     GemmDiag& operator=(const GemmDiag&) = delete;
     ~GemmDiag() { delete plan_; }
 
-    void run(const float* d_DA, const float* d_DB, float* d_C, hipStream_t stream = 0) const
+    void run(const float* d_DA, const float* d_DB, float* d_C, hipStream_t stream = 0,
+             NumericKernel kernel = NumericKernel::Auto) const
     {
-        plan_->numeric(d_DA, d_DB, d_C, stream);
+        plan_->numeric(d_DA, d_DB, d_C, stream, kernel);
     }
     const SpgemmPlan& plan() const { return *plan_; }
     const diagpu_spgemm_info& info() const { return plan_->info(); }

@@ -231,9 +231,19 @@ inline FlatPlan build_flat_plan(int n, const std::vector<int>& A_off, const std:
 
 namespace diagpu {
 
+// Which numeric kernel SpgemmPlan::numeric runs for fp32 values.
+//   Auto:   Band where the plan qualifies (see SpgemmPlan::uses_band), else Gather;
+//   Gather: diagpu_spgemm_numeric_f32, any plan;
+//   Band:   diagpu_spgemm_numeric_band_f32 (operands staged in LDS; narrow
+//           bands only, else diagpu::Error with DIAGPU_ERR_CAPACITY).
+// Both return the same bits.
+enum class NumericKernel { Auto, Gather, Band };
+
 // Device-resident C = A * B for HM operands whose offsets, lengths and starts
 // are device arrays: the plan is built once (symbolic), numeric() may run
-// many times on new values with the same structure.
+// many times on new values with the same structure.  The plan keeps its own
+// copies of the operands' offsets and starts; the caller's arrays need not
+// outlive the constructor.
 class SpgemmPlan {
 public:
     SpgemmPlan(int n, const int* dA_off, const int* dA_len, const int64_t* dA_starts, int a_ndiag,
@@ -257,11 +267,44 @@ public:
                                      ptr_.data(), pairs_.data(), pcap,
                                      want_lookup ? lookup_.data() : nullptr, ws.data(), ws_bytes,
                                      &info_, stream));
+        nA_ = a_ndiag;
+        nB_ = b_ndiag;
+        A_off_.resize(a_ndiag);
+        A_starts_.resize(a_ndiag);
+        B_off_.resize(b_ndiag);
+        B_starts_.resize(b_ndiag);
+        copy_d2d(A_off_.data(), dA_off, a_ndiag, stream);
+        copy_d2d(A_starts_.data(), dA_starts, a_ndiag, stream);
+        copy_d2d(B_off_.data(), dB_off, b_ndiag, stream);
+        copy_d2d(B_starts_.data(), dB_starts, b_ndiag, stream);
+        // The band kernel's tables for plans the automatic choice may take
+        // (one more stream synchronisation); others prepare on demand.
+        band_auto_ = info_.c_ndiag > 0 && a_ndiag <= 65535 && b_ndiag <= 32767 &&
+                     info_.n_pairs >= 3 * info_.c_ndiag && int64_t(n) >= 1024 * 256;
+        if (band_auto_) prepare_band(stream);
     }
 
-    // C_vals (device, info().c_nnz values) = A * B; asynchronous on `stream`.
-    void numeric(const float* dA_vals, const float* dB_vals, float* dC_vals, hipStream_t stream = 0) const
+    // True where NumericKernel::Auto runs the band kernel for fp32 values:
+    // the staged operands fit in LDS, the C diagonals average >= 3 plan
+    // entries (each staged operand run then feeds several entries) and there
+    // are >= 1024 row blocks of 256 (one workgroup each; fewer leave CUs
+    // idle, where the gather splits its work finer).
+    bool uses_band() const { return band_auto_ && band_.eligible; }
+
+    // C_vals (device, info().c_nnz values) = A * B; asynchronous on `stream`
+    // (NumericKernel::Band on a plan not yet prepared for it synchronises
+    // once to prepare).
+    void numeric(const float* dA_vals, const float* dB_vals, float* dC_vals, hipStream_t stream = 0,
+                 NumericKernel kernel = NumericKernel::Auto) const
     {
+        if (kernel == NumericKernel::Band && !band_prepared_) prepare_band(stream);
+        if (kernel == NumericKernel::Band || (kernel == NumericKernel::Auto && uses_band())) {
+            check(diagpu_spgemm_numeric_band_f32(
+                n_, A_off_.data(), A_starts_.data(), nA_, dA_vals, B_off_.data(), B_starts_.data(),
+                nB_, dB_vals, C_off_.data(), C_starts_.data(), info_.c_ndiag, ptr_.data(),
+                entries_.data(), &band_, dC_vals, stream));
+            return;
+        }
         check(diagpu_spgemm_numeric_f32(n_, dA_vals, dB_vals, C_off_.data(), C_len_.data(),
                                         C_starts_.data(), info_.c_ndiag, ptr_.data(), pairs_.data(),
                                         info_.max_pairs, dC_vals, stream));
@@ -285,11 +328,32 @@ public:
     const int* c_lookup() const { return lookup_.size() ? lookup_.data() : nullptr; }
 
 private:
+    template <typename T>
+    static void copy_d2d(T* dst, const T* src, int count, hipStream_t stream)
+    {
+        if (count > 0)
+            check_hip(hipMemcpyAsync(dst, src, size_t(count) * sizeof(T), hipMemcpyDeviceToDevice, stream),
+                      "hipMemcpyAsync");
+    }
+    void prepare_band(hipStream_t stream) const
+    {
+        entries_.resize(size_t(4 * info_.n_pairs + 4));
+        check(diagpu_spgemm_band_prepare(n_, A_off_.data(), A_starts_.data(), nA_, B_starts_.data(),
+                                         nB_, pairs_.data(), info_.n_pairs, entries_.data(), &band_,
+                                         stream));
+        band_prepared_ = true;
+    }
+
     int n_;
-    DeviceArray<int> C_off_, C_len_, lookup_;
-    DeviceArray<int64_t> C_starts_, ptr_;
+    int nA_ = 0, nB_ = 0;
+    DeviceArray<int> C_off_, C_len_, lookup_, A_off_, B_off_;
+    DeviceArray<int64_t> C_starts_, ptr_, A_starts_, B_starts_;
     DeviceArray<diagpu_gpair> pairs_;
     diagpu_spgemm_info info_{};
+    bool band_auto_ = false;
+    mutable DeviceArray<int32_t> entries_;
+    mutable diagpu_band_info band_{};
+    mutable bool band_prepared_ = false;
 };
 
 }  // namespace diagpu

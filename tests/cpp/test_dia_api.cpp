@@ -224,6 +224,84 @@ static void test_spgemm(const char* name, int n, std::vector<int> oa, std::vecto
     report((std::string(name) + " spgemm_hm values").c_str(), ok);
 }
 
+// The two numeric kernels of one plan: NumericKernel::Band (operands staged
+// in LDS) returns the gather's bits; Auto picks Band on the reference
+// driver's band (offsets -10..10, gemm_diag/gemm_diag.cu:467-486) at
+// n = 2^18 and the gather where the plan is too small; a plan whose staged
+// window does not fit refuses Band with DIAGPU_ERR_CAPACITY.
+static void test_band_kernel()
+{
+    std::mt19937 g(7);
+    std::vector<int> offs;
+    for (int d = -10; d <= 10; ++d) offs.push_back(d);
+    const int n = 1 << 18, P = (int)offs.size();
+    std::vector<float> D((size_t)P * n, 0.0f);
+    for (int i = 0; i < P; ++i) {
+        const int sr = offs[i] >= 0 ? 0 : -offs[i];
+        for (int p = 0; p < n - std::abs(offs[i]); ++p)
+            D[(size_t)i * n + sr + p] = 0.5f + (float)(g() % 65536) / 65536.0f;
+    }
+    diagpu::DeviceArray<int> doff(offs);
+    diagpu::DeviceArray<float> dD(D);
+    diagpu::GemmDiag gd(n, doff.data(), P, doff.data(), P);
+    report("band: Auto picks Band at n = 2^18", gd.plan().uses_band());
+    const size_t nnz = (size_t)gd.info().c_nnz;
+    diagpu::DeviceArray<float> c_band(nnz), c_gather(nnz), c_auto(nnz);
+    gd.run(dD.data(), dD.data(), c_gather.data(), 0, diagpu::NumericKernel::Gather);
+    gd.run(dD.data(), dD.data(), c_band.data(), 0, diagpu::NumericKernel::Band);
+    gd.run(dD.data(), dD.data(), c_auto.data());
+    diagpu::check_hip(hipDeviceSynchronize(), "sync");
+    const auto cg = c_gather.download(), cb = c_band.download(), ca = c_auto.download();
+    report("band: Band == Gather, bit for bit",
+           std::memcmp(cg.data(), cb.data(), nnz * sizeof(float)) == 0);
+    report("band: Auto == Band", std::memcmp(ca.data(), cb.data(), nnz * sizeof(float)) == 0);
+    // and the values against fp64 (the gather's bound)
+    const diagpu::CLayout L = diagpu::build_c_layout(n, offs, offs);
+    std::vector<double> want(L.total_c), absum(L.total_c);
+    orc_gemm_diag_f64(n, D.data(), offs.data(), P, D.data(), offs.data(), P, L.k_to_idx.data(),
+                      L.C_offsets.data(), want.data(), absum.data());
+    bool ok = (int64_t)nnz == L.total_c;
+    for (int64_t i = 0; ok && i < L.total_c; ++i)
+        ok &= std::fabs(cb[i] - want[i]) <= 1e-5 * absum[i] + 1e-300;
+    report("band: values", ok);
+
+    // a small plan: Auto takes the gather, Band forced still matches it
+    const int ns = 512;
+    std::vector<float> Ds((size_t)P * ns, 0.0f);
+    for (int i = 0; i < P; ++i) {
+        const int sr = offs[i] >= 0 ? 0 : -offs[i];
+        for (int p = 0; p < ns - std::abs(offs[i]); ++p)
+            Ds[(size_t)i * ns + sr + p] = 0.5f + (float)(g() % 65536) / 65536.0f;
+    }
+    diagpu::DeviceArray<float> dDs(Ds);
+    diagpu::GemmDiag small(ns, doff.data(), P, doff.data(), P);
+    report("band: Auto keeps the gather at n = 512", !small.plan().uses_band());
+    const size_t snz = (size_t)small.info().c_nnz;
+    diagpu::DeviceArray<float> s_band(snz), s_gather(snz);
+    small.run(dDs.data(), dDs.data(), s_gather.data(), 0, diagpu::NumericKernel::Gather);
+    small.run(dDs.data(), dDs.data(), s_band.data(), 0, diagpu::NumericKernel::Band);
+    diagpu::check_hip(hipDeviceSynchronize(), "sync");
+    const auto sg = s_gather.download(), sb = s_band.download();
+    report("band: forced Band == Gather at n = 512",
+           std::memcmp(sg.data(), sb.data(), snz * sizeof(float)) == 0);
+
+    // A span of 8000 rows: two B windows of 8256 floats exceed the LDS budget
+    std::vector<int> wide = {-4000, 4000};
+    const int nw = 5000;
+    std::vector<float> Dw((size_t)2 * nw, 1.0f);
+    diagpu::DeviceArray<int> dwo(wide);
+    diagpu::DeviceArray<float> dDw(Dw);
+    diagpu::GemmDiag gw(nw, dwo.data(), 2, dwo.data(), 2);
+    diagpu::DeviceArray<float> cw((size_t)std::max<int64_t>(1, gw.info().c_nnz));
+    int status = DIAGPU_OK;
+    try {
+        gw.run(dDw.data(), dDw.data(), cw.data(), 0, diagpu::NumericKernel::Band);
+    } catch (const diagpu::Error& e) {
+        status = e.status;
+    }
+    report("band: too wide a window -> DIAGPU_ERR_CAPACITY", status == DIAGPU_ERR_CAPACITY);
+}
+
 static void test_gemm_diag(const char* name, int n, std::vector<int> oa, std::vector<int> ob)
 {
     std::mt19937 g(42);
@@ -276,6 +354,7 @@ int main()
         test_spgemm("scattered", 2000, {-1900, -77, 0, 5, 640}, {-3, -2, 300, 1999, 1});
         test_gemm_diag("gemm_diag band", 512, {-3, -2, -1, 0, 1, 2, 3}, {-3, -2, -1, 0, 1, 2, 3});
         test_gemm_diag("gemm_diag scattered", 700, {-300, -9, 0, 33}, {-600, -1, 2, 5, 450});
+        test_band_kernel();
     } catch (const std::exception& e) {
         std::printf("  exception: %s\n", e.what());
         g_all = false;
