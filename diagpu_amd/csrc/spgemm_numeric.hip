@@ -14,8 +14,8 @@
 //
 // Work decomposition.  An item is (row block rb, C diagonal k): the 256 x E
 // positions of diagonal k whose matrix rows fall in block rb (E = 4 for fp32,
-// 2 for complex64; shifted by at most E - 1 so the item's first C element is
-// 16-byte aligned).  Each lane owns E consecutive positions: one aligned
+// 2 for complex64; shifted back by less than one 128-byte line so the item's
+// first C element starts a line).  Each lane owns E consecutive positions: one aligned
 // 128-bit streaming store of C and, per plan entry, one 128-bit load each of A
 // and B (dword aligned).  A workgroup
 // takes a batch of up to 16 consecutive C diagonals of one row block (fewer
@@ -49,6 +49,12 @@ constexpr int kBatch = 16;        // consecutive C diagonals per batch
 // Positions per lane (16 bytes of T) and per item.
 template <typename T> constexpr int epl() { return (int)(16 / sizeof(T)); }
 template <typename T> constexpr int item_positions() { return kBlock * epl<T>(); }
+// Positions per 128-byte line: items start on a line of C, so consecutive
+// items of a C diagonal split it at line boundaries.  (A line written in two
+// parts by two workgroups at different times costs a read-modify-write in
+// HBM: measured, 4 KB store chunks that start 16-byte- but not line-aligned
+// run at 3.5 TB/s against 5.4 aligned.)
+template <typename T> constexpr int line_positions() { return (int)(128 / sizeof(T)); }
 
 // acc + a * b over a lane's positions
 __device__ __forceinline__ float mac(float acc, float a, float b) { return __builtin_fmaf(a, b, acc); }
@@ -130,7 +136,7 @@ __global__ __launch_bounds__(kBlock) void k_gather(
             const int64_t cst = C_starts[kb + t];
             const int mc = dc < 0 ? dc : 0;
             DiagRec d;
-            d.P0 = (int64_t)rb * TB + mc - (int)((cst + mc) & (E - 1));
+            d.P0 = (int64_t)rb * TB + mc - (int)((cst + mc) & (line_positions<T>() - 1));
             d.cst = cst;
             d.len = C_len[kb + t];
             d.pad0 = 0;
@@ -149,7 +155,7 @@ __global__ __launch_bounds__(kBlock) void k_gather(
             const int64_t p = d.P0 + p_lane;
             T* __restrict__ cp = Cv + d.cst;
             if (d.P0 >= 0 && d.P0 + TB <= d.len) {
-                store_run_nt<T, E>(cp + p, acc);   // cst + P0 is a multiple of E: 16-byte aligned
+                store_run_nt<T, E>(cp + p, acc);   // cst + P0 starts a 128-byte line
             } else if (d.P0 < d.len && d.P0 + TB > 0) {
 #pragma unroll
                 for (int e = 0; e < E; ++e)
@@ -267,7 +273,7 @@ int numeric_launch(int32_t n, const T* A_vals, const T* B_vals, const int32_t* C
 
     constexpr int TB = item_positions<T>();
     ItemSpace is;
-    is.NB = (int32_t)ceil_div<int64_t>((int64_t)n + epl<T>() - 1, TB);
+    is.NB = (int32_t)ceil_div<int64_t>((int64_t)n + line_positions<T>() - 1, TB);
     is.nb_per_xcd = ceil_div<int32_t>(is.NB, kNumXcd);
     // Many C diagonals (wide operands): 4-entry chunks, 4 workgroups per CU;
     // few: 8-entry chunks and 8 workgroups per CU for more loads in flight.
