@@ -11,6 +11,14 @@
 // No reference counterpart: the reference describes a matrix-power chain
 // (spmspm/gather_flat.cuh:13-14,110-117) but ships no driver for it.  The
 // Taylor chain needs this to scale H and to add each power into the sum.
+//
+// Work: (Z diagonal, span) items, spans fastest, in contiguous ranges per
+// workgroup, so a workgroup looks up X's and Y's diagonal (two binary
+// searches of dependent scalar loads) only when its Z diagonal changes.  A
+// span is kRuns 16-byte runs per lane, all loaded before any store.  The
+// spans of a diagonal are shifted back by less than one 128-byte line so
+// that they start on a line of Z: a line written in two parts by two
+// workgroups at different times costs a read-modify-write in HBM.
 #include "common.hpp"
 #include "elem.hpp"
 
@@ -18,7 +26,11 @@ namespace diagpu {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kSpan = kBlock * 4;   // positions per workgroup iteration
+constexpr int kRuns = 4;   // 16-byte runs per lane per span
+
+template <typename T> constexpr int run_len() { return (int)(16 / sizeof(T)); }
+template <typename T> constexpr int span_len() { return kBlock * kRuns * run_len<T>(); }
+template <typename T> constexpr int line_len() { return (int)(128 / sizeof(T)); }
 
 __device__ __forceinline__ int find_offset(const int32_t* __restrict__ off, int cnt, int d)
 {
@@ -47,32 +59,68 @@ __global__ __launch_bounds__(kBlock) void k_axpby(
     const T* Xv, T alpha, const int32_t* __restrict__ Y_off,
     const int64_t* __restrict__ Y_starts, int32_t ny, const T* Yv, T beta,
     const int32_t* __restrict__ Z_off, const int64_t* __restrict__ Z_starts, int32_t nz,
-    T* Zv, int32_t span_blocks)
+    T* Zv, int32_t spans, int64_t per_wg)
 {
-    // blockIdx.x enumerates (Z diagonal, span) pairs, spans fastest.
-    for (int64_t w = blockIdx.x; w < (int64_t)nz * span_blocks; w += gridDim.x) {
-        const int z = (int)(w / span_blocks);
-        const int sb = (int)(w - (int64_t)z * span_blocks);
-        const int d = Z_off[z];
-        const int len = n - (d < 0 ? -d : d);
-        const int64_t p0 = (int64_t)sb * kSpan;
-        if (p0 >= len) continue;
-        const int xi = find_offset(X_off, nx, d);
-        const int yi = find_offset(Y_off, ny, d);
-        // Z may be X (or Y) itself, element for element: each lane reads its
-        // positions before it writes them, so the value pointers are not restrict.
-        const T* xp = xi >= 0 ? Xv + X_starts[xi] : nullptr;
-        const T* yp = yi >= 0 ? Yv + Y_starts[yi] : nullptr;
-        T* zp = Zv + Z_starts[z];
-        T xv[4], yv[4];
-        for (int e = 0; e < 4; ++e) {           // all loads first, then the stores
-            const int64_t p = p0 + (int64_t)e * kBlock + threadIdx.x;
-            xv[e] = (xp && p < len) ? xp[p] : zero_of<T>();
-            yv[e] = (yp && p < len) ? yp[p] : zero_of<T>();
+    constexpr int E = run_len<T>(), SPAN = span_len<T>(), L = line_len<T>();
+    typedef Run<T, E> V;
+    const int64_t total = (int64_t)nz * spans;
+    const int64_t w0 = (int64_t)blockIdx.x * per_wg;
+    const int64_t w1 = w0 + per_wg < total ? w0 + per_wg : total;
+    int zc = -1, len = 0;
+    int64_t shift = 0;
+    // Z may be X (or Y) itself, element for element: each lane reads its
+    // positions before it writes them, so the value pointers are not restrict.
+    const T* xp = nullptr;
+    const T* yp = nullptr;
+    T* zp = nullptr;
+    for (int64_t w = w0; w < w1; ++w) {
+        const int z = (int)(w / spans);
+        const int sb = (int)(w - (int64_t)z * spans);
+        if (z != zc) {
+            zc = z;
+            const int d = Z_off[z];
+            len = n - (d < 0 ? -d : d);
+            const int xi = find_offset(X_off, nx, d);
+            const int yi = find_offset(Y_off, ny, d);
+            xp = xi >= 0 ? Xv + X_starts[xi] : nullptr;
+            yp = yi >= 0 ? Yv + Y_starts[yi] : nullptr;
+            const int64_t zs = Z_starts[z];
+            zp = Zv + zs;
+            shift = zs & (L - 1);   // Z + zs - shift starts a line
         }
-        for (int e = 0; e < 4; ++e) {
-            const int64_t p = p0 + (int64_t)e * kBlock + threadIdx.x;
-            if (p < len) zp[p] = axpby_(alpha, xv[e], beta, yv[e]);
+        const int64_t p0 = (int64_t)sb * SPAN - shift;
+        if (p0 >= len) continue;
+        V xv[kRuns], yv[kRuns];
+#pragma unroll
+        for (int q = 0; q < kRuns; ++q) {           // all loads first, then the stores
+            const int64_t p = p0 + ((int64_t)q * kBlock + threadIdx.x) * E;
+            if (p >= 0 && p + E <= len) {
+#pragma unroll
+                for (int e = 0; e < E; ++e) xv[q].v[e] = yv[q].v[e] = zero_of<T>();
+                if (xp) xv[q] = load_run<T, E, false>(xp + p);
+                if (yp) yv[q] = load_run<T, E, false>(yp + p);
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const bool ok = p + e >= 0 && p + e < len;
+                    xv[q].v[e] = (xp && ok) ? xp[p + e] : zero_of<T>();
+                    yv[q].v[e] = (yp && ok) ? yp[p + e] : zero_of<T>();
+                }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < kRuns; ++q) {
+            const int64_t p = p0 + ((int64_t)q * kBlock + threadIdx.x) * E;
+            V r;
+#pragma unroll
+            for (int e = 0; e < E; ++e) r.v[e] = axpby_(alpha, xv[q].v[e], beta, yv[q].v[e]);
+            if (p >= 0 && p + E <= len) {
+                store_run<T, E>(zp + p, r);          // zs + p is a multiple of E: 16-byte aligned
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; ++e)
+                    if (p + e >= 0 && p + e < len) zp[p + e] = r.v[e];
+            }
         }
     }
 }
@@ -94,13 +142,15 @@ int axpby_launch(int32_t n, const int32_t* X_off, const int64_t* X_starts, int32
     if (ny > 0 && (!Y_off || !Y_starts || !Y_vals)) return fail(DIAGPU_ERR_ARG, "%s: Y arrays are NULL", fn);
     if (is_zero(alpha)) nx = 0;      // BLAS convention: a zero factor's operand is not read
     if (is_zero(beta)) ny = 0;
-    const int32_t spans = (int32_t)ceil_div<int64_t>(n, kSpan);
-    int64_t grid = (int64_t)nz * spans;
-    const int64_t cap = (int64_t)cu_count() * 16;
-    if (grid > cap) grid = cap;
+    // spans per diagonal: n positions plus a shift of less than one line
+    const int32_t spans = (int32_t)ceil_div<int64_t>((int64_t)n + line_len<T>() - 1, span_len<T>());
+    const int64_t total = (int64_t)nz * spans;
+    const int64_t slots = (int64_t)cu_count() * 8;
+    const int64_t per_wg = ceil_div<int64_t>(total, slots);
+    const int64_t grid = ceil_div<int64_t>(total, per_wg);
     hipLaunchKernelGGL(k_axpby<T>, dim3((unsigned)grid), dim3(kBlock), 0, as_stream(stream), n,
                        X_off, X_starts, nx, X_vals, alpha, Y_off, Y_starts, ny, Y_vals, beta,
-                       Z_off, Z_starts, nz, Z_vals, spans);
+                       Z_off, Z_starts, nz, Z_vals, spans, per_wg);
     return check_launch(fn);
 }
 

@@ -105,4 +105,14 @@ __device__ __forceinline__ void store_run_nt(T* p, const Run<T, R>& r)
     for (int i = 0; i < NQ; ++i) __builtin_nontemporal_store(q[i], reinterpret_cast<f4dw*>(p) + i);
 }
 
+template <typename T, int R>
+__device__ __forceinline__ void store_run(T* p, const Run<T, R>& r)
+{
+    constexpr int NQ = (int)(R * sizeof(T) / 16);
+    f4dw q[NQ];
+    __builtin_memcpy(q, &r, sizeof(r));
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) reinterpret_cast<f4dw*>(p)[i] = q[i];
+}
+
 }  // namespace diagpu
