@@ -307,6 +307,7 @@ def time_spgemm(cfg: int, seed: int, reps: int, complex_values: bool = False,
         "A_diags": A.ndiag, "B_diags": B.ndiag, "C_diags": plan.info.c_ndiag,
         "pairs": plan.info.n_pairs, "max_pairs_per_C": plan.info.max_pairs,
         "C_nnz": plan.info.c_nnz, "numeric_ms": round(ms, 5),
+        "kernel": plan.kernel_for(torch.complex64 if complex_values else torch.float32),
         "symbolic_ms": round(sym_ms, 5), "symbolic_wall_ms_first": round(sym_wall_ms, 3),
         "GFLOPs": round(flops / (ms * 1e6), 1), "useful_flops": flops,
         "GBs": round(alg / (ms * 1e6), 1), "frac_hbm": round(alg / (ms * 1e6) / HBM_PEAK_GBS, 4),
@@ -420,9 +421,10 @@ def time_gemm_diag(n: int = 4096, hb: int = 10, reps: int = 100):
     U(0.5, 1.5), gemm_diag.cu:467-486): the plan once, then `reps` timed
     numeric phases.  The reference kernel has no tensor-core instructions
     (products in shared memory, a sequential reduction and atomicAdd); here
-    the product runs on the SpGEMM gather kernel, so MFMA utilisation is 0:
-    at <= 0.84 flop/B every config is HBM-bound, and fp32 MFMA peak equals
-    the fp32 vector peak on MI355X."""
+    the product runs on the SpGEMM numeric kernels (the gather, or the
+    LDS-tiled band kernel at large n), so MFMA utilisation is 0: at
+    <= 0.84 flop/B every config is HBM-bound, and fp32 MFMA peak equals the
+    fp32 vector peak on MI355X."""
     import torch
     from diagpu_amd.spgemm import gemm_diag
     offs = list(range(-hb, hb + 1))
@@ -456,7 +458,8 @@ def time_gemm_diag(n: int = 4096, hb: int = 10, reps: int = 100):
     flops = plan.info.useful_flops
     return {"workload": f"gemm_diag_n{n}_hb{hb}", "n": n, "A_diags": len(offs),
             "B_diags": len(offs), "C_diags": plan.info.c_ndiag, "numeric_ms": round(ms, 5),
-            "first_call_ms": round(first_ms, 3), "GFLOPs": round(flops / (ms * 1e6), 1),
+            "kernel": plan.kernel_for(), "first_call_ms": round(first_ms, 3),
+            "GFLOPs": round(flops / (ms * 1e6), 1),
             "GBs": round(alg / (ms * 1e6), 1), "frac_hbm": round(alg / (ms * 1e6) / HBM_PEAK_GBS, 4),
             "alg_bytes": alg, "mfma_utilisation": 0.0,
             "mfma_note": "no dense tile contraction: banded products at <= 0.84 flop/B are HBM-bound, "

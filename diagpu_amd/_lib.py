@@ -121,7 +121,13 @@ PROTOTYPES: dict[str, tuple] = {
     "diagpu_spgemm_numeric_band_f32": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp,
                                                  _vp, _vp, _i64, _vp, _vp, C.POINTER(BandInfo),
                                                  _vp, _vp]),
+    "diagpu_spgemm_astat_prepare": (C.c_int, [_i32, _vp, _i32, _vp, _i64, _vp, _vp]),
+    "diagpu_spgemm_numeric_astat_f32": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp,
+                                                  _i64, _vp, _vp, _i64, _vp, _vp]),
 }
+
+# diagpu.h: DIAGPU_ASTAT_MAX_A
+ASTAT_MAX_A = 71
 
 _lib: C.CDLL | None = None
 

@@ -1,0 +1,238 @@
+// DIA x DIA SpGEMM numeric phase with A held in LDS ("A-stationary"), for
+// products whose A diagonals each feed many plan entries but whose B window
+// is too wide for the band kernel -- e.g. the square of a 64-diagonal band
+// spread over +-512 (4096 entries over 64 A diagonals: each A run is used by
+// 64 C diagonals).  The gather kernel (spgemm_numeric.hip) reads both
+// operand runs of every entry from L2; here a workgroup stages, for a block
+// of kRB rows i and the kLead rows before it,
+//   A(i, i + da)        for every A diagonal           nA x kStage values
+// with direct global-to-LDS loads, then evaluates every C diagonal of the
+// block: the A operand of each term comes from LDS and only the B operand
+// from memory, which halves the L2 -> CU operand stream.
+//
+//   C(i, i + dc) = sum over the plan entries (da, db) of dc
+//                  A(i, i + da) * B(i + da, i + dc)
+//
+// Entries are taken in plan order (spmspm/gather_flat.cuh:231-255) with one
+// fused multiply-add each, and a term is skipped where either operand lacks
+// the element: the gather kernel's exact sequence of roundings, so both
+// kernels return the same bits.
+//
+// Per C diagonal the rows a wave evaluates start kLead - s rows before the
+// block, s = (C start + min(dc, 0)) mod 32: the block's C values then start
+// on a 128-byte line, so no line is written in two parts by two workgroups
+// (a read-modify-write in HBM).  The kLead rows staged before the block
+// cover that shift.
+//
+// A workgroup has kWaves waves; wave w evaluates C diagonals w, w + kWaves,
+// ... over the block's kRB rows, 4 rows per lane (lane l: rows l, l + 64,
+// l + 128, l + 192 of the shifted window).  The plan entries come as records
+// {a, lo, hi, b} (diagpu_spgemm_astat_prepare): a the A diagonal's index,
+// [lo, hi) the C positions where both operands hold an element, b the B
+// index of C position 0.
+#include <climits>
+
+#include "common.hpp"
+
+namespace diagpu {
+namespace {
+
+constexpr int kRB = 256;                  // rows per block
+constexpr int kLead = 32;                 // rows staged before the block
+constexpr int kStage = kRB + kLead;       // staged rows per A diagonal
+constexpr int kWaves = 16;                // waves per workgroup
+constexpr int kMaxA = DIAGPU_ASTAT_MAX_A; // 4 kStage kMaxA <= 80 KiB: two workgroups per CU
+
+// records[g] = {a, lo, hi, b} for plan entry g; flag[0] set if an entry's A
+// start is no A diagonal's start, flag[1] if its B indices do not fit int32.
+__global__ __launch_bounds__(256) void k_astat_prepare(const diagpu_gpair* __restrict__ pairs,
+                                                       int64_t n_pairs,
+                                                       const int64_t* __restrict__ A_starts,
+                                                       int32_t nA, int4* __restrict__ records,
+                                                       int32_t* __restrict__ flag)
+{
+    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (g >= n_pairs) return;
+    const diagpu_gpair p = pairs[g];
+    int lo = 0, hi = nA - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (A_starts[mid] <= (int64_t)p.ab) lo = mid; else hi = mid - 1;
+    }
+    const int plo = max(0, max(-p.ash, -p.bsh));
+    const int phi = min(p.al - p.ash, p.bl - p.bsh);
+    const int64_t b = (int64_t)p.bb + p.bsh;
+    int4 r = int4{0, 0, 0, 0};
+    if (A_starts[lo] != (int64_t)p.ab) {
+        flag[0] = 1;   // every writer stores the same value
+    } else if (b < INT_MIN || b + phi > INT_MAX) {
+        flag[1] = 1;
+    } else {
+        r = int4{lo, plo, phi, (int)b};
+    }
+    records[g] = r;
+}
+
+__global__ __launch_bounds__(64) void k_astat_clear(int32_t* __restrict__ flag)
+{
+    if (threadIdx.x < 4) flag[threadIdx.x] = 0;
+}
+
+__global__ __launch_bounds__(64 * kWaves) void k_astat(
+    int32_t n, const int32_t* __restrict__ A_off, const int64_t* __restrict__ A_starts, int32_t nA,
+    const float* __restrict__ Av, const float* __restrict__ Bv, const int32_t* __restrict__ C_off,
+    const int32_t* __restrict__ C_len, const int64_t* __restrict__ C_starts, int32_t nC,
+    const int64_t* __restrict__ pair_ptr, const int4* __restrict__ records,
+    float* __restrict__ Cv, int32_t blocks, int32_t per_xcd)
+{
+    extern __shared__ float A_l[];   // [nA][kStage]: rows i0 - kLead .. i0 + kRB - 1
+    // workgroup b on XCD b mod 8: each XCD owns a contiguous range of blocks,
+    // so neighbouring blocks (whose B windows overlap) share its L2
+    const int blk = (int)(blockIdx.x % kNumXcd) * per_xcd + (int)(blockIdx.x / kNumXcd);
+    if (blk >= blocks) return;
+    const int r = (int)threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(r >> 6), lane = r & 63;
+    const int i0 = blk * kRB;                       // n <= 2^30: rows fit int32
+
+    // Stage A: one wave-instruction per 64 rows of a diagonal, each lane's
+    // HM position clamped into the diagonal (the address is always valid; a
+    // staged element that does not exist is never used: its terms are
+    // outside [lo, hi)).
+    for (int d = wave; d < nA; d += kWaves) {
+        const int o = A_off[d];
+        const int64_t st = A_starts[d];
+        const int len = n - (o < 0 ? -o : o);
+        for (int q0 = 0; q0 < kStage; q0 += 64) {
+            if (q0 + lane < kStage) {
+                const int w = i0 - kLead + q0 + lane;
+                const int pos = min(max(w + (o < 0 ? o : 0), 0), len - 1);
+                __builtin_amdgcn_global_load_lds(Av + st + pos, A_l + d * kStage + q0, 4, 0, 0);
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's direct loads have landed in LDS
+    __syncthreads();
+
+    for (int kc = wave; kc < nC; kc += kWaves) {
+        const int dc = C_off[kc];
+        const int len = C_len[kc];
+        const int64_t cst = C_starts[kc];
+        const int mc = dc < 0 ? dc : 0;
+        const int s = (int)((cst + mc) & 31);       // C(i0 - s, ...) starts a line
+        const int g0 = (int)pair_ptr[kc], g1 = (int)pair_ptr[kc + 1];
+        const int pb = i0 - s + lane + mc;          // C position of the lane's first row
+        const int ab = kLead - s + lane;            // its staged A row
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        // one term: B by a clamped (always valid) load, A from LDS, the
+        // multiply-add kept where both operands hold the element
+        auto term = [&](const int4& e, int hi, int j, float& b, float& a, bool& ok) {
+            const int p = pb + 64 * j;
+            ok = p >= e.y && p < hi;
+            b = Bv[(int64_t)e.w + min(max(p, e.y), e.z - 1)];
+            a = A_l[e.x * kStage + ab + 64 * j];
+        };
+        int g = g0;
+        for (; g + 2 <= g1; g += 2) {               // two entries' loads in flight
+            float bv[2][4], av[2][4];
+            bool ok[2][4];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int4 e = records[g + u];
+                const int hi = min(e.z, len);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) term(e, hi, j, bv[u][j], av[u][j], ok[u][j]);
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[j] = ok[u][j] ? __builtin_fmaf(av[u][j], bv[u][j], acc[j]) : acc[j];
+        }
+        if (g < g1) {
+            const int4 e = records[g];
+            const int hi = min(e.z, len);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float b, a;
+                bool ok;
+                term(e, hi, j, b, a, ok);
+                acc[j] = ok ? __builtin_fmaf(a, b, acc[j]) : acc[j];
+            }
+        }
+        float* __restrict__ cp = Cv + cst;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int p = pb + 64 * j;
+            if (p >= 0 && p < len) __builtin_nontemporal_store(acc[j], cp + p);
+        }
+    }
+}
+
+}  // namespace
+}  // namespace diagpu
+
+extern "C" {
+
+DIAGPU_API int diagpu_spgemm_astat_prepare(int32_t n, const int64_t* A_starts, int32_t nA,
+                                           const diagpu_gpair* pairs, int64_t n_pairs,
+                                           int32_t* records, void* stream)
+{
+    using namespace diagpu;
+    const char* fn = "diagpu_spgemm_astat_prepare";
+    if (n < 1 || nA < 1 || n_pairs < 0 || n_pairs > INT_MAX)
+        return fail(DIAGPU_ERR_ARG, "%s: need n, nA >= 1 and 0 <= n_pairs <= 2^31 - 1", fn);
+    if (!A_starts || !records || (n_pairs > 0 && !pairs))
+        return fail(DIAGPU_ERR_ARG, "%s: a pointer is NULL", fn);
+    hipStream_t s = as_stream(stream);
+    int32_t* flag = records + 4 * n_pairs;   // the caller's 4 scratch ints
+    int32_t host[2] = {0, 0};
+    hipLaunchKernelGGL(k_astat_clear, dim3(1), dim3(64), 0, s, flag);
+    int st = check_launch(fn);
+    if (!st && n_pairs > 0) {
+        hipLaunchKernelGGL(k_astat_prepare, dim3((unsigned)ceil_div<int64_t>(n_pairs, 256)),
+                           dim3(256), 0, s, pairs, n_pairs, A_starts, nA,
+                           reinterpret_cast<int4*>(records), flag);
+        st = check_launch(fn);
+    }
+    if (!st) st = check_hip(hipMemcpyAsync(host, flag, sizeof(host), hipMemcpyDeviceToHost, s), fn);
+    if (!st) st = check_hip(hipStreamSynchronize(s), fn);
+    if (st) return st;
+    if (host[0]) return fail(DIAGPU_ERR_ARG, "%s: a plan entry's A start is not an A diagonal's start", fn);
+    if (host[1]) return fail(DIAGPU_ERR_CAPACITY, "%s: B indices beyond 2^31 - 1", fn);
+    return DIAGPU_OK;
+}
+
+DIAGPU_API int diagpu_spgemm_numeric_astat_f32(
+    int32_t n, const int32_t* A_off, const int64_t* A_starts, int32_t nA, const float* A_vals,
+    const float* B_vals, const int32_t* C_off, const int32_t* C_len, const int64_t* C_starts,
+    int64_t c_ndiag, const int64_t* pair_ptr, const int32_t* records, int64_t n_pairs,
+    float* C_vals, void* stream)
+{
+    using namespace diagpu;
+    const char* fn = "diagpu_spgemm_numeric_astat_f32";
+    if (n < 1 || n > (1 << 30) || nA < 1 || c_ndiag < 0 || c_ndiag > 2 * (int64_t)n - 1 ||
+        n_pairs < 0 || n_pairs > INT_MAX)
+        return fail(DIAGPU_ERR_ARG, "%s: bad sizes (n=%d nA=%d c_ndiag=%lld n_pairs=%lld)", fn,
+                    n, nA, (long long)c_ndiag, (long long)n_pairs);
+    if (nA > kMaxA)
+        return fail(DIAGPU_ERR_CAPACITY, "%s: %d A diagonals, at most %d fit in LDS", fn, nA, kMaxA);
+    if (c_ndiag == 0) return DIAGPU_OK;
+    if (!A_off || !A_starts || !A_vals || !B_vals || !C_off || !C_len || !C_starts || !pair_ptr ||
+        !records || !C_vals)
+        return fail(DIAGPU_ERR_ARG, "%s: a pointer is NULL", fn);
+    const size_t lds = (size_t)nA * kStage * sizeof(float);
+    // more than 64 KiB of dynamic LDS must be allowed explicitly
+    const int st = check_hip(hipFuncSetAttribute((const void*)k_astat,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 kStage * kMaxA * (int)sizeof(float)), fn);
+    if (st) return st;
+    const int32_t blocks = (int32_t)ceil_div<int64_t>((int64_t)n + kLead, kRB);
+    const int32_t per_xcd = ceil_div<int32_t>(blocks, kNumXcd);
+    hipLaunchKernelGGL(k_astat, dim3((unsigned)(per_xcd * kNumXcd)), dim3(64 * kWaves), lds,
+                       as_stream(stream), n, A_off, A_starts, nA, A_vals, B_vals, C_off, C_len,
+                       C_starts, (int32_t)c_ndiag, pair_ptr,
+                       reinterpret_cast<const int4*>(records), C_vals, blocks, per_xcd);
+    return check_launch(fn);
+}
+
+}  // extern "C"

@@ -56,11 +56,13 @@ class SpgemmPlan:
                        if want_lookup else None)
         self.info = _lib.SpgemmInfo()
         self._band = None
+        self._astat = None
         self.symbolic()
 
     def symbolic(self) -> None:
         A, B = self.A, self.B
         self._band = None
+        self._astat = None
         _lib.call("diagpu_spgemm_symbolic", self.n,
                   A.offsets.data_ptr(), A.lengths.data_ptr(), A.starts.data_ptr(),
                   A.offsets.numel(),
@@ -117,26 +119,77 @@ class SpgemmPlan:
             return False
         return bool(self.band_info()[1].eligible)
 
+    def astat_records(self) -> torch.Tensor:
+        """Records of diagpu_spgemm_astat_prepare for this plan (computed
+        once; one stream sync); int32 [4 n_pairs + 4]."""
+        if self._astat is None:
+            A = self.A
+            rec = torch.empty(4 * self.info.n_pairs + 4, dtype=torch.int32,
+                              device=self.C_off.device)
+            _lib.call("diagpu_spgemm_astat_prepare", self.n, A.starts.data_ptr(),
+                      A.offsets.numel(), self.pairs.data_ptr(), self.info.n_pairs,
+                      rec.data_ptr(), _stream_handle(self.stream))
+            self._astat = rec
+        return self._astat
+
+    def uses_astat(self, dtype=torch.float32) -> bool:
+        """The automatic choice after the band kernel: the A-stationary kernel
+        for fp32 plans whose A diagonals fit its LDS (at most
+        DIAGPU_ASTAT_MAX_A), each feed at least 32 plan entries on average
+        (the reuse that pays for staging them) and that have at least 1024
+        row blocks of 256; B values must be addressable with int32."""
+        na = self.A.offsets.numel()
+        if not (dtype == torch.float32 and self.info.c_ndiag > 0 and na <= _lib.ASTAT_MAX_A
+                and self.info.n_pairs >= 32 * na and self.n >= 1024 * 256):
+            return False
+        try:
+            self.astat_records()
+        except _lib.DiagpuError as e:
+            if e.status != _lib.ERR_CAPACITY:    # B indices beyond int32: not this kernel
+                raise
+            return False
+        return True
+
+    def kernel_for(self, dtype=torch.float32) -> str:
+        """The kernel "auto" runs: "band", "astat" or "gather"."""
+        if self.uses_band(dtype):
+            return "band"
+        if self.uses_astat(dtype):
+            return "astat"
+        return "gather"
+
     def numeric(self, A_vals: torch.Tensor, B_vals: torch.Tensor, C_vals: torch.Tensor,
                 kernel: str = "auto") -> None:
         """C values for the plan's structure; float32 or complex64 (all three
-        tensors the same dtype).  kernel: "auto", "gather" (any plan) or
-        "band" (fp32, narrow bands; the same bits as the gather)."""
+        tensors the same dtype).  kernel: "auto" (kernel_for), "gather" (any
+        plan), "band" (fp32, narrow bands) or "astat" (fp32, at most
+        DIAGPU_ASTAT_MAX_A A diagonals); all return the same bits."""
         dt = A_vals.dtype
         name = {torch.float32: "diagpu_spgemm_numeric_f32",
                 torch.complex64: "diagpu_spgemm_numeric_c64"}.get(dt)
         if name is None:
             raise TypeError(f"unsupported value dtype {dt}")
-        if kernel not in ("auto", "gather", "band"):
+        if kernel not in ("auto", "gather", "band", "astat"):
             raise ValueError(f"unknown kernel {kernel!r}")
         _check_dev(A_vals, dt, "A_vals")
         _check_dev(B_vals, dt, "B_vals")
         _check_dev(C_vals, dt, "C_vals")
         if C_vals.numel() < self.info.c_nnz:
             raise ValueError(f"C_vals has {C_vals.numel()} elements, needs {self.info.c_nnz}")
-        if kernel == "band" or (kernel == "auto" and self.uses_band(dt)):
-            if dt != torch.float32:
-                raise TypeError("the band kernel is fp32")
+        if kernel == "auto":
+            kernel = self.kernel_for(dt)
+        if kernel in ("band", "astat") and dt != torch.float32:
+            raise TypeError(f"the {kernel} kernel is fp32")
+        if kernel == "astat":
+            rec = self.astat_records()
+            A = self.A
+            _lib.call("diagpu_spgemm_numeric_astat_f32", self.n, A.offsets.data_ptr(),
+                      A.starts.data_ptr(), A.offsets.numel(), A_vals.data_ptr(), B_vals.data_ptr(),
+                      self.C_off.data_ptr(), self.C_len.data_ptr(), self.C_starts.data_ptr(),
+                      self.info.c_ndiag, self.ptr.data_ptr(), rec.data_ptr(), self.info.n_pairs,
+                      C_vals.data_ptr(), _stream_handle(self.stream))
+            return
+        if kernel == "band":
             pab, info = self.band_info()
             A, B = self.A, self.B
             _lib.call("diagpu_spgemm_numeric_band_f32", self.n, A.offsets.data_ptr(),

@@ -282,6 +282,40 @@ DIAGPU_API int diagpu_spgemm_numeric_band_f32(
     const int32_t* C_off, const int64_t* C_starts, int64_t c_ndiag, const int64_t* pair_ptr,
     const int32_t* entries, const diagpu_band_info* info, float* C_vals, void* stream);
 
+/* ----------------------------------------------------------------------
+ * Medium bands: the numeric phase with A held in LDS
+ * ---------------------------------------------------------------------- */
+
+/* Largest A diagonal count diagpu_spgemm_numeric_astat_f32 takes (its
+ * workgroups hold 288 rows of every A diagonal in LDS, 80 KiB at most). */
+#define DIAGPU_ASTAT_MAX_A 71
+
+/* For the A-stationary kernel, per plan (once): records[4g .. 4g+3] =
+ * {a, lo, hi, b} for plan entry g: a the index of its A diagonal (looked up
+ * from the entry's A start), [lo, hi) = [max(0, -ash, -bsh), min(al - ash,
+ * bl - bsh)) the C positions where both operands hold an element, and
+ * b = bb + bsh the B index of C position 0.  records holds 4 n_pairs + 4
+ * int32 (the last 4 are scratch).  One stream synchronisation (to report
+ * errors): DIAGPU_ERR_ARG if an entry's A start is no A diagonal's start,
+ * DIAGPU_ERR_CAPACITY if a B index exceeds 2^31 - 1.  No reference
+ * counterpart: the A-stationary form of the numeric phase below. */
+DIAGPU_API int diagpu_spgemm_astat_prepare(int32_t n, const int64_t* A_starts, int32_t nA,
+                                           const diagpu_gpair* pairs, int64_t n_pairs,
+                                           int32_t* records, void* stream);
+
+/* The numeric phase of diagpu_spgemm_numeric_f32 (same C, bit for bit) with
+ * each workgroup holding one 256-row block of every A diagonal (plus the 32
+ * rows before it) in LDS and reading only B from memory: for products whose
+ * A diagonals each feed many plan entries but whose B window is too wide for
+ * the band kernel (e.g. the square of a 64-diagonal band over +-512).
+ * records from diagpu_spgemm_astat_prepare for this plan; nA at most
+ * DIAGPU_ASTAT_MAX_A (else DIAGPU_ERR_CAPACITY). */
+DIAGPU_API int diagpu_spgemm_numeric_astat_f32(
+    int32_t n, const int32_t* A_off, const int64_t* A_starts, int32_t nA, const float* A_vals,
+    const float* B_vals, const int32_t* C_off, const int32_t* C_len, const int64_t* C_starts,
+    int64_t c_ndiag, const int64_t* pair_ptr, const int32_t* records, int64_t n_pairs,
+    float* C_vals, void* stream);
+
 /* ======================================================================
  * gemm_diag: row-packed operands, HM-layout C
  * ====================================================================== */

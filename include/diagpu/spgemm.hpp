@@ -232,12 +232,15 @@ inline FlatPlan build_flat_plan(int n, const std::vector<int>& A_off, const std:
 namespace diagpu {
 
 // Which numeric kernel SpgemmPlan::numeric runs for fp32 values.
-//   Auto:   Band where the plan qualifies (see SpgemmPlan::uses_band), else Gather;
-//   Gather: diagpu_spgemm_numeric_f32, any plan;
-//   Band:   diagpu_spgemm_numeric_band_f32 (operands staged in LDS; narrow
-//           bands only, else diagpu::Error with DIAGPU_ERR_CAPACITY).
-// Both return the same bits.
-enum class NumericKernel { Auto, Gather, Band };
+//   Auto:        Band where the plan qualifies (SpgemmPlan::uses_band), else
+//                AStationary where it qualifies (uses_astat), else Gather;
+//   Gather:      diagpu_spgemm_numeric_f32, any plan;
+//   Band:        diagpu_spgemm_numeric_band_f32 (operands staged in LDS;
+//                narrow bands only, else diagpu::Error with DIAGPU_ERR_CAPACITY);
+//   AStationary: diagpu_spgemm_numeric_astat_f32 (A held in LDS; at most
+//                DIAGPU_ASTAT_MAX_A A diagonals, else DIAGPU_ERR_CAPACITY).
+// All return the same bits.
+enum class NumericKernel { Auto, Gather, Band, AStationary };
 
 // Device-resident C = A * B for HM operands whose offsets, lengths and starts
 // are device arrays: the plan is built once (symbolic), numeric() may run
@@ -282,6 +285,18 @@ public:
         band_auto_ = info_.c_ndiag > 0 && a_ndiag <= 65535 && b_ndiag <= 32767 &&
                      info_.n_pairs >= 3 * info_.c_ndiag && int64_t(n) >= 1024 * 256;
         if (band_auto_) prepare_band(stream);
+        // The A-stationary kernel's records where the automatic choice may
+        // take it: A fits its LDS and each A diagonal feeds >= 32 entries.
+        astat_auto_ = !uses_band() && info_.c_ndiag > 0 && a_ndiag <= DIAGPU_ASTAT_MAX_A &&
+                      info_.n_pairs >= 32 * int64_t(a_ndiag) && int64_t(n) >= 1024 * 256;
+        if (astat_auto_) {
+            try {
+                prepare_astat(stream);
+            } catch (const Error& e) {
+                if (e.status != DIAGPU_ERR_CAPACITY) throw;   // B indices beyond int32
+                astat_auto_ = false;
+            }
+        }
     }
 
     // True where NumericKernel::Auto runs the band kernel for fp32 values:
@@ -290,15 +305,31 @@ public:
     // are >= 1024 row blocks of 256 (one workgroup each; fewer leave CUs
     // idle, where the gather splits its work finer).
     bool uses_band() const { return band_auto_ && band_.eligible; }
+    // True where NumericKernel::Auto runs the A-stationary kernel: the band
+    // kernel does not take the plan, A has at most DIAGPU_ASTAT_MAX_A
+    // diagonals, each feeding >= 32 plan entries on average, and there are
+    // >= 1024 row blocks of 256.
+    bool uses_astat() const { return astat_auto_; }
 
     // C_vals (device, info().c_nnz values) = A * B; asynchronous on `stream`
-    // (NumericKernel::Band on a plan not yet prepared for it synchronises
-    // once to prepare).
+    // (NumericKernel::Band or AStationary on a plan not yet prepared for it
+    // synchronises once to prepare).
     void numeric(const float* dA_vals, const float* dB_vals, float* dC_vals, hipStream_t stream = 0,
                  NumericKernel kernel = NumericKernel::Auto) const
     {
+        if (kernel == NumericKernel::Auto)
+            kernel = uses_band() ? NumericKernel::Band
+                                 : (uses_astat() ? NumericKernel::AStationary : NumericKernel::Gather);
+        if (kernel == NumericKernel::AStationary) {
+            if (!astat_prepared_) prepare_astat(stream);
+            check(diagpu_spgemm_numeric_astat_f32(
+                n_, A_off_.data(), A_starts_.data(), nA_, dA_vals, dB_vals, C_off_.data(),
+                C_len_.data(), C_starts_.data(), info_.c_ndiag, ptr_.data(), records_.data(),
+                info_.n_pairs, dC_vals, stream));
+            return;
+        }
         if (kernel == NumericKernel::Band && !band_prepared_) prepare_band(stream);
-        if (kernel == NumericKernel::Band || (kernel == NumericKernel::Auto && uses_band())) {
+        if (kernel == NumericKernel::Band) {
             check(diagpu_spgemm_numeric_band_f32(
                 n_, A_off_.data(), A_starts_.data(), nA_, dA_vals, B_off_.data(), B_starts_.data(),
                 nB_, dB_vals, C_off_.data(), C_starts_.data(), info_.c_ndiag, ptr_.data(),
@@ -343,6 +374,13 @@ private:
                                          stream));
         band_prepared_ = true;
     }
+    void prepare_astat(hipStream_t stream) const
+    {
+        records_.resize(size_t(4 * info_.n_pairs + 4));
+        check(diagpu_spgemm_astat_prepare(n_, A_starts_.data(), nA_, pairs_.data(), info_.n_pairs,
+                                          records_.data(), stream));
+        astat_prepared_ = true;
+    }
 
     int n_;
     int nA_ = 0, nB_ = 0;
@@ -351,6 +389,9 @@ private:
     DeviceArray<diagpu_gpair> pairs_;
     diagpu_spgemm_info info_{};
     bool band_auto_ = false;
+    bool astat_auto_ = false;
+    mutable DeviceArray<int32_t> records_;
+    mutable bool astat_prepared_ = false;
     mutable DeviceArray<int32_t> entries_;
     mutable diagpu_band_info band_{};
     mutable bool band_prepared_ = false;

@@ -6,6 +6,7 @@
 // Integer outputs (Recon layout, C structure, lookup, pair plan) are compared
 // bit for bit with the CPU oracle (oracle/liboracle.so, test infrastructure);
 // values against an fp64 reference with |err| <= 1e-5 * sum |terms|.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <unistd.h>
@@ -302,6 +303,48 @@ static void test_band_kernel()
     report("band: too wide a window -> DIAGPU_ERR_CAPACITY", status == DIAGPU_ERR_CAPACITY);
 }
 
+// The A-stationary kernel through diagpu::SpgemmPlan: the square of a
+// 40-diagonal band spread over +-256 at n = 2^18 (1600 plan entries, 40 per
+// A diagonal) takes it under Auto, and every kernel returns the gather's
+// bits.
+static void test_astat_kernel()
+{
+    const int n = 1 << 18;
+    std::mt19937 g(11);
+    std::vector<int> offs = {0};
+    while (offs.size() < 40) {
+        const int d = (int)(g() % 513) - 256;
+        if (std::find(offs.begin(), offs.end(), d) == offs.end()) offs.push_back(d);
+    }
+    std::sort(offs.begin(), offs.end());
+    const int K = (int)offs.size();
+    std::vector<int> lens(K);
+    std::vector<int64_t> starts(K);
+    int64_t tot = 0;
+    for (int k = 0; k < K; ++k) {
+        lens[k] = n - std::abs(offs[k]);
+        starts[k] = tot;
+        tot += lens[k];
+    }
+    std::vector<float> vals((size_t)tot);
+    for (auto& v : vals) v = -1.0f + 2.0f * (float)(g() % 65536) / 65536.0f;
+    diagpu::DeviceArray<int> doff(offs), dlen(lens);
+    diagpu::DeviceArray<int64_t> dst(starts);
+    diagpu::DeviceArray<float> dv(vals);
+    diagpu::SpgemmPlan plan(n, doff.data(), dlen.data(), dst.data(), K, doff.data(), dlen.data(),
+                            dst.data(), K);
+    report("astat: Auto picks the A-stationary kernel", plan.uses_astat() && !plan.uses_band());
+    const size_t nnz = (size_t)plan.info().c_nnz;
+    diagpu::DeviceArray<float> cg(nnz), ca(nnz), cf(nnz);
+    plan.numeric(dv.data(), dv.data(), cg.data(), 0, diagpu::NumericKernel::Gather);
+    plan.numeric(dv.data(), dv.data(), ca.data());
+    plan.numeric(dv.data(), dv.data(), cf.data(), 0, diagpu::NumericKernel::AStationary);
+    diagpu::check_hip(hipDeviceSynchronize(), "sync");
+    const auto hg = cg.download(), ha = ca.download(), hf = cf.download();
+    report("astat: Auto == Gather, bit for bit", std::memcmp(hg.data(), ha.data(), nnz * 4) == 0);
+    report("astat: AStationary == Gather", std::memcmp(hg.data(), hf.data(), nnz * 4) == 0);
+}
+
 static void test_gemm_diag(const char* name, int n, std::vector<int> oa, std::vector<int> ob)
 {
     std::mt19937 g(42);
@@ -355,6 +398,7 @@ int main()
         test_gemm_diag("gemm_diag band", 512, {-3, -2, -1, 0, 1, 2, 3}, {-3, -2, -1, 0, 1, 2, 3});
         test_gemm_diag("gemm_diag scattered", 700, {-300, -9, 0, 33}, {-600, -1, 2, 5, 450});
         test_band_kernel();
+        test_astat_kernel();
     } catch (const std::exception& e) {
         std::printf("  exception: %s\n", e.what());
         g_all = false;

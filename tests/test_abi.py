@@ -170,3 +170,24 @@ def test_complex_and_krylov_argument_errors():
     assert call(4, band) == _lib.ERR_CAPACITY    # lds_bytes does not match nA
     band.eligible = 0
     assert call(3, band) == _lib.ERR_CAPACITY
+    # A-stationary kernel: argument checks before any HIP call or launch
+    assert _status("diagpu_spgemm_astat_prepare", 0, fake, 1, fake, 1, fake, None) == _lib.ERR_ARG
+    assert _status("diagpu_spgemm_astat_prepare", 10, fake, 0, fake, 1, fake, None) == _lib.ERR_ARG
+    assert _status("diagpu_spgemm_astat_prepare", 10, None, 1, fake, 1, fake, None) == _lib.ERR_ARG
+    assert _status("diagpu_spgemm_astat_prepare", 10, fake, 1, fake, -1, fake, None) == _lib.ERR_ARG
+    astat = lambda nA, nC: _status("diagpu_spgemm_numeric_astat_f32", 100, fake, fake, nA, fake,
+                                   fake, fake, fake, fake, nC, fake, fake, 1, fake, None)
+    assert astat(0, 5) == _lib.ERR_ARG
+    assert astat(_lib.ASTAT_MAX_A + 1, 5) == _lib.ERR_CAPACITY
+    assert astat(3, 200) == _lib.ERR_ARG           # c_ndiag > 2n - 1
+    assert astat(3, 0) == _lib.OK                   # empty C: nothing to do
+
+
+def test_astat_max_a_matches_header():
+    """The Python constant mirrors DIAGPU_ASTAT_MAX_A, and 288 rows of that
+    many A diagonals fit the kernel's 80 KiB of LDS."""
+    import re
+    hdr = (Path(__file__).resolve().parents[1] / "include" / "diagpu.h").read_text()
+    m = re.search(r"#define DIAGPU_ASTAT_MAX_A (\d+)", hdr)
+    assert m and int(m.group(1)) == _lib.ASTAT_MAX_A
+    assert 288 * _lib.ASTAT_MAX_A * 4 <= 80 * 1024 < 288 * (_lib.ASTAT_MAX_A + 1) * 4

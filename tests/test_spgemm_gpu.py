@@ -335,3 +335,83 @@ def test_band_kernel_choice_and_capacity(dev):
     with pytest.raises(_lib.DiagpuError) as e:                    # refused before any launch
         pw.multiply(wide.values, narrow.values, kernel="band")
     assert e.value.status == _lib.ERR_CAPACITY
+
+
+def _random_offsets(rng, cnt, lo, hi, with_zero=True):
+    offs = set(rng.choice(np.arange(lo, hi + 1), size=cnt, replace=False).tolist())
+    if with_zero:
+        offs.add(0)
+    return sorted(offs)
+
+
+@pytest.mark.parametrize("n,case", [
+    (4096, "band64"),       # 64 random offsets over +-512: the cfg-3 square, small n
+    (37, "edges"),          # smaller than one block, offsets reaching +-(n-1)
+    (1000, "wideB"),        # narrow A, B spanning the matrix
+    (70001, "ragged"),      # ragged last block, B beyond the A window
+    (5000, "maxA"),         # DIAGPU_ASTAT_MAX_A A diagonals
+])
+def test_astat_kernel_same_bits_as_gather(dev, oracle, n, case):
+    """The A-stationary kernel returns the gather kernel's C bit for bit
+    (same plan order, same fused multiply-adds, same skipped terms), and its
+    records point every plan entry at its A diagonal with the positions both
+    operands hold."""
+    rng = np.random.default_rng(n)
+    if case == "band64":
+        offs_a = _random_offsets(rng, 63, -512, 512)
+        offs_b = _random_offsets(rng, 63, -512, 512)
+    elif case == "edges":
+        offs_a, offs_b = [-36, -3, 0, 2, 36], [-30, -1, 0, 5, 36]
+    elif case == "wideB":
+        offs_a, offs_b = list(range(-40, 41, 3)), [-999, -7, 0, 1, 998]
+    elif case == "ragged":
+        offs_a, offs_b = list(range(-12, 13)), [-65000, -3, 0, 4, 65000]
+    else:
+        offs_a = _random_offsets(rng, _lib.ASTAT_MAX_A, -2000, 2000, with_zero=False)
+        offs_b = _random_offsets(rng, 9, -100, 100)
+    assert len(offs_a) <= _lib.ASTAT_MAX_A
+    A = workloads.hm_random(n, offs_a, 21, dev)
+    B = workloads.hm_random(n, offs_b, 22, dev)
+    plan = SpgemmPlan(A, B)
+    rec = plan.astat_records()[: 4 * plan.info.n_pairs].cpu().numpy().reshape(-1, 4)
+    pairs = plan.pairs_numpy()
+    a_st = A.starts.cpu().numpy()
+    a_idx = np.searchsorted(a_st, pairs["ab"].astype(np.int64))
+    assert np.array_equal(rec[:, 0], a_idx)
+    assert np.array_equal(rec[:, 1], np.maximum(0, np.maximum(-pairs["ash"], -pairs["bsh"])))
+    assert np.array_equal(rec[:, 2], np.minimum(pairs["al"] - pairs["ash"], pairs["bl"] - pairs["bsh"]))
+    assert np.array_equal(rec[:, 3], pairs["bb"].astype(np.int64) + pairs["bsh"])
+    Cg = plan.multiply(A.values, B.values, kernel="gather")
+    Ca = plan.multiply(A.values, B.values, kernel="astat")
+    assert torch.equal(Cg.view(torch.int32), Ca.view(torch.int32))
+    if n <= 5000:
+        ptr, c_len, c_st = plan.pair_ptr().cpu().numpy(), plan.c_lengths().cpu().numpy(), plan.c_starts().cpu().numpy()
+        want, ab = oracle.spgemm_pairs_f64(A.values.cpu().numpy(), B.values.cpu().numpy(), c_len,
+                                           c_st, ptr, pairs, 0, plan.info.c_ndiag)
+        check_values(Ca.cpu().numpy(), want, ab)
+
+
+def test_astat_kernel_choice_and_capacity(dev):
+    """auto picks the A-stationary kernel for the square of a 64-diagonal
+    band over +-512 (64 entries per A diagonal), the band kernel for
+    gemm_diag's contiguous band and the gather for config 4; more than
+    DIAGPU_ASTAT_MAX_A A diagonals are refused with DIAGPU_ERR_CAPACITY."""
+    rng = np.random.default_rng(3)
+    n = 1 << 18
+    offs = _random_offsets(rng, 63, -512, 512)
+    H = workloads.hm_random(n, offs, 5, dev)
+    p = SpgemmPlan(H, H)
+    assert p.kernel_for() == "astat"
+    Cg = p.multiply(H.values, H.values, kernel="gather")
+    Ca = p.multiply(H.values, H.values)
+    assert torch.equal(Cg.view(torch.int32), Ca.view(torch.int32))
+    G = workloads.hm_random(n, range(-10, 11), 1, dev)
+    assert SpgemmPlan(G, G).kernel_for() == "band"
+    A4, B4 = workloads.spgemm_config(4, seed=4, device=dev)
+    assert SpgemmPlan(A4, B4).kernel_for() == "gather"
+    wide = workloads.hm_random(4096, _random_offsets(rng, _lib.ASTAT_MAX_A + 1, -300, 300), 6, dev)
+    pw = SpgemmPlan(wide, wide)
+    assert pw.kernel_for() != "astat"
+    with pytest.raises(_lib.DiagpuError) as e:                    # refused before any launch
+        pw.multiply(wide.values, wide.values, kernel="astat")
+    assert e.value.status == _lib.ERR_CAPACITY
