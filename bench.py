@@ -46,7 +46,8 @@ def parse_args(argv=None):
     ap.add_argument("--no-extras", dest="extras", action="store_false")
     ap.add_argument("--only", default="",
                     help="profiling aid: run just one workload (spmv2, spmv2d, spmv2c, "
-                         "spmv2rc, spmv1, spmv3, spgemm4, spgemm5, spgemm4c, spgemm5c, taylor, krylov, "
+                         "spmv2rc, spmv1, spmv3, spgemm1..spgemm3 (the squares of the SpMV "
+                         "configs' matrices), spgemm4, spgemm5, spgemm4c, spgemm5c, taylor, krylov, "
                          "propagator, propagator2d, gemmdiag, gemmdiag20, copy) "
                          "and print its line")
     return ap.parse_args(argv)
