@@ -108,21 +108,22 @@ class SpgemmPlan:
         return self._band
 
     def uses_band(self, dtype=torch.float32) -> bool:
-        """The automatic choice: the LDS-staged band kernel for fp32 plans
-        whose staged operands fit, whose C diagonals average >= 3 entries
-        (each operand run then feeds several entries) and that have at least
-        1024 row blocks of 256 (one workgroup each: fewer leave CUs idle,
-        where the gather splits its work finer), else the gather."""
+        """The automatic first choice: the LDS-staged band kernel for fp32
+        plans whose staged operands fit, whose C diagonals average >= 3
+        entries (each operand run then feeds several entries) and that have
+        at least 2048 row blocks of 256 (below that the A-stationary kernel
+        or the gather is faster: measured on gemm_diag's band, 39 vs 42 us at
+        n = 2^18, 130 vs 109 us at n = 2^20)."""
         na, nb = self.A.offsets.numel(), self.B.offsets.numel()
         if (dtype != torch.float32 or self.info.c_ndiag == 0 or na > 65535 or nb > 32767
-                or self.info.n_pairs < 3 * self.info.c_ndiag or self.n < 1024 * 256):
+                or self.info.n_pairs < 3 * self.info.c_ndiag or self.n < 2048 * 256):
             return False
         return bool(self.band_info()[1].eligible)
 
     def astat_records(self) -> torch.Tensor:
         """Records of diagpu_spgemm_astat_prepare for this plan (computed
         once; one stream sync); int32 [4 n_pairs + 4]."""
-        if self._astat is None:
+        if self._astat is None or self._astat is False:
             A = self.A
             rec = torch.empty(4 * self.info.n_pairs + 4, dtype=torch.int32,
                               device=self.C_off.device)
@@ -135,18 +136,23 @@ class SpgemmPlan:
     def uses_astat(self, dtype=torch.float32) -> bool:
         """The automatic choice after the band kernel: the A-stationary kernel
         for fp32 plans whose A diagonals fit its LDS (at most
-        DIAGPU_ASTAT_MAX_A), each feed at least 32 plan entries on average
-        (the reuse that pays for staging them) and that have at least 1024
-        row blocks of 256; B values must be addressable with int32."""
+        DIAGPU_ASTAT_MAX_A) and each feed at least 16 plan entries on average
+        (the reuse that pays for staging them: gemm_diag's band, 21 per A
+        diagonal, runs faster than on the gather at every n from 4096 up;
+        config 4, 7 per A diagonal, slower), with n >= 4096; B values must
+        be addressable with int32."""
         na = self.A.offsets.numel()
         if not (dtype == torch.float32 and self.info.c_ndiag > 0 and na <= _lib.ASTAT_MAX_A
-                and self.info.n_pairs >= 32 * na and self.n >= 1024 * 256):
+                and self.info.n_pairs >= 16 * na and self.n >= 4096):
+            return False
+        if self._astat is False:                  # refused before: B indices beyond int32
             return False
         try:
             self.astat_records()
         except _lib.DiagpuError as e:
-            if e.status != _lib.ERR_CAPACITY:    # B indices beyond int32: not this kernel
+            if e.status != _lib.ERR_CAPACITY:
                 raise
+            self._astat = False
             return False
         return True
 

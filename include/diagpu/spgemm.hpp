@@ -283,12 +283,12 @@ public:
         // The band kernel's tables for plans the automatic choice may take
         // (one more stream synchronisation); others prepare on demand.
         band_auto_ = info_.c_ndiag > 0 && a_ndiag <= 65535 && b_ndiag <= 32767 &&
-                     info_.n_pairs >= 3 * info_.c_ndiag && int64_t(n) >= 1024 * 256;
+                     info_.n_pairs >= 3 * info_.c_ndiag && int64_t(n) >= 2048 * 256;
         if (band_auto_) prepare_band(stream);
         // The A-stationary kernel's records where the automatic choice may
-        // take it: A fits its LDS and each A diagonal feeds >= 32 entries.
+        // take it: A fits its LDS and each A diagonal feeds >= 16 entries.
         astat_auto_ = !uses_band() && info_.c_ndiag > 0 && a_ndiag <= DIAGPU_ASTAT_MAX_A &&
-                      info_.n_pairs >= 32 * int64_t(a_ndiag) && int64_t(n) >= 1024 * 256;
+                      info_.n_pairs >= 16 * int64_t(a_ndiag) && int64_t(n) >= 4096;
         if (astat_auto_) {
             try {
                 prepare_astat(stream);
@@ -302,13 +302,12 @@ public:
     // True where NumericKernel::Auto runs the band kernel for fp32 values:
     // the staged operands fit in LDS, the C diagonals average >= 3 plan
     // entries (each staged operand run then feeds several entries) and there
-    // are >= 1024 row blocks of 256 (one workgroup each; fewer leave CUs
-    // idle, where the gather splits its work finer).
+    // are >= 2048 row blocks of 256 (below that the A-stationary kernel or
+    // the gather is faster).
     bool uses_band() const { return band_auto_ && band_.eligible; }
     // True where NumericKernel::Auto runs the A-stationary kernel: the band
     // kernel does not take the plan, A has at most DIAGPU_ASTAT_MAX_A
-    // diagonals, each feeding >= 32 plan entries on average, and there are
-    // >= 1024 row blocks of 256.
+    // diagonals, each feeding >= 16 plan entries on average, and n >= 4096.
     bool uses_astat() const { return astat_auto_; }
 
     // C_vals (device, info().c_nnz values) = A * B; asynchronous on `stream`

@@ -228,14 +228,14 @@ static void test_spgemm(const char* name, int n, std::vector<int> oa, std::vecto
 // The two numeric kernels of one plan: NumericKernel::Band (operands staged
 // in LDS) returns the gather's bits; Auto picks Band on the reference
 // driver's band (offsets -10..10, gemm_diag/gemm_diag.cu:467-486) at
-// n = 2^18 and the gather where the plan is too small; a plan whose staged
+// n = 2^19 and the gather where the plan is too small; a plan whose staged
 // window does not fit refuses Band with DIAGPU_ERR_CAPACITY.
 static void test_band_kernel()
 {
     std::mt19937 g(7);
     std::vector<int> offs;
     for (int d = -10; d <= 10; ++d) offs.push_back(d);
-    const int n = 1 << 18, P = (int)offs.size();
+    const int n = 1 << 19, P = (int)offs.size();
     std::vector<float> D((size_t)P * n, 0.0f);
     for (int i = 0; i < P; ++i) {
         const int sr = offs[i] >= 0 ? 0 : -offs[i];
@@ -245,7 +245,7 @@ static void test_band_kernel()
     diagpu::DeviceArray<int> doff(offs);
     diagpu::DeviceArray<float> dD(D);
     diagpu::GemmDiag gd(n, doff.data(), P, doff.data(), P);
-    report("band: Auto picks Band at n = 2^18", gd.plan().uses_band());
+    report("band: Auto picks Band at n = 2^19", gd.plan().uses_band());
     const size_t nnz = (size_t)gd.info().c_nnz;
     diagpu::DeviceArray<float> c_band(nnz), c_gather(nnz), c_auto(nnz);
     gd.run(dD.data(), dD.data(), c_gather.data(), 0, diagpu::NumericKernel::Gather);

@@ -314,14 +314,16 @@ def test_band_kernel_same_bits_as_gather(dev, oracle, n, offs_a, offs_b):
 
 
 def test_band_kernel_choice_and_capacity(dev):
-    """auto picks the band kernel for gemm_diag's contiguous bands and the
-    gather for config 4 (1.3 entries per C diagonal); a plan whose staged
-    operands exceed the LDS budget is refused with DIAGPU_ERR_CAPACITY."""
+    """auto picks the band kernel for gemm_diag's contiguous bands from 2048
+    row blocks on (the A-stationary kernel below that) and the gather for
+    config 4 (1.3 entries per C diagonal); a plan whose staged operands
+    exceed the LDS budget is refused with DIAGPU_ERR_CAPACITY."""
     n = 1 << 18
-    A = workloads.hm_random(n, range(-10, 11), 1, dev)
+    A = workloads.hm_random(1 << 19, range(-10, 11), 1, dev)
     assert SpgemmPlan(A, A).uses_band()
-    small = workloads.hm_random(8192, range(-10, 11), 1, dev)     # 32 row blocks: the gather
-    assert not SpgemmPlan(small, small).uses_band()
+    small = workloads.hm_random(n, range(-10, 11), 1, dev)        # 1024 row blocks
+    ps = SpgemmPlan(small, small)
+    assert not ps.uses_band() and ps.kernel_for() == "astat"
     A4, B4 = workloads.spgemm_config(4, seed=4, device=dev)
     p4 = SpgemmPlan(A4, B4)
     assert not p4.uses_band()
@@ -393,8 +395,9 @@ def test_astat_kernel_same_bits_as_gather(dev, oracle, n, case):
 
 def test_astat_kernel_choice_and_capacity(dev):
     """auto picks the A-stationary kernel for the square of a 64-diagonal
-    band over +-512 (64 entries per A diagonal), the band kernel for
-    gemm_diag's contiguous band and the gather for config 4; more than
+    band over +-512 (64 entries per A diagonal) and for gemm_diag's band
+    below 2048 row blocks (21 per A diagonal), the band kernel above, the
+    gather for config 4 (7 per A diagonal); more than
     DIAGPU_ASTAT_MAX_A A diagonals are refused with DIAGPU_ERR_CAPACITY."""
     rng = np.random.default_rng(3)
     n = 1 << 18
@@ -405,8 +408,12 @@ def test_astat_kernel_choice_and_capacity(dev):
     Cg = p.multiply(H.values, H.values, kernel="gather")
     Ca = p.multiply(H.values, H.values)
     assert torch.equal(Cg.view(torch.int32), Ca.view(torch.int32))
-    G = workloads.hm_random(n, range(-10, 11), 1, dev)
+    G = workloads.hm_random(1 << 19, range(-10, 11), 1, dev)
     assert SpgemmPlan(G, G).kernel_for() == "band"
+    G4 = workloads.hm_random(4096, range(-10, 11), 1, dev)       # gemm_diag's default size
+    assert SpgemmPlan(G4, G4).kernel_for() == "astat"
+    g5 = workloads.hm_random(2048, range(-10, 11), 1, dev)       # below n = 4096: the gather
+    assert SpgemmPlan(g5, g5).kernel_for() == "gather"
     A4, B4 = workloads.spgemm_config(4, seed=4, device=dev)
     assert SpgemmPlan(A4, B4).kernel_for() == "gather"
     wide = workloads.hm_random(4096, _random_offsets(rng, _lib.ASTAT_MAX_A + 1, -300, 300), 6, dev)
