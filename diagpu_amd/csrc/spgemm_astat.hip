@@ -54,11 +54,16 @@ __global__ __launch_bounds__(256) void k_astat_prepare(const diagpu_gpair* __res
     const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (g >= n_pairs) return;
     const diagpu_gpair p = pairs[g];
+    // binary search (diagonals stored in offset order: starts ascend), then a
+    // linear scan for operands stored in another order
     int lo = 0, hi = nA - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
         if (A_starts[mid] <= (int64_t)p.ab) lo = mid; else hi = mid - 1;
     }
+    if (A_starts[lo] != (int64_t)p.ab)
+        for (int i = 0; i < nA; ++i)
+            if (A_starts[i] == (int64_t)p.ab) lo = i;
     const int plo = max(0, max(-p.ash, -p.bsh));
     const int phi = min(p.al - p.ash, p.bl - p.bsh);
     const int64_t b = (int64_t)p.bb + p.bsh;

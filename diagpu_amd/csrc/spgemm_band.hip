@@ -53,8 +53,8 @@ bool band_fits(int64_t lds_bytes, int64_t n_pairs)
 }
 
 // entries[g] = {a kRB, b WB + (da - min da), da, 0}, a and b the indices of
-// pairs[g].ab in A_starts and of pairs[g].bb in B_starts (binary search: the
-// starts ascend), WB = window_rows(span).  span[0..1] = min, max da (k_span, which
+// pairs[g].ab in A_starts and of pairs[g].bb in B_starts, WB =
+// window_rows(span).  span[0..1] = min, max da (k_span, which
 // runs first on the stream); span[2] is set if an entry matches no diagonal.
 __global__ __launch_bounds__(256) void k_band_prepare(const diagpu_gpair* __restrict__ pairs,
                                                       int64_t n_pairs,
@@ -67,13 +67,18 @@ __global__ __launch_bounds__(256) void k_band_prepare(const diagpu_gpair* __rest
 {
     const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (g >= n_pairs) return;
+    // binary search (diagonals stored in offset order: starts ascend), then a
+    // linear scan for operands stored in another order
     auto find = [](const int64_t* s, int32_t cnt, int64_t v) -> int {
         int lo = 0, hi = cnt - 1;
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
             if (s[mid] <= v) lo = mid; else hi = mid - 1;
         }
-        return s[lo] == v ? lo : -1;
+        if (s[lo] == v) return lo;
+        for (int i = 0; i < cnt; ++i)
+            if (s[i] == v) return i;
+        return -1;
     };
     const diagpu_gpair p = pairs[g];
     const int a = find(A_starts, nA, (int64_t)p.ab);

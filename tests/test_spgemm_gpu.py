@@ -422,3 +422,25 @@ def test_astat_kernel_choice_and_capacity(dev):
     with pytest.raises(_lib.DiagpuError) as e:                    # refused before any launch
         pw.multiply(wide.values, wide.values, kernel="astat")
     assert e.value.status == _lib.ERR_CAPACITY
+
+
+def test_lds_kernels_with_operands_in_any_order(dev):
+    """The band and A-stationary kernels look each plan entry's diagonals up
+    by their starts: operands whose diagonals are stored out of offset order
+    (starts not ascending) give the gather's bits too, and "auto" still
+    works on them."""
+    rng = np.random.default_rng(9)
+    n = 6000
+
+    def shuffled(offs, seed):
+        M = workloads.hm_random(n, offs, seed, dev)
+        perm = torch.as_tensor(rng.permutation(len(offs)), device=dev)
+        return workloads.HM(n, M.offsets[perm].contiguous(), M.lengths[perm].contiguous(),
+                            M.starts[perm].contiguous(), M.values)
+    A = shuffled(list(range(-10, 11)), 31)
+    B = shuffled(list(range(-8, 9)), 32)
+    plan = SpgemmPlan(A, B)
+    Cg = plan.multiply(A.values, B.values, kernel="gather")
+    for k in ("band", "astat", "auto"):
+        Ck = plan.multiply(A.values, B.values, kernel=k)
+        assert torch.equal(Cg.view(torch.int32), Ck.view(torch.int32)), k
