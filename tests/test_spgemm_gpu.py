@@ -283,6 +283,8 @@ def test_square_of_spmv_configs(dev, oracle, cfg):
     (37, [-36, -3, 0, 2, 36], [-30, -1, 0, 5, 36]),            # smaller than one block, edges
     (1000, list(range(-40, 41, 3)), [-999, -7, 0, 1, 998]),    # narrow A, B spanning the matrix
     (70001, list(range(-12, 13)), [-65000, -3, 0, 4, 65000]),  # ragged last block
+    (1, [0], [0]),                                             # a 1 x 1 matrix
+    (3, [-2, -1, 0, 1, 2], [-2, 0, 1]),                        # every diagonal of 3 x 3
 ])
 def test_band_kernel_same_bits_as_gather(dev, oracle, n, offs_a, offs_b):
     """The LDS-staged band kernel returns the gather kernel's C bit for bit
@@ -352,6 +354,8 @@ def _random_offsets(rng, cnt, lo, hi, with_zero=True):
     (1000, "wideB"),        # narrow A, B spanning the matrix
     (70001, "ragged"),      # ragged last block, B beyond the A window
     (5000, "maxA"),         # DIAGPU_ASTAT_MAX_A A diagonals
+    (1, "one"),             # a 1 x 1 matrix: one block, 32 lead rows before row 0
+    (3, "three"),           # every diagonal of a 3 x 3 matrix
 ])
 def test_astat_kernel_same_bits_as_gather(dev, oracle, n, case):
     """The A-stationary kernel returns the gather kernel's C bit for bit
@@ -368,6 +372,10 @@ def test_astat_kernel_same_bits_as_gather(dev, oracle, n, case):
         offs_a, offs_b = list(range(-40, 41, 3)), [-999, -7, 0, 1, 998]
     elif case == "ragged":
         offs_a, offs_b = list(range(-12, 13)), [-65000, -3, 0, 4, 65000]
+    elif case == "one":
+        offs_a, offs_b = [0], [0]
+    elif case == "three":
+        offs_a, offs_b = [-2, -1, 0, 1, 2], [-2, 0, 1]
     else:
         offs_a = _random_offsets(rng, _lib.ASTAT_MAX_A, -2000, 2000, with_zero=False)
         offs_b = _random_offsets(rng, 9, -100, 100)
