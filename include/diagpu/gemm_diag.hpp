@@ -11,12 +11,36 @@
 #pragma once
 
 #include <cstdint>
+#include <cstdlib>
+#include <random>
 #include <vector>
 
 #include "common.hpp"
 #include "spgemm.hpp"
 
 namespace diagpu {
+
+// pack_diag_matrix (gemm_diag.cu:362-382): the P x n row-packed operand of
+// the reference driver.  Row ri holds diagonal d = offsets[ri]: its n - |d|
+// elements at columns [max(-d, 0), max(-d, 0) + n - |d|), drawn in that
+// order, diagonal after diagonal, from U(0.5, 1.5) with std::mt19937(seed);
+// zeros elsewhere.  The draws are the reference's; the values equal its
+// wherever the standard library's uniform_real_distribution is the same.
+inline void pack_diag_matrix(int n, const std::vector<int>& offsets, unsigned seed,
+                             std::vector<float>& DA_out, std::vector<int>& off_out)
+{
+    const int P = static_cast<int>(offsets.size());
+    DA_out.assign(static_cast<size_t>(P) * n, 0.0f);
+    off_out = offsets;
+    std::mt19937 rng(seed);
+    std::uniform_real_distribution<float> dist(0.5f, 1.5f);
+    for (int ri = 0; ri < P; ++ri) {
+        const int d = offsets[ri];
+        const int first = d >= 0 ? 0 : -d;
+        const int len = n - std::abs(d);
+        for (int p = 0; p < len; ++p) DA_out[static_cast<size_t>(ri) * n + first + p] = dist(rng);
+    }
+}
 
 // build_c_layout (gemm_diag.cu:388-423) with 64-bit C offsets.
 struct CLayout {
