@@ -37,6 +37,30 @@ struct ReconMatrix {
     std::vector<float> values;
 };
 
+// dense_to_dia of the reference's SpMV tests (spmv/test/test_tc_spmv.cu:39-62,
+// spmv/test/test_reconstruct.cpp): every diagonal of the row-major
+// rows x cols matrix H that holds a nonzero, offsets ascending from
+// -(rows - 1), each stored whole (zeros included).
+inline DiaMatrix dense_to_dia(const float* H, int rows, int cols)
+{
+    DiaMatrix D;
+    D.rows = rows;
+    D.cols = cols;
+    for (int d = -(rows - 1); d <= cols - 1; ++d) {
+        const int sr = d >= 0 ? 0 : -d, sc = d >= 0 ? d : 0;
+        const int len = std::min(rows - sr, cols - sc);
+        if (len <= 0) continue;
+        bool any = false;
+        for (int j = 0; j < len && !any; ++j) any = H[size_t(sr + j) * cols + (sc + j)] != 0.0f;
+        if (!any) continue;
+        D.offsets.push_back(d);
+        D.diag_starts.push_back(static_cast<int>(D.values.size()));
+        D.diag_lengths.push_back(len);
+        for (int j = 0; j < len; ++j) D.values.push_back(H[size_t(sr + j) * cols + (sc + j)]);
+    }
+    return D;
+}
+
 // build_recon (:77-107): offsets sorted descending; row k receives the values
 // of the first input diagonal whose offset equals d_k.
 inline ReconMatrix build_recon(const DiaMatrix& H)
@@ -74,6 +98,23 @@ static_assert(sizeof(ReconView) == sizeof(diagpu_recon_view_f32) &&
                   offsetof(ReconView, diag_offsets) == offsetof(diagpu_recon_view_f32, diag_offsets) &&
                   offsetof(ReconView, values) == offsetof(diagpu_recon_view_f32, values),
               "ReconView must match diagpu_recon_view_f32");
+
+// spmv_from_recon of the reference's SpMV tests (test_tc_spmv.cu:64-79,
+// test_reconstruct.cpp:122-138): y = R x on the host in fp32, one row at a
+// time, terms in Recon row order (offsets descending).
+inline std::vector<float> spmv_from_recon(const ReconMatrix& R, const std::vector<float>& x)
+{
+    std::vector<float> y(static_cast<size_t>(R.rows), 0.0f);
+    for (int r = 0; r < R.rows; ++r) {
+        float sum = 0.0f;
+        for (int k = 0; k < R.num_diags; ++k) {
+            const int c = r + R.diag_offsets[k];
+            if (c >= 0 && c < R.cols) sum += R.values[size_t(k) * R.cols + c] * x[c];
+        }
+        y[r] = sum;
+    }
+    return y;
+}
 
 // y = H x on `stream` (:139-144; tc_spmv_regdirect_kernel.cu:135-147): y is
 // overwritten, rows == 0 is a no-op, asynchronous, allocates nothing.

@@ -41,27 +41,6 @@ static void report(const char* name, bool ok, const char* detail = "")
     g_all &= ok;
 }
 
-// dense_to_dia of the reference tests (test_tc_spmv.cu:39-62).
-static DiaMatrix dense_to_dia(const float* H, int rows, int cols)
-{
-    DiaMatrix D;
-    D.rows = rows;
-    D.cols = cols;
-    for (int d = -(rows - 1); d <= cols - 1; ++d) {
-        const int sr = d >= 0 ? 0 : -d, sc = d >= 0 ? d : 0;
-        const int len = std::min(rows - sr, cols - sc);
-        if (len <= 0) continue;
-        bool nz = false;
-        for (int j = 0; j < len; ++j) nz |= H[(size_t)(sr + j) * cols + (sc + j)] != 0.0f;
-        if (!nz) continue;
-        D.offsets.push_back(d);
-        D.diag_starts.push_back((int)D.values.size());
-        D.diag_lengths.push_back(len);
-        for (int j = 0; j < len; ++j) D.values.push_back(H[(size_t)(sr + j) * cols + (sc + j)]);
-    }
-    return D;
-}
-
 static std::vector<float> gpu_spmv(const ReconMatrix& R, const std::vector<float>& x)
 {
     diagpu::DeviceRecon dR(R);
@@ -112,7 +91,8 @@ static void test_tc_case(const char* name, int N, const std::vector<int>& offset
                         D.values.data(), o_off.data(), o_val.data());
     const bool layout_ok = o_off == R.diag_offsets && o_val == R.values;
     const auto y = gpu_spmv(R, x);
-    bool ok = true;
+    const auto yh = spmv_from_recon(R, x);   // the header's host SpMV, same bound
+    bool ok = yh.size() == (size_t)N;
     double worst = 0;
     for (int r = 0; r < N; ++r) {
         double s = 0, a = 0;
@@ -124,6 +104,7 @@ static void test_tc_case(const char* name, int N, const std::vector<int>& offset
         const double err = std::fabs(y[r] - s);
         worst = std::max(worst, err / (a + 1e-300));
         ok &= err <= 1e-5 * a + 1e-300;
+        ok &= std::fabs(yh[r] - s) <= 1e-5 * a + 1e-300;
     }
     char buf[96];
     std::snprintf(buf, sizeof buf, "N=%d diags=%d worst err/sum|t|=%.1e", N, R.num_diags, worst);
