@@ -15,6 +15,7 @@
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
+#include <random>
 #include <stdexcept>
 #include <vector>
 
@@ -395,6 +396,36 @@ private:
     mutable diagpu_band_info band_{};
     mutable bool band_prepared_ = false;
 };
+
+}  // namespace diagpu
+
+namespace diagpu {
+
+// make_banded of the reference SpGEMM benchmark (spmspm/bench_spmspm.cu:89-106)
+// as an HMMatrix: offsets -w..w ascending (those with n - |d| > 0), each
+// diagonal's n - |d| values drawn in order from U(-1, 1) with
+// std::mt19937(seed).  The draws are the reference's; the values equal its
+// wherever the standard library's uniform_real_distribution is the same.
+inline HMMatrix make_banded(int n, int w, unsigned seed)
+{
+    HMMatrix M;
+    M.n = n;
+    std::mt19937 rng(seed);
+    std::uniform_real_distribution<float> dist(-1.0f, 1.0f);
+    int64_t start = 0;
+    for (int d = -w; d <= w; ++d) {
+        const int len = n - std::abs(d);
+        if (len <= 0) continue;
+        M.diag_offsets.push_back(d);
+        M.diag_starts.push_back(start);
+        M.diag_lengths.push_back(len);
+        for (int p = 0; p < len; ++p) M.values.push_back(dist(rng));
+        start += len;
+    }
+    M.num_diags = static_cast<int>(M.diag_offsets.size());
+    M.total_nz = start;
+    return M;
+}
 
 }  // namespace diagpu
 

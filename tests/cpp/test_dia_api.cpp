@@ -28,6 +28,9 @@ int64_t orc_pairs_only(int n, const int* A_off, int nA, const int* A_len, const 
 void orc_spgemm_pairs_f64(const float* A_vals, const float* B_vals, const int* C_len,
                           const int64_t* C_starts, const int64_t* pair_ptr, const void* pairs,
                           int kbeg, int kend, double* out, double* abs_out);
+int orc_make_banded(int n, int w, unsigned seed, int* offsets, int64_t* starts, int* lengths,
+                    float* values);
+void orc_pack_diag_matrix(int n, const int* offsets, int P, unsigned seed, float* DA);
 void orc_gemm_diag_f64(int n, const float* DA, const int* off_A, int P, const float* DB,
                        const int* off_B, int Q, const int* C_lookup, const int64_t* C_starts,
                        double* out, double* abs_out);
@@ -326,6 +329,41 @@ static void test_astat_kernel()
     report("astat: AStationary == Gather", std::memcmp(hg.data(), hf.data(), nnz * 4) == 0);
 }
 
+// The reference benchmarks' operand generators against the oracle's
+// restatements: make_banded(100000, 16, 1234 / 5678)
+// (spmspm/bench_spmspm.cu:465-466) and pack_diag_matrix(4096, -10..10, 42 /
+// 137) (gemm_diag/gemm_diag.cu:485-486), value for value.
+static void test_generators()
+{
+    bool ok = true;
+    for (unsigned seed : {1234u, 5678u}) {
+        const int n = 100000, w = 16;
+        const HMMatrix M = diagpu::make_banded(n, w, seed);
+        std::vector<int> off(2 * w + 1), len(2 * w + 1);
+        std::vector<int64_t> st(2 * w + 1);
+        std::vector<float> val((size_t)(2 * w + 1) * n);
+        const int nd = orc_make_banded(n, w, seed, off.data(), st.data(), len.data(), val.data());
+        off.resize(nd);
+        len.resize(nd);
+        st.resize(nd);
+        ok &= M.num_diags == nd && M.diag_offsets == off && M.diag_lengths == len &&
+              M.diag_starts == st && (int64_t)M.values.size() == M.total_nz &&
+              std::memcmp(M.values.data(), val.data(), M.values.size() * sizeof(float)) == 0;
+    }
+    report("make_banded == oracle (seeds 1234, 5678)", ok);
+    bool pk = true;
+    std::vector<int> offs;
+    for (int d = -10; d <= 10; ++d) offs.push_back(d);
+    for (unsigned seed : {42u, 137u}) {
+        std::vector<float> DA, want(offs.size() * 4096);
+        std::vector<int> oo;
+        diagpu::pack_diag_matrix(4096, offs, seed, DA, oo);
+        orc_pack_diag_matrix(4096, offs.data(), (int)offs.size(), seed, want.data());
+        pk &= DA == want && oo == offs;
+    }
+    report("pack_diag_matrix == oracle (seeds 42, 137)", pk);
+}
+
 // pack_diag_matrix (gemm_diag/gemm_diag.cu:362-382): zeros outside each
 // diagonal's rows, U(0.5, 1.5) inside, in the draw order of one
 // std::mt19937 stream; then the reference driver's product (seeds 42 and
@@ -422,6 +460,7 @@ int main()
         test_band_kernel();
         test_astat_kernel();
         test_pack_diag_matrix();
+        test_generators();
     } catch (const std::exception& e) {
         std::printf("  exception: %s\n", e.what());
         g_all = false;
