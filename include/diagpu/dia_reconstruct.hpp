@@ -150,6 +150,58 @@ inline void launch_dia_spmv(ReconViewF64 R, const double* d_x, int64_t x_size, d
                                 d_y, stream));
 }
 
+// Band values of the reference SpMV benchmark (spmv/bench/bench_cusparse.cu:
+// 70-82; the same hval is in spmv/tools/gen_banded_mtx.cpp:18-23): an integer
+// hash of (row, offset), resp. of the index, whose low 16 bits map onto
+// [-1, 1) in steps of 2^-15.  hval(r, d) is H[r, r + d]; xval(i) is x[i].
+inline float hval(int r, int d)
+{
+    uint32_t h = static_cast<uint32_t>(r) * 2654435761u;
+    h ^= static_cast<uint32_t>(d + 1024) * 40503u;
+    h ^= h >> 13;
+    h *= 0x5bd1e995u;
+    h ^= h >> 15;
+    return static_cast<float>(h & 0xFFFFu) * (2.0f / 65536.0f) - 1.0f;
+}
+
+inline float xval(int i)
+{
+    uint32_t h = static_cast<uint32_t>(i) * 2246822519u;
+    h ^= h >> 13;
+    h *= 0x85ebca6bu;
+    h ^= h >> 16;
+    return static_cast<float>(h & 0xFFFFu) * (2.0f / 65536.0f) - 1.0f;
+}
+
+// The benchmark's N x N Recon matrix for the given offsets (:84-89 default
+// {-9, -5, -2, -1, 0, 1, 2, 5, 9}; fill :131-144): offsets sorted descending,
+// R[k][c] = hval(c - d_k, d_k) where that row exists, zero elsewhere.
+inline ReconMatrix make_hash_band(int N, std::vector<int> offsets)
+{
+    std::sort(offsets.begin(), offsets.end(), std::greater<int>());
+    ReconMatrix R;
+    R.rows = N;
+    R.cols = N;
+    R.num_diags = static_cast<int>(offsets.size());
+    R.diag_offsets = offsets;
+    R.values.assign(static_cast<size_t>(R.num_diags) * static_cast<size_t>(N), 0.0f);
+    for (int k = 0; k < R.num_diags; ++k) {
+        const int d = offsets[k];
+        const int c0 = std::max(d, 0), c1 = std::min(N, N + d);
+        float* row = R.values.data() + static_cast<size_t>(k) * N;
+        for (int c = c0; c < c1; ++c) row[c] = hval(c - d, d);
+    }
+    return R;
+}
+
+// x of the same benchmark (:97-98).
+inline std::vector<float> make_hash_x(int N)
+{
+    std::vector<float> x(static_cast<size_t>(N));
+    for (int i = 0; i < N; ++i) x[static_cast<size_t>(i)] = xval(i);
+    return x;
+}
+
 // Owning device copy of a ReconMatrix with its view.
 struct DeviceRecon {
     DeviceArray<int> offsets;

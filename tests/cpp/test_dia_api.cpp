@@ -31,6 +31,8 @@ void orc_spgemm_pairs_f64(const float* A_vals, const float* B_vals, const int* C
 int orc_make_banded(int n, int w, unsigned seed, int* offsets, int64_t* starts, int* lengths,
                     float* values);
 void orc_pack_diag_matrix(int n, const int* offsets, int P, unsigned seed, float* DA);
+void orc_hash_band_recon(int N, const int* offsets, int K, int* r_offsets, float* r_values,
+                         float* x);
 void orc_gemm_diag_f64(int n, const float* DA, const int* off_A, int P, const float* DB,
                        const int* off_B, int Q, const int* C_lookup, const int64_t* C_starts,
                        double* out, double* abs_out);
@@ -362,6 +364,18 @@ static void test_generators()
         pk &= DA == want && oo == offs;
     }
     report("pack_diag_matrix == oracle (seeds 42, 137)", pk);
+    // The SpMV benchmark's band (bench_cusparse.cu:84-144), offsets given
+    // unsorted, one of them reaching past the matrix.
+    const int N = 1 << 16;
+    const std::vector<int> bo = {0, -9, 5, 2, -1, 1, -2, 9, -5, N + 3};
+    const ReconMatrix R = diagpu::make_hash_band(N, bo);
+    const std::vector<float> hx = diagpu::make_hash_x(N);
+    std::vector<int> ro(bo.size());
+    std::vector<float> rv(bo.size() * (size_t)N), rx(N);
+    orc_hash_band_recon(N, bo.data(), (int)bo.size(), ro.data(), rv.data(), rx.data());
+    report("make_hash_band / make_hash_x == oracle",
+           R.rows == N && R.cols == N && R.num_diags == (int)bo.size() && R.diag_offsets == ro &&
+               R.values == rv && hx == rx);
 }
 
 // pack_diag_matrix (gemm_diag/gemm_diag.cu:362-382): zeros outside each
