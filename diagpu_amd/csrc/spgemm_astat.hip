@@ -70,6 +70,11 @@ __global__ __launch_bounds__(256) void k_astat_prepare(const diagpu_gpair* __res
     int4 r = int4{0, 0, 0, 0};
     if (A_starts[lo] != (int64_t)p.ab) {
         flag[0] = 1;   // every writer stores the same value
+    } else if (plo >= phi) {
+        // No position holds both operands (a symbolic plan has no such entry,
+        // a caller's may): a record that never fires, whose clamped B load
+        // min(max(p, 1), 0) = 0 reads B[0].
+        r = int4{lo, 1, 1, 0};
     } else if (b < INT_MIN || b + phi > INT_MAX) {
         flag[1] = 1;
     } else {

@@ -452,3 +452,40 @@ def test_lds_kernels_with_operands_in_any_order(dev):
     for k in ("band", "astat", "auto"):
         Ck = plan.multiply(A.values, B.values, kernel=k)
         assert torch.equal(Cg.view(torch.int32), Ck.view(torch.int32)), k
+
+
+def test_plan_entries_without_positions(dev):
+    """A caller's plan may hold entries where no position has both operands
+    (a symbolic plan never does: |da|, |db|, |dc| < n leaves at least one
+    row).  The gather and the A-stationary kernel take each entry's range
+    from its lengths: here entries of the first B diagonal (B start 0, where
+    the clamped B load of an empty range would fall before the array) get
+    al = 0 on the device, the A-stationary records mark them {a, 1, 1, 0}
+    (a record that never fires and loads B[0]), both kernels return the same
+    bits, and those bits differ from the full plan's product on exactly the
+    C diagonals of the emptied entries.  (The band kernel derives each
+    term's validity from the operands' offsets, not from the entry.)"""
+    n = 3000
+    A = workloads.hm_random(n, list(range(-20, 21, 4)), 41, dev)
+    B = workloads.hm_random(n, [-2999, -700, 0, 5, 2998], 42, dev)
+    plan = SpgemmPlan(A, B)
+    pairs = plan.pairs_numpy()
+    hit = np.nonzero(pairs["bb"] == 0)[0][:7]
+    assert hit.size > 0
+    words = plan.pairs[: plan.info.n_pairs * 32].view(torch.int32).view(-1, 8)
+    words[torch.as_tensor(hit, device=dev), 6] = 0             # al = 0: empty range
+    plan._astat = None                                           # records from the edited plan
+    rec = plan.astat_records()[: 4 * plan.info.n_pairs].cpu().numpy().reshape(-1, 4)
+    assert (rec[hit, 1:] == [1, 1, 0]).all()
+    Cg = plan.multiply(A.values, B.values, kernel="gather")
+    Ca = plan.multiply(A.values, B.values, kernel="astat")
+    assert torch.equal(Cg.view(torch.int32), Ca.view(torch.int32))
+    full = SpgemmPlan(A, B)
+    Cf = full.multiply(A.values, B.values, kernel="gather")
+    ptr = full.pair_ptr().cpu().numpy()
+    c_st, c_len = full.c_starts().cpu().numpy(), full.c_lengths().cpu().numpy()
+    touched = np.zeros(full.info.c_ndiag, bool)
+    touched[np.searchsorted(ptr, hit, side="right") - 1] = True
+    diff = (Cg != Cf).cpu().numpy()
+    for k in range(full.info.c_ndiag):
+        assert diff[c_st[k]: c_st[k] + c_len[k]].any() == touched[k], k
