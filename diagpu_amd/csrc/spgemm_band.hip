@@ -32,7 +32,9 @@
 namespace diagpu {
 namespace {
 
-constexpr int kRB = 256;                       // rows per block (one per lane)
+constexpr int kRB = 256;                       // rows per block
+constexpr int kThreads = 512;                  // lanes per workgroup: two halves of kRB
+constexpr int kHalves = kThreads / kRB;
 constexpr int64_t kLdsBudget = 64 * 1024;      // keeps two workgroups per CU
 
 // Rows of one B diagonal's window in LDS: kRB + span, padded to a multiple
@@ -133,7 +135,7 @@ __global__ __launch_bounds__(256) void k_span(const int32_t* __restrict__ off, i
 // i + dc) only where C(i, i + dc) is written (so column i + dc exists) and
 // A(i, i + da) exists (so row i + da does), and the evaluation skips every
 // term whose A element is missing, so no such value reaches a C element.
-__global__ __launch_bounds__(kRB) void k_band(
+__global__ __launch_bounds__(kThreads) void k_band(
     int32_t n, const int32_t* __restrict__ A_off, const int64_t* __restrict__ A_starts, int32_t nA,
     const float* __restrict__ Av, const int32_t* __restrict__ B_off,
     const int64_t* __restrict__ B_starts, int32_t nB, const float* __restrict__ Bv,
@@ -153,11 +155,15 @@ __global__ __launch_bounds__(kRB) void k_band(
     int4* E_l = reinterpret_cast<int4*>(B_l + (int64_t)nB * WB);   // [n_pairs] plan entries
     const int r = (int)threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(r >> 6), lane = r & 63;
+    // staging: half h of the workgroup (kRB lanes, one row each) takes the
+    // diagonal groups h, h + kHalves, ...
+    const int half = __builtin_amdgcn_readfirstlane(r / kRB), rr = r % kRB;
+    const int hw = __builtin_amdgcn_readfirstlane(rr >> 6);   // wave within the half
 
     // the plan's entries, once per workgroup: read below with uniform LDS
     // addresses (as global loads the compiler kept them in the vector memory
     // queue, behind the staging loads)
-    for (int g = r; g < n_pairs; g += kRB) E_l[g] = entries[g];
+    for (int g = r; g < n_pairs; g += kThreads) E_l[g] = entries[g];
 
     // One wave's 64 rows of one diagonal: lane l loads the element of row
     // w (its HM position clamped into the diagonal, so the address is
@@ -174,7 +180,7 @@ __global__ __launch_bounds__(kRB) void k_band(
     constexpr int kS = 8;
     const int slots = (WB + kRB - 1) / kRB;         // kRB-row slots of a B window
     auto stage = [&](int i0) {
-        for (int d0 = 0; d0 < nA; d0 += kS) {       // A: rows i0 + r
+        for (int d0 = half * kS; d0 < nA; d0 += kHalves * kS) {   // A: rows i0 + rr
             int o[kS];
             int64_t st[kS];
 #pragma unroll
@@ -185,9 +191,9 @@ __global__ __launch_bounds__(kRB) void k_band(
             }
 #pragma unroll
             for (int u = 0; u < kS; ++u)
-                if (d0 + u < nA) load_row(Av, st[u], o[u], i0 + r, A_l + (d0 + u) * kRB + wave * 64);
+                if (d0 + u < nA) load_row(Av, st[u], o[u], i0 + rr, A_l + (d0 + u) * kRB + hw * 64);
         }
-        for (int d0 = 0; d0 < nB; d0 += kS) {       // B: window rows i0 + a_min + q
+        for (int d0 = half * kS; d0 < nB; d0 += kHalves * kS) {   // B: window rows i0 + a_min + q
             int o[kS];
             int64_t st[kS];
 #pragma unroll
@@ -197,19 +203,19 @@ __global__ __launch_bounds__(kRB) void k_band(
                 st[u] = B_starts[d];
             }
             for (int sl = 0; sl < slots; ++sl) {
-                const int q = r + kRB * sl;
+                const int q = rr + kRB * sl;
                 if (q < WB) {
 #pragma unroll
                     for (int u = 0; u < kS; ++u)
                         if (d0 + u < nB)
                             load_row(Bv, st[u], o[u], i0 + a_min + q,
-                                     B_l + (d0 + u) * WB + kRB * sl + wave * 64);
+                                     B_l + (d0 + u) * WB + kRB * sl + hw * 64);
                 }
             }
         }
     };
 
-    constexpr int kWaves = kRB / 64, kR = kRB / 64;
+    constexpr int kWaves = kThreads / 64, kR = kRB / 64;
     for (; blk < blk_end; blk += wg_per_xcd) {
         const int64_t i0 = (int64_t)blk * kRB;
         __syncthreads();                 // every wave is done with the previous block's LDS
@@ -221,7 +227,7 @@ __global__ __launch_bounds__(kRB) void k_band(
         const bool interior =
             i0 + kRB <= n && i0 + a_min >= 0 && i0 + kRB + (int64_t)a_max <= n;
         const int row0 = (int)i0 + lane;             // n <= 2^30: rows fit int32
-        // Wave w evaluates C diagonals w, w + 4, ... over all kRB rows, kR
+        // Wave w evaluates C diagonals w, w + kWaves, ... over all kRB rows, kR
         // rows per lane (lane l: rows l, l + 64, ...): each entry's lookup
         // then feeds kR independent pairs of LDS reads.
         auto evaluate = [&](auto interior_tag) {
@@ -364,12 +370,12 @@ DIAGPU_API int diagpu_spgemm_numeric_band_f32(
     // persistent: as many workgroups per XCD as fit at once, at most one
     // per row block of its range
     int per_cu = 0;
-    int st = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_band, kRB,
+    int st = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_band, kThreads,
                                                                     (size_t)info->lds_bytes), fn);
     if (st) return st;
     int64_t wg = (int64_t)(cu_count() / kNumXcd) * (per_cu > 0 ? per_cu : 1);
     if (wg > per_xcd) wg = per_xcd;
-    hipLaunchKernelGGL(k_band, dim3((unsigned)(wg * kNumXcd)), dim3(kRB), (size_t)info->lds_bytes,
+    hipLaunchKernelGGL(k_band, dim3((unsigned)(wg * kNumXcd)), dim3(kThreads), (size_t)info->lds_bytes,
                        as_stream(stream), n, A_off, A_starts, nA, A_vals, B_off, B_starts, nB,
                        B_vals, C_off, C_starts, (int32_t)c_ndiag, pair_ptr,
                        reinterpret_cast<const int4*>(entries), (int32_t)n_pairs, C_vals,
