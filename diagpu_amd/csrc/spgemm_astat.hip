@@ -141,6 +141,11 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
             b = Bv[(int64_t)e.w + min(max(p, e.y), e.z - 1)];
             a = A_l[e.x * kStage + ab + 64 * j];
         };
+        // Taken once every load of a batch is issued: the values pass through
+        // an empty asm, so the compiler cannot turn a masked multiply-add into
+        // a branch around its own load (each such branch ends in a full
+        // vmcnt(0) drain: gfx9 counts loads in order).
+        auto pin = [](float& b, float& a) { asm volatile("" : "+v"(b), "+v"(a)); };
         int g = g0;
         for (; g + 2 <= g1; g += 2) {               // two entries' loads in flight
             float bv[2][4], av[2][4];
@@ -155,19 +160,24 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
 #pragma unroll
             for (int u = 0; u < 2; ++u)
 #pragma unroll
+                for (int j = 0; j < 4; ++j) pin(bv[u][j], av[u][j]);
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc[j] = ok[u][j] ? __builtin_fmaf(av[u][j], bv[u][j], acc[j]) : acc[j];
         }
         if (g < g1) {
             const int4 e = records[g];
             const int hi = min(e.z, len);
+            float bv[4], av[4];
+            bool ok[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float b, a;
-                bool ok;
-                term(e, hi, j, b, a, ok);
-                acc[j] = ok ? __builtin_fmaf(a, b, acc[j]) : acc[j];
-            }
+            for (int j = 0; j < 4; ++j) term(e, hi, j, bv[j], av[j], ok[j]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) pin(bv[j], av[j]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j] = ok[j] ? __builtin_fmaf(av[j], bv[j], acc[j]) : acc[j];
         }
         float* __restrict__ cp = Cv + cst;
 #pragma unroll
