@@ -30,6 +30,7 @@
 // {a, lo, hi, b} (diagpu_spgemm_astat_prepare): a the A diagonal's index,
 // [lo, hi) the C positions where both operands hold an element, b the B
 // index of C position 0.
+#include <algorithm>
 #include <climits>
 
 #include "common.hpp"
@@ -93,13 +94,17 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
     const float* __restrict__ Av, const float* __restrict__ Bv, const int32_t* __restrict__ C_off,
     const int32_t* __restrict__ C_len, const int64_t* __restrict__ C_starts, int32_t nC,
     const int64_t* __restrict__ pair_ptr, const int4* __restrict__ records,
-    float* __restrict__ Cv, int32_t blocks, int32_t per_xcd)
+    float* __restrict__ Cv, int32_t blocks, int32_t groups, int32_t per_xcd)
 {
     extern __shared__ float A_l[];   // [nA][kStage]: rows i0 - kLead .. i0 + kRB - 1
-    // workgroup b on XCD b mod 8: each XCD owns a contiguous range of blocks,
-    // so neighbouring blocks (whose B windows overlap) share its L2
-    const int blk = (int)(blockIdx.x % kNumXcd) * per_xcd + (int)(blockIdx.x / kNumXcd);
-    if (blk >= blocks) return;
+    // workgroup b on XCD b mod 8: each XCD owns a contiguous range of work
+    // units, so neighbouring blocks (whose B windows overlap) share its L2.
+    // Unit = (block, group): a block's C diagonals are split over `groups`
+    // workgroups (more than one only when the blocks alone cannot fill the
+    // GPU), each staging the block's A rows.
+    const int unit = (int)(blockIdx.x % kNumXcd) * per_xcd + (int)(blockIdx.x / kNumXcd);
+    if (unit >= blocks * groups) return;
+    const int blk = unit / groups, grp = unit % groups;
     const int r = (int)threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(r >> 6), lane = r & 63;
     const int i0 = blk * kRB;                       // n <= 2^30: rows fit int32
@@ -123,7 +128,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
     __builtin_amdgcn_s_waitcnt(0);   // this wave's direct loads have landed in LDS
     __syncthreads();
 
-    for (int kc = wave; kc < nC; kc += kWaves) {
+    for (int kc = grp * kWaves + wave; kc < nC; kc += groups * kWaves) {
         const int dc = C_off[kc];
         const int len = C_len[kc];
         const int64_t cst = C_starts[kc];
@@ -247,11 +252,18 @@ DIAGPU_API int diagpu_spgemm_numeric_astat_f32(
                                                  kStage * kMaxA * (int)sizeof(float)), fn);
     if (st) return st;
     const int32_t blocks = (int32_t)ceil_div<int64_t>((int64_t)n + kLead, kRB);
-    const int32_t per_xcd = ceil_div<int32_t>(blocks, kNumXcd);
+    // too few blocks to give every CU two workgroups: split each block's C
+    // diagonals over several (at most one per wave's worth of diagonals)
+    int32_t groups = 1;
+    const int64_t fill = 2 * (int64_t)cu_count();
+    if (blocks < fill)
+        groups = (int32_t)std::max<int64_t>(1, std::min<int64_t>(ceil_div<int64_t>(fill, blocks),
+                                                                 ceil_div<int64_t>(c_ndiag, kWaves)));
+    const int32_t per_xcd = (int32_t)ceil_div<int64_t>((int64_t)blocks * groups, kNumXcd);
     hipLaunchKernelGGL(k_astat, dim3((unsigned)(per_xcd * kNumXcd)), dim3(64 * kWaves), lds,
                        as_stream(stream), n, A_off, A_starts, nA, A_vals, B_vals, C_off, C_len,
                        C_starts, (int32_t)c_ndiag, pair_ptr,
-                       reinterpret_cast<const int4*>(records), C_vals, blocks, per_xcd);
+                       reinterpret_cast<const int4*>(records), C_vals, blocks, groups, per_xcd);
     return check_launch(fn);
 }
 

@@ -111,12 +111,12 @@ class SpgemmPlan:
         """The automatic first choice: the LDS-staged band kernel for fp32
         plans whose staged operands fit, whose C diagonals average >= 3
         entries (each operand run then feeds several entries) and that have
-        at least 256 row blocks of 256 (below that the A-stationary kernel or
+        at least 512 row blocks of 256 (below that the A-stationary kernel or
         the gather is faster: measured on gemm_diag's band, A-stationary vs
-        band 11.7 vs 15.8 us at n = 16384, 18.1 vs 16.5 us at n = 65536)."""
+        band 15.3 vs 16.4 us at n = 65536, 23.5 vs 19.4 us at n = 131072)."""
         na, nb = self.A.offsets.numel(), self.B.offsets.numel()
         if (dtype != torch.float32 or self.info.c_ndiag == 0 or na > 65535 or nb > 32767
-                or self.info.n_pairs < 3 * self.info.c_ndiag or self.n < 256 * 256):
+                or self.info.n_pairs < 3 * self.info.c_ndiag or self.n < 512 * 256):
             return False
         return bool(self.band_info()[1].eligible)
 

@@ -284,7 +284,7 @@ public:
         // The band kernel's tables for plans the automatic choice may take
         // (one more stream synchronisation); others prepare on demand.
         band_auto_ = info_.c_ndiag > 0 && a_ndiag <= 65535 && b_ndiag <= 32767 &&
-                     info_.n_pairs >= 3 * info_.c_ndiag && int64_t(n) >= 256 * 256;
+                     info_.n_pairs >= 3 * info_.c_ndiag && int64_t(n) >= 512 * 256;
         if (band_auto_) prepare_band(stream);
         // The A-stationary kernel's records where the automatic choice may
         // take it: A fits its LDS and each A diagonal feeds >= 16 entries.
@@ -303,7 +303,7 @@ public:
     // True where NumericKernel::Auto runs the band kernel for fp32 values:
     // the staged operands fit in LDS, the C diagonals average >= 3 plan
     // entries (each staged operand run then feeds several entries) and there
-    // are >= 256 row blocks of 256 (below that the A-stationary kernel or
+    // are >= 512 row blocks of 256 (below that the A-stationary kernel or
     // the gather is faster).
     bool uses_band() const { return band_auto_ && band_.eligible; }
     // True where NumericKernel::Auto runs the A-stationary kernel: the band

@@ -316,12 +316,12 @@ def test_band_kernel_same_bits_as_gather(dev, oracle, n, offs_a, offs_b):
 
 
 def test_band_kernel_choice_and_capacity(dev):
-    """auto picks the band kernel for gemm_diag's contiguous bands from 256
+    """auto picks the band kernel for gemm_diag's contiguous bands from 512
     row blocks on (the A-stationary kernel below that) and the gather for
     config 4 (1.3 entries per C diagonal); a plan whose staged operands
     exceed the LDS budget is refused with DIAGPU_ERR_CAPACITY."""
     n = 1 << 14
-    A = workloads.hm_random(1 << 16, range(-10, 11), 1, dev)     # 256 row blocks
+    A = workloads.hm_random(1 << 17, range(-10, 11), 1, dev)     # 512 row blocks
     assert SpgemmPlan(A, A).uses_band()
     small = workloads.hm_random(n, range(-10, 11), 1, dev)        # 64 row blocks
     ps = SpgemmPlan(small, small)
@@ -404,7 +404,7 @@ def test_astat_kernel_same_bits_as_gather(dev, oracle, n, case):
 def test_astat_kernel_choice_and_capacity(dev):
     """auto picks the A-stationary kernel for the square of a 64-diagonal
     band over +-512 (64 entries per A diagonal) and for gemm_diag's band
-    below 256 row blocks (21 per A diagonal), the band kernel above, the
+    below 512 row blocks (21 per A diagonal), the band kernel above, the
     gather for config 4 (7 per A diagonal); more than
     DIAGPU_ASTAT_MAX_A A diagonals are refused with DIAGPU_ERR_CAPACITY."""
     rng = np.random.default_rng(3)
