@@ -275,12 +275,15 @@ int numeric_launch(int32_t n, const T* A_vals, const T* B_vals, const int32_t* C
     ItemSpace is;
     is.NB = (int32_t)ceil_div<int64_t>((int64_t)n + line_positions<T>() - 1, TB);
     is.nb_per_xcd = ceil_div<int32_t>(is.NB, kNumXcd);
-    // Many C diagonals (wide operands): 4-entry chunks, 4 workgroups per CU;
-    // few: 8-entry chunks for more loads in flight, and 16 workgroups per CU
-    // (4 fit at a time; the rest queue, and the lighter share of items per
-    // workgroup balances the tail.  Measured against 8 with the operands
-    // resident in the MALL: config 4 52.9 -> 46.0 us, the square of config 2
-    // 80.6 -> 71.4 us; with cold operands, HBM-bound, about the same).
+    // 4-entry chunks.  Many C diagonals (wide operands): 4 workgroups per
+    // CU; few: 16 (8 fit at a time; the rest queue, and the lighter share of
+    // items per workgroup balances the tail.  Measured against 8 with the
+    // operands resident in the MALL: config 4 52.9 -> 46.0 us, the square of
+    // config 2 80.6 -> 71.4 us; with cold operands, HBM-bound, about the
+    // same).  8-entry chunks for the few-diagonal case (more loads in flight
+    // per lane, half the workgroups resident) measured slower on the cold
+    // lines: config 4 51.2 against 47.0 us, the square of config 1 16.9
+    // against 15.2 us (the square of config 2 111.3 against 115.5 us).
     const bool wide = c_ndiag >= 1024;
     const int per_cu = wide ? 4 : 16;
     const int64_t slots = (int64_t)cu_count() * per_cu;
@@ -290,7 +293,7 @@ int numeric_launch(int32_t n, const T* A_vals, const T* B_vals, const int32_t* C
     // light items -- at most two chunks -- are left whole, their prologue
     // being the larger cost), and flat item enumeration when there are too
     // few row blocks to give every XCD a share.
-    const int pc = wide ? 4 : 8;
+    constexpr int pc = 4;
     is.batch = kBatch;
     while (is.batch > 1 && (int64_t)is.NB * ceil_div<int64_t>(c_ndiag, is.batch) < slots &&
            std::min<int64_t>(is.batch, c_ndiag) * max_pairs > 2 * pc)
@@ -309,14 +312,9 @@ int numeric_launch(int32_t n, const T* A_vals, const T* B_vals, const int32_t* C
         is.wg_per_xcd = (int32_t)wg;
         grid = wg * kNumXcd;
     }
-    if (wide)
-        hipLaunchKernelGGL((k_gather<T, 4>), dim3((unsigned)grid), dim3(kBlock), 0,
-                           as_stream(stream), A_vals, B_vals, C_off, C_len, C_starts,
-                           (int32_t)c_ndiag, pair_ptr, pairs, C_vals, is);
-    else
-        hipLaunchKernelGGL((k_gather<T, 8>), dim3((unsigned)grid), dim3(kBlock), 0,
-                           as_stream(stream), A_vals, B_vals, C_off, C_len, C_starts,
-                           (int32_t)c_ndiag, pair_ptr, pairs, C_vals, is);
+    hipLaunchKernelGGL((k_gather<T, pc>), dim3((unsigned)grid), dim3(kBlock), 0,
+                       as_stream(stream), A_vals, B_vals, C_off, C_len, C_starts,
+                       (int32_t)c_ndiag, pair_ptr, pairs, C_vals, is);
     return check_launch(fn);
 }
 
