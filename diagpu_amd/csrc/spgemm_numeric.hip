@@ -284,12 +284,12 @@ int numeric_launch(int32_t n, const T* A_vals, const T* B_vals, const int32_t* C
     // per lane, half the workgroups resident) measured slower on the cold
     // lines: config 4 51.2 against 47.0 us, the square of config 1 16.9
     // against 15.2 us (the square of config 2 111.3 against 115.5 us).
-    // With 4096 row blocks or more (n >= 2^22 for fp32), 32: the batch then
-    // shrinks to half-size items (measured on the square of config 2:
-    // 115.6 -> 99.8 us; config 4, with 1024 row blocks, is 3.6% slower at
-    // 32, so it keeps 16).
+    // With 2048 row blocks or more, 32: the batch then shrinks to smaller
+    // items (measured: the square of config 2, 4096 row blocks, 115.6 ->
+    // 99.8 us; config 4 with complex values, 2048, 146.7 -> 132.4 us; config
+    // 4 in fp32, 1024, is 3.6% slower at 32, so it keeps 16).
     const bool wide = c_ndiag >= 1024;
-    const int per_cu = wide ? 4 : (is.NB >= 4096 ? 32 : 16);
+    const int per_cu = wide ? 4 : (is.NB >= 2048 ? 32 : 16);
     const int64_t slots = (int64_t)cu_count() * per_cu;
     // Small problems with heavy items: fewer C diagonals per item until the
     // items can fill the GPU (a batch's entries are walked by one workgroup,
