@@ -275,7 +275,7 @@ int numeric_launch(int32_t n, const T* A_vals, const T* B_vals, const int32_t* C
     ItemSpace is;
     is.NB = (int32_t)ceil_div<int64_t>((int64_t)n + line_positions<T>() - 1, TB);
     is.nb_per_xcd = ceil_div<int32_t>(is.NB, kNumXcd);
-    // 4-entry chunks.  Many C diagonals (wide operands): 4 workgroups per
+    // Many C diagonals (wide operands): 4 workgroups per
     // CU; few: 16 (8 fit at a time; the rest queue, and the lighter share of
     // items per workgroup balances the tail.  Measured against 8 with the
     // operands resident in the MALL: config 4 52.9 -> 46.0 us, the square of
@@ -297,7 +297,11 @@ int numeric_launch(int32_t n, const T* A_vals, const T* B_vals, const int32_t* C
     // light items -- at most two chunks -- are left whole, their prologue
     // being the larger cost), and flat item enumeration when there are too
     // few row blocks to give every XCD a share.
-    constexpr int pc = 4;
+    // Plans with up to 5 entries per C diagonal take 4-entry chunks; heavier
+    // ones (e.g. powers of a 7-point stencil, 6-7 entries) 8-entry chunks:
+    // the Taylor chain's products were 10% slower with 4 (k = 6: 1.255 ->
+    // 1.452 ms).
+    const int pc = (!wide && max_pairs >= 6) ? 8 : 4;
     is.batch = kBatch;
     while (is.batch > 1 && (int64_t)is.NB * ceil_div<int64_t>(c_ndiag, is.batch) < slots &&
            std::min<int64_t>(is.batch, c_ndiag) * max_pairs > 2 * pc)
@@ -316,9 +320,14 @@ int numeric_launch(int32_t n, const T* A_vals, const T* B_vals, const int32_t* C
         is.wg_per_xcd = (int32_t)wg;
         grid = wg * kNumXcd;
     }
-    hipLaunchKernelGGL((k_gather<T, pc>), dim3((unsigned)grid), dim3(kBlock), 0,
-                       as_stream(stream), A_vals, B_vals, C_off, C_len, C_starts,
-                       (int32_t)c_ndiag, pair_ptr, pairs, C_vals, is);
+    if (pc == 8)
+        hipLaunchKernelGGL((k_gather<T, 8>), dim3((unsigned)grid), dim3(kBlock), 0,
+                           as_stream(stream), A_vals, B_vals, C_off, C_len, C_starts,
+                           (int32_t)c_ndiag, pair_ptr, pairs, C_vals, is);
+    else
+        hipLaunchKernelGGL((k_gather<T, 4>), dim3((unsigned)grid), dim3(kBlock), 0,
+                           as_stream(stream), A_vals, B_vals, C_off, C_len, C_starts,
+                           (int32_t)c_ndiag, pair_ptr, pairs, C_vals, is);
     return check_launch(fn);
 }
 
