@@ -116,8 +116,8 @@ PROTOTYPES: dict[str, tuple] = {
     "diagpu_hm_to_recon_f32": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp]),
     "diagpu_hm_to_recon_c64": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp]),
     "diagpu_promote_f32_c64": (C.c_int, [_i64, _vp, _vp, _vp]),
-    "diagpu_spgemm_band_prepare": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _i32, _vp, _i64, _vp,
-                                             C.POINTER(BandInfo), _vp]),
+    "diagpu_spgemm_band_prepare": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _i32, _vp, _i64,
+                                             _vp, C.POINTER(BandInfo), _vp]),
     "diagpu_spgemm_numeric_band_f32": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp,
                                                  _vp, _vp, _i64, _vp, _vp, C.POINTER(BandInfo),
                                                  _vp, _vp]),

@@ -87,7 +87,7 @@ def build_cpp_tests() -> None:
     for src in sorted(src_dir.glob("*.cpp")):
         exe = out_dir / src.stem
         if src.stem.endswith("_cpu"):      # host-only: plain g++, no HIP
-            _run(["g++", "-O2", "-std=c++17", "-Wall", f"-I{ROOT / 'include'}", str(src),
+            _run(["g++", "-O2", "-std=c++17", "-Wall", f"-I{ROOT / 'include'}", f"-I{CSRC}", str(src),
                   f"-L{ROOT / 'oracle'}", "-loracle", "-Wl,-rpath,$ORIGIN/../../../oracle",
                   "-o", str(exe)])
             continue

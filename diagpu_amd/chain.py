@@ -19,12 +19,11 @@ from __future__ import annotations
 import time
 from dataclasses import dataclass, field
 
-import numpy as np
 import torch
 
 from . import _lib
 from .spgemm import SpgemmPlan, _check_dev
-from .spmv import _stream_handle
+from .spmv import _on_stream, _stream_handle
 from .workloads import HM, hm_layout
 
 
@@ -54,9 +53,10 @@ def as_complex(M: HM, stream=None) -> HM:
     if M.values.dtype == torch.complex64:
         return M
     _check_dev(M.values, torch.float32, "values")
-    out = torch.empty(M.values.numel(), dtype=torch.complex64, device=M.values.device)
-    _lib.call("diagpu_promote_f32_c64", M.values.numel(), M.values.data_ptr(), out.data_ptr(),
-              _stream_handle(stream))
+    with _on_stream(stream):
+        out = torch.empty(M.values.numel(), dtype=torch.complex64, device=M.values.device)
+        _lib.call("diagpu_promote_f32_c64", M.values.numel(), M.values.data_ptr(),
+                  out.data_ptr(), _stream_handle(stream))
     return HM(M.n, M.offsets, M.lengths, M.starts, out)
 
 
@@ -71,15 +71,21 @@ def _host_offsets(M: HM) -> list[int]:
 
 def axpby(alpha, X: HM, beta, Y: HM | None, stream=None) -> HM:
     """Z = alpha * X + beta * Y on the union of the two diagonal sets (complex
-    if either factor or operand is)."""
+    if either factor or operand is).  Every temporary and the kernel go on
+    `stream` (torch's current stream when None)."""
+    with _on_stream(stream):
+        return _axpby(alpha, X, beta, Y, stream)
+
+
+def _axpby(alpha, X: HM, beta, Y: HM | None, stream) -> HM:
     if Y is not None and Y.n != X.n:
         raise ValueError("X and Y must have the same dimension")
     cplx = (isinstance(alpha, complex) or isinstance(beta, complex)
             or X.values.dtype == torch.complex64
             or (Y is not None and Y.values.dtype == torch.complex64))
     if cplx:
-        X = as_complex(X)
-        Y = as_complex(Y) if Y is not None else None
+        X = as_complex(X, stream)
+        Y = as_complex(Y, stream) if Y is not None else None
     dt = torch.complex64 if cplx else torch.float32
     ox = _host_offsets(X)
     oy = _host_offsets(Y) if Y is not None else []
@@ -165,7 +171,12 @@ def power(H: HM, k: int, stats: ChainStats | None = None) -> HM:
 
 def add_identity(S: HM, sigma=1.0, stream=None) -> HM:
     """S + sigma I: in place when S holds the main diagonal, else a new
-    matrix on the union of the diagonal sets."""
+    matrix on the union of the diagonal sets (on `stream`, like axpby)."""
+    with _on_stream(stream):
+        return _add_identity(S, sigma, stream)
+
+
+def _add_identity(S: HM, sigma, stream) -> HM:
     offs = _host_offsets(S)
     dt = S.values.dtype
     if 0 not in offs:
@@ -228,42 +239,10 @@ def to_recon(M: HM, stream=None) -> tuple[torch.Tensor, torch.Tensor]:
             torch.complex64: "diagpu_hm_to_recon_c64"}.get(dt)
     if name is None:
         raise TypeError(f"unsupported value dtype {dt}")
-    r_off = torch.empty(M.ndiag, dtype=torch.int32, device=M.values.device)
-    r_val = torch.empty(M.ndiag * M.n, dtype=dt, device=M.values.device)
-    _lib.call(name, M.n, M.offsets.data_ptr(), M.starts.data_ptr(), M.ndiag,
-              M.values.data_ptr(), r_off.data_ptr(), r_val.data_ptr(), _stream_handle(stream))
+    with _on_stream(stream):
+        r_off = torch.empty(M.ndiag, dtype=torch.int32, device=M.values.device)
+        r_val = torch.empty(M.ndiag * M.n, dtype=dt, device=M.values.device)
+        _lib.call(name, M.n, M.offsets.data_ptr(), M.starts.data_ptr(), M.ndiag,
+                  M.values.data_ptr(), r_off.data_ptr(), r_val.data_ptr(),
+                  _stream_handle(stream))
     return r_off, r_val
-
-
-# ---- host helpers for tests and examples ----------------------------------
-
-def hm_to_dense(M: HM) -> np.ndarray:
-    """Dense float64 copy of a small HM matrix."""
-    n = M.n
-    offs = _host_offsets(M)
-    starts = M.starts.cpu().numpy()
-    v = M.values.cpu().numpy()
-    vals = v.astype(np.complex128 if np.iscomplexobj(v) else np.float64)
-    D = np.zeros((n, n), vals.dtype)
-    for d, s in zip(offs, starts):
-        ln = n - abs(d)
-        r = np.arange(ln) + max(-d, 0)
-        D[r, r + d] = vals[s: s + ln]
-    return D
-
-
-def hm_matvec64(M: HM, x: np.ndarray) -> np.ndarray:
-    """y = M x in float64 (complex128 for complex M or x) over the HM
-    diagonals (host)."""
-    n = M.n
-    offs = _host_offsets(M)
-    starts = M.starts.cpu().numpy()
-    v = M.values.cpu().numpy()
-    cplx = np.iscomplexobj(v) or np.iscomplexobj(x)
-    vals = v.astype(np.complex128 if cplx else np.float64)
-    y = np.zeros(n, np.complex128 if cplx else np.float64)
-    for d, s in zip(offs, starts):
-        ln = n - abs(d)
-        r0 = max(-d, 0)
-        y[r0: r0 + ln] += vals[s: s + ln] * x[r0 + d: r0 + d + ln]
-    return y

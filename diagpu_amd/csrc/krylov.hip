@@ -24,7 +24,7 @@
 // After m steps the host reads alpha and beta (the only synchronisation, one
 // copy), forms T_m = tridiag(beta, alpha, beta) and evaluates
 // c = exp(-i t T_m) e_1 in fp64 (expm_tridiag_e1: scaled Taylor steps on the
-// tridiagonal, no eigendecomposition).  One combine kernel then writes
+// tridiagonal, scaling and squaring for large t, no eigendecomposition).  One combine kernel then writes
 // psi(t) = ||psi_0|| sum_j c_j v_j.  A beta_j that vanishes relative to
 // |alpha_j| + beta_{j-1} marks an invariant subspace: the expansion stops
 // there and is exact (up to rounding).  The a posteriori error estimate
@@ -34,6 +34,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "expm_tridiag.hpp"
 #include "reduce.hpp"
 #include "spmv_internal.hpp"
 
@@ -164,52 +165,6 @@ __global__ __launch_bounds__(kVB) void k_combine(const cf32* __restrict__ first,
     st2(out, i, n, acc);
 }
 
-// c = exp(-i t T) e_1 for the m x m symmetric tridiagonal T (diagonal al,
-// off-diagonal be[0..m-2]), in complex128, without an eigendecomposition:
-// t is split into s sub-steps with ||t T / s|| <= 2 (Gershgorin bound), and
-// each sub-step applies exp(-i (t/s) T) to the vector as a Taylor series of
-// tridiagonal products, stopped when a term falls below 1e-17 of the sum (at
-// most 50 terms: 2^50 / 50! ~ 1e-50).  With the norm of each sub-step at most
-// 2 no term exceeds 2 times the sum's scale, so nothing cancels; the cost is
-// O(s K m), tens of microseconds for m <= 64 (a cyclic Jacobi
-// eigendecomposition of T took 276 us at m = 30).
-std::vector<std::complex<double>> expm_tridiag_e1(int m, const std::vector<double>& al,
-                                                 const std::vector<double>& be, double t)
-{
-    typedef std::complex<double> cd;
-    double gersh = 0.0;
-    for (int i = 0; i < m; ++i) {
-        const double r = std::fabs(al[i]) + (i > 0 ? std::fabs(be[i - 1]) : 0.0) +
-                         (i + 1 < m ? std::fabs(be[i]) : 0.0);
-        gersh = r > gersh ? r : gersh;
-    }
-    const double nrm = gersh * std::fabs(t);
-    const int steps = nrm > 2.0 ? (int)std::ceil(nrm / 2.0) : 1;
-    const cd h(0.0, -t / steps);
-    std::vector<cd> c(m, cd(0.0)), term(m), next(m);
-    c[0] = 1.0;
-    for (int st = 0; st < steps; ++st) {
-        term = c;
-        for (int k = 1; k <= 50; ++k) {
-            double tn = 0.0, cn = 0.0;
-            for (int i = 0; i < m; ++i) {
-                cd v = al[i] * term[i];
-                if (i > 0) v += be[i - 1] * term[i - 1];
-                if (i + 1 < m) v += be[i] * term[i + 1];
-                next[i] = v * (h / (double)k);
-            }
-            for (int i = 0; i < m; ++i) {
-                term[i] = next[i];
-                c[i] += term[i];
-                tn = std::max(tn, std::fabs(term[i].real()) + std::fabs(term[i].imag()));
-                cn = std::max(cn, std::fabs(c[i].real()) + std::fabs(c[i].imag()));
-            }
-            if (tn <= 1e-17 * cn) break;
-        }
-    }
-    return c;
-}
-
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 struct Layout {
@@ -329,7 +284,9 @@ int expm_krylov(int32_t rows, int32_t cols, int32_t K, const int32_t* offs, cons
     Coefs cf{};
     double err = 0.0;
     if (meff > 0) {
-        const std::vector<std::complex<double>> c = expm_tridiag_e1(meff, al, be, t);
+        std::vector<std::complex<double>> c;
+        if (!expm_tridiag_e1(meff, al, be, t, c))
+            return fail(DIAGPU_ERR_ARG, "%s: t T_m is not finite (|t| = %g)", fn, std::fabs(t));
         for (int j = 1; j <= meff; ++j) {
             // psi(t) = ||psi0|| sum c_j v_j, v_j = u_j / s_j, s_j = sqrt(q[j-1])
             const std::complex<double> g = nrm0 * c[j - 1] / std::sqrt(hq[j - 1]);

@@ -57,12 +57,17 @@ bool band_fits(int64_t lds_bytes, int64_t n_pairs)
 // entries[g] = {a kRB, b WB + (da - min da), da, 0}, a and b the indices of
 // pairs[g].ab in A_starts and of pairs[g].bb in B_starts, WB =
 // window_rows(span).  span[0..1] = min, max da (k_span, which
-// runs first on the stream); span[2] is set if an entry matches no diagonal.
-__global__ __launch_bounds__(256) void k_band_prepare(const diagpu_gpair* __restrict__ pairs,
+// runs first on the stream); span[2] is set if an entry matches no diagonal
+// or differs from the entry the symbolic phase makes for its two diagonals
+// (the band kernel derives each term's shifts and bounds from the operand
+// offsets, so it must be handed exactly that plan).
+__global__ __launch_bounds__(256) void k_band_prepare(int32_t n,
+                                                      const diagpu_gpair* __restrict__ pairs,
                                                       int64_t n_pairs,
                                                       const int32_t* __restrict__ A_off,
                                                       const int64_t* __restrict__ A_starts,
                                                       int32_t nA,
+                                                      const int32_t* __restrict__ B_off,
                                                       const int64_t* __restrict__ B_starts,
                                                       int32_t nB, int4* __restrict__ entries,
                                                       int32_t* __restrict__ span)
@@ -85,13 +90,24 @@ __global__ __launch_bounds__(256) void k_band_prepare(const diagpu_gpair* __rest
     const diagpu_gpair p = pairs[g];
     const int a = find(A_starts, nA, (int64_t)p.ab);
     const int b = find(B_starts, nB, (int64_t)p.bb);
-    if (a < 0 || b < 0) {
+    bool ok = a >= 0 && b >= 0;
+    int da = 0;
+    if (ok) {
+        da = A_off[a];
+        const int db = B_off[b];
+        const int64_t dc = (int64_t)da + db;
+        auto min0 = [](int64_t x) { return x < 0 ? x : (int64_t)0; };
+        auto absl = [](int64_t x) { return x < 0 ? -x : x; };
+        ok = dc > -(int64_t)n && dc < n && (int64_t)p.ash == min0(da) - min0(dc) &&
+             (int64_t)p.bsh == da + min0(db) - min0(dc) && (int64_t)p.al == n - absl(da) &&
+             (int64_t)p.bl == n - absl(db);
+    }
+    if (!ok) {
         span[2] = 1;   // every writer stores the same value
         entries[g] = int4{0, 0, 0, 0};
         return;
     }
     const int lo = span[0], wb = window_rows(span[1] - span[0]);
-    const int da = A_off[a];
     entries[g] = int4{a * kRB, b * wb + (da - lo), da, 0};
 }
 
@@ -301,7 +317,7 @@ extern "C" {
 
 DIAGPU_API int diagpu_spgemm_band_prepare(int32_t n, const int32_t* A_off,
                                           const int64_t* A_starts, int32_t nA,
-                                          const int64_t* B_starts, int32_t nB,
+                                          const int32_t* B_off, const int64_t* B_starts, int32_t nB,
                                           const diagpu_gpair* pairs, int64_t n_pairs,
                                           int32_t* entries, diagpu_band_info* info, void* stream)
 {
@@ -313,7 +329,7 @@ DIAGPU_API int diagpu_spgemm_band_prepare(int32_t n, const int32_t* A_off,
         return fail(DIAGPU_ERR_ARG, "%s: need n, nA, nB >= 1 and n_pairs >= 0", fn);
     if (nA > 65535 || nB > 32767)
         return fail(DIAGPU_ERR_ARG, "%s: at most 65535 A and 32767 B diagonals", fn);
-    if (!A_off || !A_starts || !B_starts || !entries || (n_pairs > 0 && !pairs))
+    if (!A_off || !A_starts || !B_off || !B_starts || !entries || (n_pairs > 0 && !pairs))
         return fail(DIAGPU_ERR_ARG, "%s: a pointer is NULL", fn);
     hipStream_t s = as_stream(stream);
     int32_t* dev = entries + 4 * n_pairs;   // caller's 4 scratch ints: A span, bad-entry flag
@@ -322,14 +338,16 @@ DIAGPU_API int diagpu_spgemm_band_prepare(int32_t n, const int32_t* A_off,
     int st = check_launch(fn);
     if (!st && n_pairs > 0) {
         hipLaunchKernelGGL(k_band_prepare, dim3((unsigned)ceil_div<int64_t>(n_pairs, 256)),
-                           dim3(256), 0, s, pairs, n_pairs, A_off, A_starts, nA, B_starts, nB,
-                           reinterpret_cast<int4*>(entries), dev);
+                           dim3(256), 0, s, n, pairs, n_pairs, A_off, A_starts, nA, B_off,
+                           B_starts, nB, reinterpret_cast<int4*>(entries), dev);
         st = check_launch(fn);
     }
     if (!st) st = check_hip(hipMemcpyAsync(host, dev, sizeof(host), hipMemcpyDeviceToHost, s), fn);
     if (!st) st = check_hip(hipStreamSynchronize(s), fn);
     if (st) return st;
-    if (host[2]) return fail(DIAGPU_ERR_ARG, "%s: a plan entry's start is not an operand diagonal's start", fn);
+    if (host[2])
+        return fail(DIAGPU_ERR_ARG, "%s: a plan entry's starts are no operand diagonals' starts, or "
+                    "its shifts or lengths are not the symbolic phase's for those diagonals", fn);
     if (host[0] <= -n || host[1] >= n)
         return fail(DIAGPU_ERR_OFFSET, "%s: an A offset is outside (-n, n)", fn);
     info->a_off_min = host[0];

@@ -149,7 +149,7 @@ __global__ __launch_bounds__(kBlock) void k_gather(
         V acc;
 #pragma unroll
         for (int e = 0; e < E; ++e) acc.v[e] = zero_of<T>();
-        int cur = -1;
+        int cur = -1;   // C diagonal of the batch being accumulated
         auto flush = [&](int ci) {
             const DiagRec d = drec[ci];
             const int64_t p = d.P0 + p_lane;
@@ -161,6 +161,16 @@ __global__ __launch_bounds__(kBlock) void k_gather(
                 for (int e = 0; e < E; ++e)
                     if (p + e >= 0 && p + e < d.len) cp[p + e] = acc.v[e];
             }
+        };
+        // Close diagonal `cur` and move to diagonal `to` of the batch: the
+        // diagonals in between have no plan entry and are written as zeros
+        // (every C value is written, whatever the plan holds).
+        auto advance = [&](int to) {
+            if (cur >= 0) flush(cur);
+#pragma unroll
+            for (int e = 0; e < E; ++e) acc.v[e] = zero_of<T>();
+            for (int z = cur + 1; z < to; ++z) flush(z);
+            cur = to;
         };
 
         for (int64_t gq = gb; gq < ge; gq += kBlock) {
@@ -213,12 +223,7 @@ __global__ __launch_bounds__(kBlock) void k_gather(
                     for (int c = 0; c < PC; ++c) {
                         if (s0 + c >= cnt) continue;
                         const PairRec r = prec[s0 + c];
-                        if (r.ci != cur) {
-                            if (cur >= 0) flush(cur);
-#pragma unroll
-                            for (int e = 0; e < E; ++e) acc.v[e] = zero_of<T>();
-                            cur = r.ci;
-                        }
+                        if (r.ci != cur) advance(r.ci);
                         if (r.cover > 0) {
 #pragma unroll
                             for (int e = 0; e < E; ++e) acc.v[e] = mac(acc.v[e], a[c].v[e], b[c].v[e]);
@@ -227,12 +232,7 @@ __global__ __launch_bounds__(kBlock) void k_gather(
                 } else {
                     for (int c = 0; c < PC && s0 + c < cnt; ++c) {
                         const PairRec r = prec[s0 + c];
-                        if (r.ci != cur) {
-                            if (cur >= 0) flush(cur);
-#pragma unroll
-                            for (int e = 0; e < E; ++e) acc.v[e] = zero_of<T>();
-                            cur = r.ci;
-                        }
+                        if (r.ci != cur) advance(r.ci);
                         if (r.cover < 0) continue;
                         const int64_t p = drec[r.ci].P0 + p_lane;
                         T av[E], bv[E];
@@ -251,7 +251,7 @@ __global__ __launch_bounds__(kBlock) void k_gather(
                 }
             }
         }
-        if (cur >= 0) flush(cur);
+        advance(gv);
     }
 }
 

@@ -45,8 +45,9 @@ def expm_krylov(offsets: torch.Tensor, values: torch.Tensor, n: int, psi0: torch
                 workspace: KrylovWorkspace | None = None, stream=None) -> KrylovResult:
     """exp(-i t H) psi0 for the Hermitian n x n Recon matrix (offsets, values);
     values float32 (real symmetric H) or complex64; psi0 complex64 [n]."""
-    if psi0.dtype != torch.complex64 or not psi0.is_cuda or psi0.numel() != n:
-        raise TypeError("psi0 must be a complex64 device tensor of n elements")
+    if (psi0.dtype != torch.complex64 or not psi0.is_cuda or psi0.numel() != n
+            or not psi0.is_contiguous()):
+        raise TypeError("psi0 must be a contiguous complex64 device tensor of n elements")
     view = recon_view(offsets, values, n, n)
     name = {torch.complex64: "diagpu_expm_krylov_c64",
             torch.float32: "diagpu_expm_krylov_f32"}.get(values.dtype)
@@ -56,6 +57,11 @@ def expm_krylov(offsets: torch.Tensor, values: torch.Tensor, n: int, psi0: torch
         workspace = KrylovWorkspace(n, m, psi0.device)
     if out is None:
         out = torch.empty_like(psi0)
+    if (out.dtype != torch.complex64 or not out.is_cuda or out.numel() != n
+            or not out.is_contiguous()):
+        raise TypeError("out must be a contiguous complex64 device tensor of n elements")
+    if out.data_ptr() == psi0.data_ptr():
+        raise ValueError("out must not overlap psi0")
     alpha = np.zeros(m, np.float64)
     beta = np.zeros(m, np.float64)
     info = _lib.KrylovInfo()

@@ -40,6 +40,10 @@ class SpgemmPlan:
             _check_dev(M.starts, torch.int64, f"{nm}.starts")
         self.A, self.B, self.n = A, B, A.n
         self.stream = stream
+        # values each operand must hold: the end of its furthest diagonal
+        self.a_need, self.b_need = (
+            int((M.starts + M.lengths).max().item()) if M.offsets.numel() else 0
+            for M in (A, B))
         dev = A.offsets.device
         na, nb = A.offsets.numel(), B.offsets.numel()
         self.c_cap = max(1, min(na * nb, 2 * self.n - 1))
@@ -101,9 +105,10 @@ class SpgemmPlan:
                               device=self.C_off.device)
             info = _lib.BandInfo()
             _lib.call("diagpu_spgemm_band_prepare", self.n, A.offsets.data_ptr(),
-                      A.starts.data_ptr(), A.offsets.numel(), B.starts.data_ptr(),
-                      B.offsets.numel(), self.pairs.data_ptr(), self.info.n_pairs,
-                      pab.data_ptr(), C.byref(info), _stream_handle(self.stream))
+                      A.starts.data_ptr(), A.offsets.numel(), B.offsets.data_ptr(),
+                      B.starts.data_ptr(), B.offsets.numel(), self.pairs.data_ptr(),
+                      self.info.n_pairs, pab.data_ptr(), C.byref(info),
+                      _stream_handle(self.stream))
             self._band = (pab, info)
         return self._band
 
@@ -180,6 +185,9 @@ class SpgemmPlan:
         _check_dev(A_vals, dt, "A_vals")
         _check_dev(B_vals, dt, "B_vals")
         _check_dev(C_vals, dt, "C_vals")
+        if A_vals.numel() < self.a_need or B_vals.numel() < self.b_need:
+            raise ValueError(f"A_vals / B_vals hold {A_vals.numel()} / {B_vals.numel()} values; "
+                             f"the plan's operands need {self.a_need} / {self.b_need}")
         if C_vals.numel() < self.info.c_nnz:
             raise ValueError(f"C_vals has {C_vals.numel()} elements, needs {self.info.c_nnz}")
         if kernel == "auto":

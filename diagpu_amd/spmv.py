@@ -7,11 +7,23 @@ diagpu_spmv_recon_f32 / _f64 / _c64 / _f32_c64 in libdiagpu.so.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes as C
 
 import torch
 
 from . import _lib
+
+
+def _on_stream(stream):
+    """Context in which torch allocates and launches on `stream` (a
+    torch.cuda.Stream, a raw HIP stream handle, or None for the current
+    stream), so a wrapper's temporaries are ordered with its kernels."""
+    if stream is None:
+        return contextlib.nullcontext()
+    if not isinstance(stream, torch.cuda.Stream):
+        stream = torch.cuda.ExternalStream(int(stream))
+    return torch.cuda.stream(stream)
 
 
 def _stream_handle(stream) -> int:
@@ -54,12 +66,12 @@ def spmv_recon(offsets: torch.Tensor, values: torch.Tensor, rows: int, cols: int
     float32 values with a complex64 x (y takes x's dtype)."""
     view = recon_view(offsets, values, rows, cols)
     name = _SPMV.get((values.dtype, x.dtype))
-    if name is None or not x.is_cuda:
-        raise TypeError(f"unsupported (values, x) dtypes ({values.dtype}, {x.dtype}) "
-                        "or x not on the device")
+    if name is None or not x.is_cuda or not x.is_contiguous():
+        raise TypeError(f"unsupported (values, x) dtypes ({values.dtype}, {x.dtype}), "
+                        "or x not a contiguous device tensor")
     if y is None:
         y = torch.empty(rows, dtype=x.dtype, device=values.device)
-    if y.dtype != x.dtype or y.numel() < rows or not y.is_cuda:
-        raise TypeError("y must be a device tensor of x's dtype with >= rows elements")
+    if y.dtype != x.dtype or y.numel() < rows or not y.is_cuda or not y.is_contiguous():
+        raise TypeError("y must be a contiguous device tensor of x's dtype with >= rows elements")
     _lib.call(name, C.byref(view), x.data_ptr(), x.numel(), y.data_ptr(), _stream_handle(stream))
     return y

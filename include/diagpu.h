@@ -261,11 +261,16 @@ typedef struct diagpu_band_info {
  * indices of its A and B diagonals (looked up from the entry's starts), and
  * A's offset span in *info.  entries holds 4 n_pairs + 4 int32 (the last 4
  * are scratch).  One stream synchronisation (to return *info).
- * DIAGPU_ERR_OFFSET if an A offset lies outside (-n, n).  No reference
+ * DIAGPU_ERR_OFFSET if an A offset lies outside (-n, n); DIAGPU_ERR_ARG if an
+ * entry's starts are not the starts of an A and a B diagonal, or if its
+ * ash, bsh, al, bl differ from what diagpu_spgemm_symbolic writes for those
+ * two diagonals (the band kernel computes each term's shifts and bounds from
+ * the operand offsets, so it takes only such plans).  No reference
  * counterpart: the LDS-tiled form of the numeric phase below. */
 DIAGPU_API int diagpu_spgemm_band_prepare(int32_t n, const int32_t* A_off,
                                           const int64_t* A_starts, int32_t nA,
-                                          const int64_t* B_starts, int32_t nB,
+                                          const int32_t* B_off, const int64_t* B_starts,
+                                          int32_t nB,
                                           const diagpu_gpair* pairs, int64_t n_pairs,
                                           int32_t* entries, diagpu_band_info* info,
                                           void* stream);

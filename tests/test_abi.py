@@ -156,11 +156,13 @@ def test_complex_and_krylov_argument_errors():
     assert _status("diagpu_promote_f32_c64", 5, None, fake, None) == _lib.ERR_ARG
     assert _status("diagpu_promote_f32_c64", 0, None, None, None) == _lib.OK
     band = _lib.BandInfo()
-    assert _status("diagpu_spgemm_band_prepare", 0, fake, fake, 1, fake, 1, fake, 1, fake,
+    assert _status("diagpu_spgemm_band_prepare", 0, fake, fake, 1, fake, fake, 1, fake, 1, fake,
                    C.byref(band), None) == _lib.ERR_ARG
-    assert _status("diagpu_spgemm_band_prepare", 100, fake, fake, 70000, fake, 1, fake, 1, fake,
+    assert _status("diagpu_spgemm_band_prepare", 100, fake, fake, 70000, fake, fake, 1, fake, 1,
+                   fake, C.byref(band), None) == _lib.ERR_ARG
+    assert _status("diagpu_spgemm_band_prepare", 100, None, fake, 1, fake, fake, 1, fake, 1, fake,
                    C.byref(band), None) == _lib.ERR_ARG
-    assert _status("diagpu_spgemm_band_prepare", 100, None, fake, 1, fake, 1, fake, 1, fake,
+    assert _status("diagpu_spgemm_band_prepare", 100, fake, fake, 1, None, fake, 1, fake, 1, fake,
                    C.byref(band), None) == _lib.ERR_ARG
     # numeric_band needs an eligible, consistent info (validated before any launch)
     band = _lib.BandInfo(0, 4, 256, 1, 4 * (3 * 256 + 2 * 260) + 16 * 7, 7)
@@ -191,3 +193,4 @@ def test_astat_max_a_matches_header():
     m = re.search(r"#define DIAGPU_ASTAT_MAX_A (\d+)", hdr)
     assert m and int(m.group(1)) == _lib.ASTAT_MAX_A
     assert 288 * _lib.ASTAT_MAX_A * 4 <= 80 * 1024 < 288 * (_lib.ASTAT_MAX_A + 1) * 4
+

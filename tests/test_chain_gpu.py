@@ -19,6 +19,7 @@ import torch
 
 from diagpu_amd import chain
 from diagpu_amd.workloads import hm_random, hm_stencil7
+from hm_host import dense_of, matvec64
 
 pytestmark = pytest.mark.gpu
 
@@ -33,10 +34,10 @@ def test_axpby_union(dev):
     Y = hm_random(n, [-5, 1, 2, 100], 2, dev)
     Z = chain.axpby(0.75, X, -1.5, Y)
     assert Z.offsets.cpu().tolist() == [-5, 0, 1, 2, 100]
-    Xd, Yd = chain.hm_to_dense(X), chain.hm_to_dense(Y)
+    Xd, Yd = dense_of(X), dense_of(Y)
     want = 0.75 * Xd - 1.5 * Yd
     bound = 0.75 * np.abs(Xd) + 1.5 * np.abs(Yd)
-    assert np.all(np.abs(chain.hm_to_dense(Z) - want) <= 1.2e-7 * bound)
+    assert np.all(np.abs(dense_of(Z) - want) <= 1.2e-7 * bound)
 
 
 def test_axpby_zero_factor_does_not_read(dev):
@@ -46,9 +47,9 @@ def test_axpby_zero_factor_does_not_read(dev):
     Y.values.fill_(float("nan"))
     Z = chain.axpby(2.0, X, 0.0, Y)
     assert Z.offsets.cpu().tolist() == [-1, 0, 1, 4]
-    D = chain.hm_to_dense(Z)
+    D = dense_of(Z)
     assert np.isfinite(D).all()
-    assert np.array_equal(D, 2.0 * chain.hm_to_dense(X))   # exact: scaling by 2
+    assert np.array_equal(D, 2.0 * dense_of(X))   # exact: scaling by 2
 
 
 def test_axpby_rejects_unsorted(dev):
@@ -68,14 +69,14 @@ def test_axpby_rejects_unsorted(dev):
 def test_power_against_dense(dev, n, offs, k):
     H = hm_random(n, offs, 10 + k, dev)
     P = chain.power(H, k)
-    Hd = chain.hm_to_dense(H)
+    Hd = dense_of(H)
     want = np.linalg.matrix_power(Hd, k)
     bound = np.linalg.matrix_power(np.abs(Hd), k)
     expect = offs
     for _ in range(k - 1):
         expect = _sumset(expect, offs, n)
     assert P.offsets.cpu().tolist() == expect
-    err = np.abs(chain.hm_to_dense(P) - want)
+    err = np.abs(dense_of(P) - want)
     assert np.all(err <= 1e-5 * k * bound + 1e-30), float((err / (bound + 1e-30)).max())
 
 
@@ -88,12 +89,12 @@ def test_taylor_against_expm(dev, n, offs, t, order):
     stats = chain.ChainStats()
     S = chain.taylor_expm(H, t, order, stats)
     assert len(stats.numeric) == order - 1 and len(stats.axpby) == 2 * order - 1
-    Hd = chain.hm_to_dense(H)
+    Hd = dense_of(H)
     want = scipy.linalg.expm(t * Hd)
     bound = scipy.linalg.expm(t * np.abs(Hd))
     norm = t * np.abs(Hd).sum(axis=1).max()
     trunc = norm ** (order + 1) / math.factorial(order + 1) * math.exp(norm)
-    err = np.abs(chain.hm_to_dense(S) - want)
+    err = np.abs(dense_of(S) - want)
     assert np.all(err <= 1e-5 * order * bound + trunc)
     # every offset reachable in at most `order` steps is present
     reach, frontier = {0}, [0]
@@ -106,22 +107,22 @@ def test_taylor_against_expm(dev, n, offs, t, order):
 def test_add_identity_in_place_and_union(dev):
     n = 90
     S = hm_random(n, [-3, 0, 2], 12, dev)
-    before = chain.hm_to_dense(S)
+    before = dense_of(S)
     ptr = S.values.data_ptr()
     T = chain.add_identity(S, 0.5)
     assert T is S and T.values.data_ptr() == ptr        # main diagonal present: in place
     want = before.astype(np.float32) + np.float32(0.5) * np.eye(n, dtype=np.float32)  # one fp32 rounding
-    assert np.array_equal(chain.hm_to_dense(T), want.astype(np.float64))
+    assert np.array_equal(dense_of(T), want.astype(np.float64))
     U = hm_random(n, [-3, 2], 13, dev)
     V = chain.add_identity(U, 2.0)                       # no main diagonal: union
     assert V.offsets.cpu().tolist() == [-3, 0, 2]
-    assert np.array_equal(chain.hm_to_dense(V), chain.hm_to_dense(U) + 2.0 * np.eye(n))
+    assert np.array_equal(dense_of(V), dense_of(U) + 2.0 * np.eye(n))
 
 
 def test_taylor_order_zero_is_identity(dev):
     H = hm_random(64, [-1, 1], 9, dev)
     S = chain.taylor_expm(H, 1.0, 0)
-    assert np.array_equal(chain.hm_to_dense(S), np.eye(64))
+    assert np.array_equal(dense_of(S), np.eye(64))
 
 
 def test_taylor_stencil_2pow20(dev):
@@ -135,9 +136,9 @@ def test_taylor_stencil_2pow20(dev):
     x = rng.uniform(-1.0, 1.0, H.n)
     want, v = x.copy(), x.copy()
     for k in range(1, order + 1):
-        v = chain.hm_matvec64(H, v)
+        v = matvec64(H, v)
         want += t ** k / math.factorial(k) * v
-    got = chain.hm_matvec64(S, x)
+    got = matvec64(S, x)
     # the stencil's absolute row sums are <= 12, so sum_k t^k/k! (|H|^k |x|) <= this
     abs_bound = sum((t * 12) ** k / math.factorial(k) for k in range(order + 1)) * np.abs(x).max()
     assert np.all(np.abs(got - want) <= 1e-5 * order * abs_bound)

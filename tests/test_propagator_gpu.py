@@ -23,6 +23,7 @@ from diagpu_amd import chain
 from diagpu_amd.krylov import expm_krylov
 from diagpu_amd.spmv import spmv_recon
 from diagpu_amd.workloads import HM, hm_random, hm_stencil7
+from hm_host import dense_of, matvec64
 
 pytestmark = pytest.mark.gpu
 
@@ -70,7 +71,7 @@ def test_hm_to_recon_matches_reference_build_recon(dev, oracle):
         # and the SpMV of the Recon form is the HM matrix's product
         x = np.random.default_rng(5).standard_normal(n).astype(np.complex64)
         y = spmv_recon(r_off, r_val, n, n, torch.as_tensor(x, device=dev)).cpu().numpy()
-        assert np.allclose(y, chain.hm_matvec64(M, x.astype(np.complex128)), rtol=0, atol=1e-4)
+        assert np.allclose(y, matvec64(M, x.astype(np.complex128)), rtol=0, atol=1e-4)
 
 
 @pytest.mark.parametrize("count", [1, 2, 7, 1 << 20, (1 << 20) + 3])
@@ -95,15 +96,15 @@ def test_complex_axpby(dev):
     a, b = 0.5 - 1.25j, -2.0 + 0.5j
     Z = chain.axpby(a, X, b, Y)
     assert Z.values.dtype == torch.complex64 and Z.offsets.cpu().tolist() == [-4, 0, 9, 50]
-    Xd, Yd = chain.hm_to_dense(X), chain.hm_to_dense(Y)
+    Xd, Yd = dense_of(X), dense_of(Y)
     want = a * Xd + b * Yd
     bound = abs(a) * np.abs(Xd) + abs(b) * np.abs(Yd)
     # fp32 complex products and sum: |err| <= sqrt(2) * 4 * 2^-24 * bound
-    assert np.all(np.abs(chain.hm_to_dense(Z) - want) <= 4e-7 * bound + 1e-30)
+    assert np.all(np.abs(dense_of(Z) - want) <= 4e-7 * bound + 1e-30)
     # a zero complex factor does not read its operand
     Y.values.fill_(complex("nan+nanj"))
     Z0 = chain.axpby(2.0j, X, 0j, Y)
-    D0 = chain.hm_to_dense(Z0)
+    D0 = dense_of(Z0)
     assert np.isfinite(D0).all() and np.allclose(D0, 2.0j * Xd, rtol=0, atol=1e-6)
 
 
@@ -111,11 +112,11 @@ def test_complex_axpby(dev):
 def test_propagator_matches_expm(dev, complex_values):
     n, dt, order = 240, 0.05, 10
     H = _hermitian_hm(n, [0, 1, 3, 17], 7, dev, complex_values)
-    Hd = chain.hm_to_dense(H).astype(np.complex128)
+    Hd = dense_of(H).astype(np.complex128)
     assert np.allclose(Hd, Hd.conj().T)
     U = chain.propagator(H, dt, order)
     assert U.values.dtype == torch.complex64
-    Ud = chain.hm_to_dense(U)
+    Ud = dense_of(U)
     want = scipy.linalg.expm(-1j * dt * Hd)
     nrm = np.abs(Hd).sum(axis=1).max() * dt          # ||dt H||_inf
     trunc = nrm ** (order + 1) / math.factorial(order + 1) * math.exp(nrm)

@@ -463,8 +463,9 @@ def test_plan_entries_without_positions(dev):
     al = 0 on the device, the A-stationary records mark them {a, 1, 1, 0}
     (a record that never fires and loads B[0]), both kernels return the same
     bits, and those bits differ from the full plan's product on exactly the
-    C diagonals of the emptied entries.  (The band kernel derives each
-    term's validity from the operands' offsets, not from the entry.)"""
+    C diagonals of the emptied entries.  The band kernel derives each
+    term's validity from the operands' offsets, not from the entry, so its
+    prepare step refuses the edited plan (DIAGPU_ERR_ARG)."""
     n = 3000
     A = workloads.hm_random(n, list(range(-20, 21, 4)), 41, dev)
     B = workloads.hm_random(n, [-2999, -700, 0, 5, 2998], 42, dev)
@@ -480,6 +481,10 @@ def test_plan_entries_without_positions(dev):
     Cg = plan.multiply(A.values, B.values, kernel="gather")
     Ca = plan.multiply(A.values, B.values, kernel="astat")
     assert torch.equal(Cg.view(torch.int32), Ca.view(torch.int32))
+    plan._band = None
+    with pytest.raises(_lib.DiagpuError) as e:
+        plan.band_info()
+    assert e.value.status == _lib.ERR_ARG and "symbolic" in str(e.value)
     full = SpgemmPlan(A, B)
     Cf = full.multiply(A.values, B.values, kernel="gather")
     ptr = full.pair_ptr().cpu().numpy()
@@ -489,3 +494,95 @@ def test_plan_entries_without_positions(dev):
     diff = (Cg != Cf).cpu().numpy()
     for k in range(full.info.c_ndiag):
         assert diff[c_st[k]: c_st[k] + c_len[k]].any() == touched[k], k
+
+
+def _drop_diagonals(plan, empty):
+    """Remove every plan entry of the C diagonals `empty` (their pair_ptr
+    ranges become empty); returns the kept entries' mask."""
+    nc, npair = plan.info.c_ndiag, plan.info.n_pairs
+    ptr = plan.pair_ptr().cpu().numpy()
+    pairs = plan.pairs_numpy().copy()
+    keep = np.ones(npair, bool)
+    counts = np.diff(ptr)
+    for k in empty:
+        keep[ptr[k]: ptr[k + 1]] = False
+        counts[k] = 0
+    new_ptr = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    kept = pairs[keep]
+    plan.ptr[: nc + 1].copy_(torch.as_tensor(new_ptr))
+    plan.pairs[: kept.size * 32].copy_(torch.as_tensor(kept.view(np.uint8)))
+    plan.info.n_pairs = int(kept.size)
+    plan.info.max_pairs = int(counts.max())
+    plan._band = None
+    plan._astat = None
+    return keep
+
+
+@pytest.mark.parametrize("n", [5000, 1 << 17])
+def test_empty_c_diagonals_written_as_zero(dev, n):
+    """A caller's plan may give a C diagonal no entry at all (pair_ptr[k] ==
+    pair_ptr[k + 1]), or a whole batch of diagonals none: every kernel still
+    writes every C value, zeros there, and the other diagonals keep the full
+    plan's bits.  C starts out as NaN so an unwritten value shows."""
+    A = workloads.hm_random(n, list(range(-10, 11)), 51, dev)
+    B = workloads.hm_random(n, list(range(-8, 9)), 52, dev)
+    full = SpgemmPlan(A, B)
+    Cf = full.multiply(A.values, B.values, kernel="gather")
+    plan = SpgemmPlan(A, B)
+    nc = plan.info.c_ndiag
+    assert nc == 37
+    empty = [0, *range(5, 23), nc - 2, nc - 1]    # first, 18 in a row, the last two
+    _drop_diagonals(plan, empty)
+    c_st, c_len = plan.c_starts().cpu().numpy(), plan.c_lengths().cpu().numpy()
+    zero = np.zeros(plan.info.c_nnz, bool)
+    for k in empty:
+        zero[c_st[k]: c_st[k] + c_len[k]] = True
+    want = Cf.cpu().numpy().copy()
+    want[zero] = 0.0
+    for kernel in ("gather", "band", "astat"):
+        Cv = torch.full((plan.info.c_nnz,), float("nan"), device=dev)
+        plan.numeric(A.values, B.values, Cv, kernel=kernel)
+        got = Cv.cpu().numpy()
+        assert np.array_equal(got.view(np.int32), want.view(np.int32)), kernel
+
+
+def test_plan_with_no_entries(dev):
+    """A plan whose every C diagonal is empty: all of C is written as 0."""
+    n = 3000
+    A = workloads.hm_random(n, [-3, 0, 2], 61, dev)
+    B = workloads.hm_random(n, [-1, 0, 4], 62, dev)
+    plan = SpgemmPlan(A, B)
+    _drop_diagonals(plan, range(plan.info.c_ndiag))
+    assert plan.info.n_pairs == 0
+    Cv = torch.full((plan.info.c_nnz,), float("nan"), device=dev)
+    plan.numeric(A.values, B.values, Cv, kernel="gather")
+    assert torch.equal(Cv, torch.zeros_like(Cv))
+
+
+def test_wrappers_reject_short_or_strided_operands(dev):
+    """The Python wrappers check operand sizes and layouts before any launch:
+    a value tensor shorter than its plan's operand, a strided x, psi0 or
+    out, or out aliasing psi0."""
+    from diagpu_amd.krylov import expm_krylov
+    from diagpu_amd.spmv import spmv_recon
+    A = workloads.hm_random(4000, [-5, 0, 7], 71, dev)
+    B = workloads.hm_random(4000, [-2, 0, 1], 72, dev)
+    plan = SpgemmPlan(A, B)
+    Cv = torch.empty(plan.info.c_nnz, device=dev)
+    with pytest.raises(ValueError):
+        plan.numeric(A.values[:-1], B.values, Cv)
+    with pytest.raises(ValueError):
+        plan.numeric(A.values, B.values[: B.values.numel() // 2], Cv)
+    R = workloads.recon_random(1000, [-3, 0, 3], 73, dev)
+    x2 = torch.randn(2000, device=dev)
+    with pytest.raises(TypeError):
+        spmv_recon(R.offsets, R.values, 1000, 1000, x2[::2])
+    Rc = R.values.to(torch.complex64)
+    psi = torch.randn(2000, device=dev, dtype=torch.complex64)
+    with pytest.raises(TypeError):
+        expm_krylov(R.offsets, Rc, 1000, psi[::2], 0.1, m=8)
+    psi0 = psi[:1000].contiguous()
+    with pytest.raises(TypeError):
+        expm_krylov(R.offsets, Rc, 1000, psi0, 0.1, m=8, out=psi[::2])
+    with pytest.raises(ValueError):
+        expm_krylov(R.offsets, Rc, 1000, psi0, 0.1, m=8, out=psi0)
