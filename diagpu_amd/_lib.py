@@ -94,6 +94,14 @@ PROTOTYPES: dict[str, tuple] = {
         _vp,
         _vp, _sz,
         C.POINTER(SpgemmInfo), _vp]),
+    "diagpu_spgemm_symbolic_noalloc": (C.c_int, [
+        _i32,
+        _vp, _vp, _vp, _i32,
+        _vp, _vp, _vp, _i32,
+        _vp, _vp, _vp, _i64,
+        _vp, _vp, _i64,
+        _vp,
+        C.POINTER(SpgemmInfo), _vp]),
     "diagpu_spgemm_numeric_f32": (C.c_int, [
         _i32, _vp, _vp,
         _vp, _vp, _vp, _i64,
@@ -126,8 +134,9 @@ PROTOTYPES: dict[str, tuple] = {
                                                   _i64, _vp, _vp, _i64, _vp, _vp]),
 }
 
-# diagpu.h: DIAGPU_ASTAT_MAX_A
+# diagpu.h: DIAGPU_ASTAT_MAX_A, DIAGPU_SYMBOLIC_SCRATCH_BYTES
 ASTAT_MAX_A = 71
+SYMBOLIC_SCRATCH_BYTES = 40 << 20
 
 _lib: C.CDLL | None = None
 

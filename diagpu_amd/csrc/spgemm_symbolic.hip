@@ -31,6 +31,7 @@
 //  11 fill        one lane per C diagonal: the GPairs in B order
 // then one 64-byte device-to-host copy of the counts and a stream sync.
 #include <climits>
+#include <mutex>
 
 #include "common.hpp"
 #include "scan.hpp"
@@ -374,36 +375,49 @@ int grid_for(int64_t work, int64_t cap = 65536)
     return (int)g;
 }
 
-}  // namespace
-}  // namespace diagpu
+// Scratch of diagpu_spgemm_symbolic_noalloc: the workspace of the symbolic
+// phase held in a file-scope device array, for callers that cannot allocate.
+// Each device that runs the library holds its own copy until the process ends.
+// Host code never uses the name `scratch` as an address (on the host it names
+// a stand-in, not device memory); it uses the per-device address from
+// hipGetSymbolAddress that scratch_ptr() keeps.
+constexpr size_t kScratchBytes = DIAGPU_SYMBOLIC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
-extern "C" {
-
-DIAGPU_API int diagpu_spgemm_symbolic_workspace(int32_t n, int32_t a_ndiag, int32_t b_ndiag,
-                                                size_t* bytes)
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+int scratch_ptr(const char* fn, void** out)
 {
-    using namespace diagpu;
-    if (!bytes) return fail(DIAGPU_ERR_ARG, "diagpu_spgemm_symbolic_workspace: bytes is NULL");
-    if (n < 1 || n > (1 << 30) || a_ndiag < 0 || b_ndiag < 0)
-        return fail(DIAGPU_ERR_ARG,
-                    "diagpu_spgemm_symbolic_workspace: need 1 <= n <= 2^30 and counts >= 0 "
-                    "(n=%d a=%d b=%d)", n, a_ndiag, b_ndiag);
-    *bytes = layout_for(n, a_ndiag, b_ndiag).total;
+    static std::mutex mu;
+    static void* addr[64] = {};
+    int dev = 0;
+    int rc = check_hip(hipGetDevice(&dev), fn);
+    if (rc) return rc;
+    if (dev < 0 || dev >= 64) return fail(DIAGPU_ERR_ARG, "%s: device %d out of range", fn, dev);
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), fn);
+        if (rc) return rc;
+        if (!p) return fail(DIAGPU_ERR_HIP, "%s: no device address for the scratch array", fn);
+        addr[dev] = p;
+    }
+    *out = addr[dev];
     return DIAGPU_OK;
 }
 
-DIAGPU_API int diagpu_spgemm_symbolic(
-    int32_t n,
+// The two entry points below share this runner.  workspace == nullptr asks
+// for the file-scope scratch array (diagpu_spgemm_symbolic_noalloc).
+int run_symbolic(
+    const char* fn, int32_t n,
     const int32_t* A_off, const int32_t* A_len, const int64_t* A_starts, int32_t a_ndiag,
     const int32_t* B_off, const int32_t* B_len, const int64_t* B_starts, int32_t b_ndiag,
     int32_t* C_off, int32_t* C_len, int64_t* C_starts, int64_t c_capacity,
     int64_t* pair_ptr, diagpu_gpair* pairs, int64_t pair_capacity,
-    int32_t* c_lookup,
+    int32_t* c_lookup, bool use_scratch,
     void* workspace, size_t workspace_bytes,
     diagpu_spgemm_info* info, void* stream)
 {
-    using namespace diagpu;
-    const char* fn = "diagpu_spgemm_symbolic";
     if (!info) return fail(DIAGPU_ERR_ARG, "%s: info is NULL", fn);
     if (n < 1 || n > (1 << 30))
         return fail(DIAGPU_ERR_ARG, "%s: n=%d outside [1, 2^30]", fn, n);
@@ -418,6 +432,16 @@ DIAGPU_API int diagpu_spgemm_symbolic(
         return fail(DIAGPU_ERR_ARG, "%s: C arrays are NULL", fn);
     if (pair_capacity > 0 && !pairs) return fail(DIAGPU_ERR_ARG, "%s: pairs is NULL", fn);
     const Layout L = layout_for(n, a_ndiag, b_ndiag);
+    if (use_scratch) {
+        if (L.total > kScratchBytes)
+            return fail(DIAGPU_ERR_CAPACITY,
+                        "%s: n=%d with %d x %d diagonals needs %zu bytes of scratch, more than "
+                        "the %zu the library holds (use diagpu_spgemm_symbolic with a workspace)",
+                        fn, n, a_ndiag, b_ndiag, L.total, kScratchBytes);
+        const int rc = scratch_ptr(fn, &workspace);
+        if (rc) return rc;
+        workspace_bytes = kScratchBytes;
+    }
     if (!workspace) return fail(DIAGPU_ERR_ARG, "%s: workspace is NULL", fn);
     if (workspace_bytes < L.total)
         return fail(DIAGPU_ERR_CAPACITY, "%s: workspace has %zu bytes, needs %zu", fn,
@@ -483,6 +507,54 @@ DIAGPU_API int diagpu_spgemm_symbolic(
         return fail(DIAGPU_ERR_CAPACITY, "%s: %lld pairs exceed pair_capacity=%lld", fn,
                     (long long)h.n_pairs, (long long)pair_capacity);
     return DIAGPU_OK;
+}
+
+}  // namespace
+}  // namespace diagpu
+
+extern "C" {
+
+DIAGPU_API int diagpu_spgemm_symbolic_workspace(int32_t n, int32_t a_ndiag, int32_t b_ndiag,
+                                                size_t* bytes)
+{
+    using namespace diagpu;
+    if (!bytes) return fail(DIAGPU_ERR_ARG, "diagpu_spgemm_symbolic_workspace: bytes is NULL");
+    if (n < 1 || n > (1 << 30) || a_ndiag < 0 || b_ndiag < 0)
+        return fail(DIAGPU_ERR_ARG,
+                    "diagpu_spgemm_symbolic_workspace: need 1 <= n <= 2^30 and counts >= 0 "
+                    "(n=%d a=%d b=%d)", n, a_ndiag, b_ndiag);
+    *bytes = layout_for(n, a_ndiag, b_ndiag).total;
+    return DIAGPU_OK;
+}
+
+DIAGPU_API int diagpu_spgemm_symbolic(
+    int32_t n,
+    const int32_t* A_off, const int32_t* A_len, const int64_t* A_starts, int32_t a_ndiag,
+    const int32_t* B_off, const int32_t* B_len, const int64_t* B_starts, int32_t b_ndiag,
+    int32_t* C_off, int32_t* C_len, int64_t* C_starts, int64_t c_capacity,
+    int64_t* pair_ptr, diagpu_gpair* pairs, int64_t pair_capacity,
+    int32_t* c_lookup,
+    void* workspace, size_t workspace_bytes,
+    diagpu_spgemm_info* info, void* stream)
+{
+    return diagpu::run_symbolic("diagpu_spgemm_symbolic", n, A_off, A_len, A_starts, a_ndiag,
+                                B_off, B_len, B_starts, b_ndiag, C_off, C_len, C_starts,
+                                c_capacity, pair_ptr, pairs, pair_capacity, c_lookup, false,
+                                workspace, workspace_bytes, info, stream);
+}
+
+DIAGPU_API int diagpu_spgemm_symbolic_noalloc(
+    int32_t n,
+    const int32_t* A_off, const int32_t* A_len, const int64_t* A_starts, int32_t a_ndiag,
+    const int32_t* B_off, const int32_t* B_len, const int64_t* B_starts, int32_t b_ndiag,
+    int32_t* C_off, int32_t* C_len, int64_t* C_starts, int64_t c_capacity,
+    int64_t* pair_ptr, diagpu_gpair* pairs, int64_t pair_capacity,
+    int32_t* c_lookup, diagpu_spgemm_info* info, void* stream)
+{
+    return diagpu::run_symbolic("diagpu_spgemm_symbolic_noalloc", n, A_off, A_len, A_starts,
+                                a_ndiag, B_off, B_len, B_starts, b_ndiag, C_off, C_len, C_starts,
+                                c_capacity, pair_ptr, pairs, pair_capacity, c_lookup, true,
+                                nullptr, 0, info, stream);
 }
 
 }  // extern "C"

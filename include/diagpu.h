@@ -217,6 +217,27 @@ DIAGPU_API int diagpu_spgemm_symbolic(
     void* workspace, size_t workspace_bytes,
     diagpu_spgemm_info* info, void* stream);
 
+/* diagpu_spgemm_symbolic without the workspace argument: for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * The workspace is a file-scope device array of DIAGPU_SYMBOLIC_SCRATCH_BYTES
+ * that each GPU holds until the process ends; a problem whose workspace
+ * (diagpu_spgemm_symbolic_workspace) is larger is rejected with
+ * DIAGPU_ERR_CAPACITY before any GPU work (n up to about 4.7 million fits
+ * for any diagonal counts).  Same arguments, outputs and errors as
+ * diagpu_spgemm_symbolic otherwise; allocates nothing.  Every call on one GPU
+ * shares that GPU's array, so calls that overlap on one GPU (other host
+ * threads, other streams) race; calls in sequence do not, because each call
+ * synchronises its stream before returning and re-initialises what it reads. */
+#define DIAGPU_SYMBOLIC_SCRATCH_BYTES (40u << 20)
+DIAGPU_API int diagpu_spgemm_symbolic_noalloc(
+    int32_t n,
+    const int32_t* A_off, const int32_t* A_len, const int64_t* A_starts, int32_t a_ndiag,
+    const int32_t* B_off, const int32_t* B_len, const int64_t* B_starts, int32_t b_ndiag,
+    int32_t* C_off, int32_t* C_len, int64_t* C_starts, int64_t c_capacity,
+    int64_t* pair_ptr, diagpu_gpair* pairs, int64_t pair_capacity,
+    int32_t* c_lookup, diagpu_spgemm_info* info, void* stream);
+
 /* Numeric phase: C_vals[C_starts[k] + p] = sum over the plan entries of C
  * diagonal k (fp32 products, fp32 accumulation in plan order), for every
  * 0 <= p < C_len[k]; every C value is written exactly once (no atomics, no

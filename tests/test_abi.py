@@ -194,3 +194,23 @@ def test_astat_max_a_matches_header():
     assert m and int(m.group(1)) == _lib.ASTAT_MAX_A
     assert 288 * _lib.ASTAT_MAX_A * 4 <= 80 * 1024 < 288 * (_lib.ASTAT_MAX_A + 1) * 4
 
+
+def test_symbolic_noalloc_rejects_beyond_scratch():
+    """diagpu_spgemm_symbolic_noalloc: a workspace larger than the library's
+    scratch array is DIAGPU_ERR_CAPACITY, reported before any HIP call (the
+    fake pointers are never read)."""
+    lib = _lib.load()
+    n = 1 << 23
+    ws = C.c_size_t(0)
+    assert lib.diagpu_spgemm_symbolic_workspace(n, 3, 3, C.byref(ws)) == _lib.OK
+    assert ws.value > _lib.SYMBOLIC_SCRATCH_BYTES
+    fake = C.c_void_p(0x1000)
+    info = _lib.SpgemmInfo()
+    st = lib.diagpu_spgemm_symbolic_noalloc(n, fake, fake, fake, 3, fake, fake, fake, 3, fake,
+                                            fake, fake, 9, fake, fake, 9, None, C.byref(info),
+                                            None)
+    assert st == _lib.ERR_CAPACITY
+    assert b"scratch" in lib.diagpu_last_error()
+    assert lib.diagpu_spgemm_symbolic_noalloc(n, fake, fake, fake, 3, fake, fake, fake, 3, fake,
+                                              fake, fake, 9, fake, fake, 9, None, None,
+                                              None) == _lib.ERR_ARG
