@@ -36,6 +36,7 @@ def lib() -> C.CDLL:
         _lib.orc_spgemm_pairs_omp_f32.restype = C.c_int
         _lib.orc_max_threads.restype = C.c_int
         _lib.orc_make_banded.restype = C.c_int
+        _lib.orc_hval_band.restype = C.c_int64
     return _lib
 
 
@@ -73,6 +74,21 @@ def hval(r: int, d: int) -> float:
 
 def xval(i: int) -> float:
     return lib().orc_xval(i)
+
+
+def xval_array(N: int) -> np.ndarray:
+    x = np.empty(N, dtype=np.float32)
+    lib().orc_xval_fill(N, _p(x))
+    return x
+
+
+def hval_band(N: int, offsets) -> np.ndarray:
+    """hval(r, d) for every entry of the N x N band, offset by offset (given
+    order), rows ascending."""
+    offs = _i32(offsets)
+    out = np.empty(max(1, sum(N - abs(int(d)) for d in offs if abs(int(d)) < N)), np.float32)
+    cnt = lib().orc_hval_band(N, _p(offs), len(offs), _p(out))
+    return out[:cnt]
 
 
 def hash_band_recon(N: int, offsets) -> tuple[np.ndarray, np.ndarray, np.ndarray]:

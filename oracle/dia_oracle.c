@@ -78,6 +78,24 @@ ORC_API float orc_xval(int i)
     return (float)(h & 0xFFFFu) / 65536.0f * 2.0f - 1.0f;
 }
 
+/* x[i] = orc_xval(i) for i < N. */
+ORC_API void orc_xval_fill(int N, float* x)
+{
+    for (int i = 0; i < N; ++i) x[i] = orc_xval(i);
+}
+
+/* The band entries H[r, r + d] = orc_hval(r, d) that exist in an N x N
+ * matrix, offset by offset in the given order, rows ascending; returns the
+ * count written. */
+ORC_API int64_t orc_hval_band(int N, const int* offsets, int K, float* out)
+{
+    int64_t o = 0;
+    for (int k = 0; k < K; ++k)
+        for (int r = 0; r < N; ++r)
+            if (r + offsets[k] >= 0 && r + offsets[k] < N) out[o++] = orc_hval(r, offsets[k]);
+    return o;
+}
+
 /* Recon array of the SpMV bench directly from offsets (any order) with the
  * hash values: spmv/bench/bench_cusparse.cu:131-144 (offsets sorted
  * descending, Recon[k][c] = hval(c - d_k, d_k) for valid rows).  Fills

@@ -6,6 +6,7 @@ reference programs built from its sources), the reference programs run
 live where oracle/_ref is built, scipy's independent DIA definition, dense
 numpy products, closed forms, and a second traversal of the same algebra.
 """
+import hashlib
 import json
 import subprocess
 from pathlib import Path
@@ -318,3 +319,117 @@ def test_reference_generators(oracle):
     assert np.all(DA[0, :4] == 0) and np.all(DA[2, 43:] == 0)
     nz = DA[DA != 0]
     assert nz.size == 46 + 50 + 43 and nz.min() >= 0.5 and nz.max() < 1.5
+
+
+# ---------------------------------------------------------------------------
+# The reference's input generators: the oracle's restatements against the
+# outputs of the reference's own source text (tests/golden/generators.json,
+# written by tests/golden/make_generator_golden.py from oracle/_ref/
+# ref_generators), and the mt19937 draws against the published algorithm.
+# ---------------------------------------------------------------------------
+
+GEN = json.loads((Path(__file__).resolve().parent / "golden" / "generators.json").read_text())
+
+
+def _sha(a) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def _check_summary(a: np.ndarray, s: dict):
+    a = np.ascontiguousarray(a, np.float32)
+    assert a.size == s["count"]
+    if "bits" in s:
+        assert a.view(np.uint32).tolist() == s["bits"]
+    else:
+        assert a[:64].view(np.uint32).tolist() == s["head_bits"]
+    assert _sha(a) == s["sha256"]
+
+
+def test_xval_hval_match_reference(oracle):
+    """orc_xval / orc_hval (dia_oracle.c) against bench_cusparse.cu:70-82
+    run as written, value for value (N = 1000) and by digest (N = 2^20); the
+    SpMV bench's Recon fill and x (orc_hash_band_recon) use exactly them."""
+    for f in GEN["xval"]:
+        _check_summary(oracle.xval_array(f["N"]), f)
+    for f in GEN["hval"]:
+        _check_summary(oracle.hval_band(f["N"], f["offsets"]), f)
+    N, offs = 4096, GEN["hval"][0]["offsets"]
+    r_off, r_val, x = oracle.hash_band_recon(N, offs)
+    assert np.array_equal(x, oracle.xval_array(N))
+    band = oracle.hval_band(N, list(r_off))
+    o = 0
+    for k, d in enumerate(r_off):
+        c = np.arange(max(d, 0), min(N, N + d))
+        assert np.array_equal(r_val[k * N + c], band[o: o + c.size]), d
+        o += c.size
+
+
+def test_tc_spmv_cases_match_reference(oracle):
+    """orc_tc_spmv_case against run_case's LCG fill (test_tc_spmv.cu:86-98)
+    for the six structural cases of :168-179: every band entry in fill order,
+    the whole dense H by digest, and x."""
+    for f in GEN["lcg"]:
+        N, offs = f["N"], f["offsets"]
+        H, x = oracle.tc_spmv_case(N, offs)
+        band = np.array([H[r, r + d] for r in range(N) for d in offs if 0 <= r + d < N],
+                        np.float32)
+        assert band.view(np.uint32).tolist() == f["band_bits"], N
+        assert _sha(H) == f["H_sha256"], N
+        assert x.view(np.uint32).tolist() == f["x_bits"], N
+
+
+def test_make_banded_matches_reference(oracle):
+    """orc_make_banded against DiaMatrix + make_banded of
+    bench_spmspm.cu:79-106: offsets, int64 starts, lengths and every value,
+    including diagonals skipped for n <= |d| and the bench's own operands
+    make_banded(100000, 16, 1234 / 5678) (:465-466)."""
+    for f in GEN["make_banded"]:
+        offs, starts, lens, vals = oracle.make_banded(f["n"], f["w"], f["seed"])
+        assert offs.tolist() == f["offsets"]
+        assert starts.tolist() == f["starts"]
+        assert lens.tolist() == f["lengths"]
+        _check_summary(vals, f["values"])
+
+
+def test_pack_diag_matrix_matches_reference(oracle):
+    """orc_pack_diag_matrix against pack_diag_matrix of gemm_diag.cu:361-382,
+    including the driver's own operands (n = 4096, -10..10, seeds 42 / 137)."""
+    for f in GEN["pack_diag_matrix"]:
+        DA = oracle.pack_diag_matrix(f["n"], f["offsets"], f["seed"])
+        _check_summary(DA.reshape(-1), f["DA"])
+
+
+def _mt19937_uniform(seed: int, count: int, a: float, b: float) -> np.ndarray:
+    """std::uniform_real_distribution<float>(a, b) over std::mt19937(seed) as
+    libstdc++ computes it, from the published algorithms: the MT19937 engine
+    with init_genrand seeding (numpy's legacy RandomState seeding), one
+    32-bit draw per value for generate_canonical<float, 24>, g / 2^32 in
+    float (1.0 replaced by the float just below it), then g * (b - a) + a in
+    float."""
+    raw = np.random.RandomState(seed).randint(0, 2 ** 32, size=count, dtype=np.uint32)
+    c = raw.astype(np.float32) / np.float32(2.0 ** 32)
+    c = np.where(c >= 1, np.nextafter(np.float32(1), np.float32(0)), c).astype(np.float32)
+    return (c * (np.float32(b) - np.float32(a)) + np.float32(a)).astype(np.float32)
+
+
+def test_mt19937_draws_follow_published_algorithm(oracle):
+    """The fixtures and the oracle's draw loops against MT19937 and
+    libstdc++'s uniform mapping computed independently in numpy: the draw
+    order of make_banded (diagonal by diagonal, positions ascending) and of
+    pack_diag_matrix (row by row, only in-range positions)."""
+    for f in GEN["make_banded"]:
+        want = _mt19937_uniform(f["seed"], f["values"]["count"], -1.0, 1.0)
+        _check_summary(want, f["values"])
+    n, w, seed = 100000, 16, 5678
+    assert np.array_equal(oracle.make_banded(n, w, seed)[3],
+                          _mt19937_uniform(seed, 33 * n - 2 * 136, -1.0, 1.0))
+    for f in GEN["pack_diag_matrix"]:
+        n, offs = f["n"], f["offsets"]
+        lens = [n - abs(d) for d in offs]
+        draws = _mt19937_uniform(f["seed"], sum(lens), 0.5, 1.5)
+        DA = np.zeros((len(offs), n), np.float32)
+        o = 0
+        for i, (d, ln) in enumerate(zip(offs, lens)):
+            DA[i, max(-d, 0): max(-d, 0) + ln] = draws[o: o + ln]
+            o += ln
+        _check_summary(DA.reshape(-1), f["DA"])
