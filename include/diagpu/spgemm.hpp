@@ -20,6 +20,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "schedule.hpp"
 
 // HM (Hossain-Mahmud) diagonal storage (spmspm/paper_hm.cuh:18-37): diagonal d
 // has length n - |d|; element (i, j) sits at position min(i, j).
@@ -162,6 +163,17 @@ inline HMMatrix compute_c_hm_structure(const HMMatrix& A, const HMMatrix& B, int
     C.total_nz = r.info.c_nnz;
     C.values.assign(static_cast<size_t>(C.total_nz), 0.0f);
     return C;
+}
+
+// The bench's schedule types and planner under their reference names
+// (spmspm/spmspm.cu:40-46, spmspm/bench_spmspm.cu:137-243), over HM
+// operands and C (e.g. from compute_c_hm_structure).
+using PairEntry = diagpu::PairEntry;
+using Schedule = diagpu::Schedule;
+
+inline Schedule build_schedule(const HMMatrix& A, const HMMatrix& B, const HMMatrix& C, int n)
+{
+    return diagpu::build_schedule(n, A.diag_offsets, B.diag_offsets, C.diag_offsets);
 }
 
 // build_c_diag_lookup (:121-130): lookup[d + n - 1] = C index, -1 elsewhere.
@@ -357,6 +369,18 @@ public:
     const int64_t* pair_ptr() const { return ptr_.data(); }
     const diagpu_gpair* pairs() const { return pairs_.data(); }
     const int* c_lookup() const { return lookup_.size() ? lookup_.data() : nullptr; }
+
+    // The grouped pair schedule of this plan (build_schedule,
+    // spmspm/bench_spmspm.cu:137-243): the plan is copied to the host after
+    // `stream` finishes and each C diagonal's entries re-ordered into A order
+    // (schedule_from_plan).  Groups of t_diags C diagonals, n_tile-wide blocks.
+    Schedule schedule(int t_diags = 8, int n_tile = 256, hipStream_t stream = 0) const
+    {
+        check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+        return schedule_from_plan(n_, A_starts_.download(), B_starts_.download(), info_.c_ndiag,
+                                  ptr_.download(size_t(info_.c_ndiag + 1)),
+                                  pairs_.download(size_t(info_.n_pairs)), t_diags, n_tile);
+    }
 
 private:
     template <typename T>

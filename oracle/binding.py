@@ -353,3 +353,39 @@ def gemm_diag_f64(n, DA, off_A, DB, off_B, C_lookup, C_starts, nnz):
     lib().orc_gemm_diag_f64(n, _p(DA), _p(oa), len(oa), _p(DB), _p(ob), len(ob), _p(lk),
                             _p(st), _p(out), _p(ab))
     return out[:nnz], ab[:nnz]
+
+
+SCHED_ENTRY_DTYPE = np.dtype([("a_local", "<i4"), ("b_local", "<i4"), ("c_local", "<i4"),
+                              ("a_shift", "<i4"), ("b_shift", "<i4")])
+
+
+def build_schedule(n: int, A_off, B_off, C_off, T: int = 8, n_tile: int = 256) -> dict:
+    """build_schedule of spmspm/bench_spmspm.cu:137-243 (orc_build_schedule):
+    a dict with the Schedule's members (pairs as SCHED_ENTRY_DTYPE)."""
+    a, b, c = _i32(A_off), _i32(B_off), _i32(C_off)
+    sc = np.zeros(8, np.int32)
+    lib().orc_build_schedule(n, _p(a), len(a), _p(b), len(b), _p(c), len(c), T, n_tile, _p(sc),
+                             *([None] * 10))
+    a_halo, b_halo, G, max_a, max_b, max_p, ntiles, nblocks = (int(v) for v in sc)
+    out = {k: np.zeros(G, np.int32) for k in ("a_count", "b_count", "pair_count", "t_out")}
+    out["a_globals"] = np.zeros(max(1, G * max_a), np.int32)
+    out["b_globals"] = np.zeros(max(1, G * max_b), np.int32)
+    out["c_globals"] = np.zeros(max(1, G * T), np.int32)
+    out["pairs"] = np.zeros(max(1, G * max_p), SCHED_ENTRY_DTYPE)
+    out["block_group"] = np.zeros(max(1, nblocks), np.int32)
+    out["block_tile"] = np.zeros(max(1, nblocks), np.int32)
+    lib().orc_build_schedule(n, _p(a), len(a), _p(b), len(b), _p(c), len(c), T, n_tile, _p(sc),
+                             _p(out["a_count"]), _p(out["b_count"]), _p(out["pair_count"]),
+                             _p(out["t_out"]), _p(out["a_globals"]), _p(out["b_globals"]),
+                             _p(out["c_globals"]), _p(out["pairs"]), _p(out["block_group"]),
+                             _p(out["block_tile"]))
+    out["a_globals"] = out["a_globals"][: G * max_a]
+    out["b_globals"] = out["b_globals"][: G * max_b]
+    out["c_globals"] = out["c_globals"][: G * T]
+    out["pairs"] = out["pairs"][: G * max_p]
+    out["block_group"] = out["block_group"][:nblocks]
+    out["block_tile"] = out["block_tile"][:nblocks]
+    out.update(a_halo=a_halo, b_halo=b_halo, num_groups=G, max_a=max_a, max_b=max_b,
+               max_pairs=max_p, num_ntiles=ntiles, num_blocks=nblocks)
+    return out
+

@@ -428,6 +428,100 @@ ORC_API void orc_c_lookup(int n, const int* C_off, int nC, int* lookup)
     for (int k = 0; k < nC; ++k) lookup[C_off[k] + (n - 1)] = k;
 }
 
+/* PairEntry of spmspm/spmspm.cu:40-46. */
+typedef struct { int32_t a_local, b_local, c_local, a_shift, b_shift; } orc_pair_entry;
+
+/* build_schedule (spmspm/bench_spmspm.cu:137-243): the C diagonals in groups
+ * of T consecutive ones; per group, for each of its C diagonals dc in order
+ * and each A diagonal ai in A's order with db = dc - da an offset of B (the
+ * last B index holding it), one PairEntry{a_local, b_local, c_local,
+ * min0(da) - min0(dc), da + min0(db) - min0(dc)}, where a_local / b_local
+ * number the group's A / B diagonals in order of first use; halos are the
+ * largest |a_shift| / |b_shift| over all groups.  Per-group lists are padded
+ * to the largest group (a/b/c globals and pairs group-strided, zeros in the
+ * padding), then one block per (group, n-tile): block_group = g, block_tile =
+ * t * n_tile.
+ * scalars[8] = {a_halo, b_halo, num_groups, max_a, max_b, max_pairs,
+ * num_ntiles, num_blocks}.  With a_count == NULL only the scalars are
+ * computed (to size the arrays); otherwise every array is written. */
+ORC_API void orc_build_schedule(int n, const int* A_off, int nA, const int* B_off, int nB,
+                                const int* C_off, int nC, int T, int n_tile, int* scalars,
+                                int* a_count, int* b_count, int* pair_count, int* t_out,
+                                int* a_globals, int* b_globals, int* c_globals,
+                                orc_pair_entry* pairs, int* block_group, int* block_tile)
+{
+    const int64_t nlk = 2 * (int64_t)n - 1;
+    int* blk = (int*)malloc(sizeof(int) * (size_t)nlk);
+    int* aloc = (int*)malloc(sizeof(int) * (size_t)(nA > 0 ? nA : 1));
+    int* bloc = (int*)malloc(sizeof(int) * (size_t)(nB > 0 ? nB : 1));
+    for (int64_t i = 0; i < nlk; ++i) blk[i] = -1;
+    for (int b = 0; b < nB; ++b)
+        if (B_off[b] > -n && B_off[b] < n) blk[B_off[b] + (n - 1)] = b;
+    const int groups = (nC + T - 1) / T;
+    int a_halo = 0, b_halo = 0, max_a = 0, max_b = 0, max_p = 0;
+    /* two sweeps over the groups: sizes, then (with arrays) the contents */
+    for (int pass = 0; pass < (a_count ? 2 : 1); ++pass) {
+        for (int g = 0; g < groups; ++g) {
+            for (int i = 0; i < nA; ++i) aloc[i] = -1;
+            for (int i = 0; i < nB; ++i) bloc[i] = -1;
+            int na = 0, nb = 0, np = 0;
+            const int c0 = g * T, c1 = c0 + T < nC ? c0 + T : nC;
+            for (int cl = 0; cl < c1 - c0; ++cl) {
+                const int dc = C_off[c0 + cl];
+                if (pass) c_globals[(size_t)g * T + cl] = c0 + cl;
+                for (int ai = 0; ai < nA; ++ai) {
+                    const int64_t db = (int64_t)dc - A_off[ai];
+                    if (db <= -(int64_t)n || db >= n) continue;
+                    const int bi = blk[db + (n - 1)];
+                    if (bi < 0) continue;
+                    if (aloc[ai] < 0) {
+                        if (pass) a_globals[(size_t)g * max_a + na] = ai;
+                        aloc[ai] = na++;
+                    }
+                    if (bloc[bi] < 0) {
+                        if (pass) b_globals[(size_t)g * max_b + nb] = bi;
+                        bloc[bi] = nb++;
+                    }
+                    const int da = A_off[ai];
+                    const int ash = imin0(da) - imin0(dc);
+                    const int bsh = da + imin0((int)db) - imin0(dc);
+                    if (pass) {
+                        orc_pair_entry e = {aloc[ai], bloc[bi], cl, ash, bsh};
+                        pairs[(size_t)g * max_p + np] = e;
+                    } else {
+                        if (iabs_(ash) > a_halo) a_halo = iabs_(ash);
+                        if (iabs_(bsh) > b_halo) b_halo = iabs_(bsh);
+                    }
+                    ++np;
+                }
+            }
+            if (pass) {
+                a_count[g] = na; b_count[g] = nb; pair_count[g] = np; t_out[g] = c1 - c0;
+            } else {
+                if (na > max_a) max_a = na;
+                if (nb > max_b) max_b = nb;
+                if (np > max_p) max_p = np;
+            }
+        }
+        if (!pass && a_count) {     /* zero the padding before the fill sweep */
+            memset(a_globals, 0, sizeof(int) * (size_t)groups * max_a);
+            memset(b_globals, 0, sizeof(int) * (size_t)groups * max_b);
+            memset(c_globals, 0, sizeof(int) * (size_t)groups * T);
+            memset(pairs, 0, sizeof(orc_pair_entry) * (size_t)groups * max_p);
+        }
+    }
+    const int ntiles = (n + n_tile - 1) / n_tile;
+    if (a_count)
+        for (int g = 0; g < groups; ++g)
+            for (int t = 0; t < ntiles; ++t) {
+                block_group[(size_t)g * ntiles + t] = g;
+                block_tile[(size_t)g * ntiles + t] = t * n_tile;
+            }
+    scalars[0] = a_halo; scalars[1] = b_halo; scalars[2] = groups; scalars[3] = max_a;
+    scalars[4] = max_b; scalars[5] = max_p; scalars[6] = ntiles; scalars[7] = groups * ntiles;
+    free(blk); free(aloc); free(bloc);
+}
+
 /* build_pairs_only (spmspm/gather_flat.cuh:231-255): for each C diagonal k in
  * order and each B diagonal bi in B's order, da = dc - db; skip |da| >= n or
  * an A offset that is absent (Alookup, built as the bench builds its offset

@@ -452,6 +452,59 @@ static void test_gemm_diag(const char* name, int n, std::vector<int> oa, std::ve
     report((std::string(name) + " GemmDiag values").c_str(), ok);
 }
 
+// The grouped pair schedule from a GPU-built plan (SpgemmPlan::schedule)
+// equals build_schedule over the operands' offsets (schedule.hpp, checked
+// against the oracle's restatement of spmspm/bench_spmspm.cu:137-243 on the
+// CPU), member for member: the bench's make_banded(100000, 16) operands and
+// BASELINE config 4's offsets.
+static void test_schedule()
+{
+    auto same = [](const Schedule& x, const Schedule& y) {
+        return x.a_halo == y.a_halo && x.b_halo == y.b_halo && x.num_groups == y.num_groups &&
+               x.max_a == y.max_a && x.max_b == y.max_b && x.max_pairs == y.max_pairs &&
+               x.num_blocks == y.num_blocks && x.a_count == y.a_count && x.b_count == y.b_count &&
+               x.pair_count == y.pair_count && x.t_out == y.t_out && x.a_globals == y.a_globals &&
+               x.b_globals == y.b_globals && x.c_globals == y.c_globals &&
+               x.pairs.size() == y.pairs.size() &&
+               std::memcmp(x.pairs.data(), y.pairs.data(), x.pairs.size() * sizeof(PairEntry)) == 0 &&
+               x.block_group == y.block_group && x.block_tile == y.block_tile;
+    };
+    {
+        const HMMatrix A = diagpu::make_banded(100000, 16, 1234u);
+        const HMMatrix B = diagpu::make_banded(100000, 16, 5678u);
+        const HMMatrix C = compute_c_hm_structure(A, B, 100000);
+        const Schedule want = build_schedule(A, B, C, 100000);
+        diagpu::DeviceArray<int> ao(A.diag_offsets), al(A.diag_lengths), bo(B.diag_offsets),
+            bl(B.diag_lengths);
+        diagpu::DeviceArray<int64_t> as(A.diag_starts), bs(B.diag_starts);
+        diagpu::SpgemmPlan plan(100000, ao.data(), al.data(), as.data(), A.num_diags, bo.data(),
+                                bl.data(), bs.data(), B.num_diags);
+        char buf[96];
+        std::snprintf(buf, sizeof buf, "groups=%d halos=(%d,%d) blocks=%d", want.num_groups,
+                      want.a_halo, want.b_halo, want.num_blocks);
+        report("schedule: make_banded(100000,16) plan", same(plan.schedule(), want) &&
+               want.num_groups == 9 && want.max_pairs == 236, buf);
+    }
+    {
+        const int n = 1 << 20;
+        const std::vector<int> ao_h = {-4, -3, -2, -1, 0, 1, 2, 3, 4};
+        const std::vector<int> bo_h = {-16384, -128, -1, 0, 1, 128, 16384};
+        std::vector<int> al_h, bl_h;
+        for (int d : ao_h) al_h.push_back(n - std::abs(d));
+        for (int d : bo_h) bl_h.push_back(n - std::abs(d));
+        diagpu::DeviceArray<int> ao(ao_h), al(al_h), bo(bo_h), bl(bl_h);
+        diagpu::DeviceArray<int64_t> as(diagpu::hm_starts(n, ao_h)), bs(diagpu::hm_starts(n, bo_h));
+        diagpu::SpgemmPlan plan(n, ao.data(), al.data(), as.data(), 9, bo.data(), bl.data(),
+                                bs.data(), 7);
+        std::vector<int> c_off(plan.info().c_ndiag);
+        diagpu::check_hip(hipMemcpy(c_off.data(), plan.c_offsets(), c_off.size() * sizeof(int),
+                                    hipMemcpyDeviceToHost), "copy");
+        const Schedule want = diagpu::build_schedule(n, ao_h, bo_h, c_off);
+        report("schedule: config 4 plan (a_halo 16384)",
+               same(plan.schedule(), want) && want.a_halo == 16384 && want.num_groups == 6);
+    }
+}
+
 int main()
 {
     // Unbuffered, so every line is out before anything that follows it.
@@ -475,6 +528,7 @@ int main()
         test_astat_kernel();
         test_pack_diag_matrix();
         test_generators();
+        test_schedule();
     } catch (const std::exception& e) {
         std::printf("  exception: %s\n", e.what());
         g_all = false;

@@ -433,3 +433,44 @@ def test_mt19937_draws_follow_published_algorithm(oracle):
             DA[i, max(-d, 0): max(-d, 0) + ln] = draws[o: o + ln]
             o += ln
         _check_summary(DA.reshape(-1), f["DA"])
+
+
+# ---------------------------------------------------------------------------
+# The grouped pair schedule (build_schedule, spmspm/bench_spmspm.cu:137-243):
+# orc_build_schedule and orc_c_structure against the reference planner run
+# from its own source text (tests/golden/schedule.json, written by
+# tests/golden/make_schedule_golden.py from oracle/_ref/ref_schedule).
+# ---------------------------------------------------------------------------
+
+SCHED = json.loads((Path(__file__).resolve().parent / "golden" / "schedule.json").read_text())
+SCHED_ARRAYS = ("a_count", "b_count", "pair_count", "t_out", "a_globals", "b_globals",
+                "c_globals", "block_group", "block_tile")
+
+
+def _check_int_array(a, f, name):
+    a = np.ascontiguousarray(a, np.int32)
+    assert a.size == f["count"], name
+    if "values" in f:
+        assert a.tolist() == f["values"], name
+    assert _sha(a) == f["sha256"], name
+
+
+@pytest.mark.parametrize("idx", range(len(SCHED["cases"])))
+def test_schedule_matches_reference(oracle, idx):
+    case = SCHED["cases"][idx]
+    if "banded" in case:
+        n, w, sa, sb = case["banded"]
+        a_off = oracle.make_banded(n, w, sa)[0]
+        b_off = oracle.make_banded(n, w, sb)[0]
+    else:
+        n, a_off, b_off = case["n"], case["A"], case["B"]
+    c_off = oracle.c_structure(n, a_off, b_off)[0]
+    _check_int_array(c_off, case["c_offsets"], "c_offsets")
+    T, n_tile = case["scalars"][8], case["scalars"][9]
+    S = oracle.build_schedule(n, a_off, b_off, c_off, T, n_tile)
+    assert [S[k] for k in ("a_halo", "b_halo", "num_groups", "max_a", "max_b", "max_pairs",
+                           "num_ntiles", "num_blocks")] == case["scalars"][:8]
+    for k in SCHED_ARRAYS:
+        _check_int_array(S[k], case[k], k)
+    flat = S["pairs"].view(np.int32).reshape(-1)
+    _check_int_array(flat, case["pairs"], "pairs")
