@@ -126,6 +126,26 @@ def time_spmv(cfg: int, dtype, steps: int, warmup: int, seed: int, sets: int, xd
     }
 
 
+def host_cores() -> dict:
+    """Host CPUs this process may run on: logical CPUs in its affinity mask,
+    the physical cores (distinct package and core ids in sysfs) behind them,
+    and the machine's logical CPU count."""
+    try:
+        cpus = sorted(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        cpus = list(range(os.cpu_count() or 1))
+    cores = set()
+    for c in cpus:
+        base = Path(f"/sys/devices/system/cpu/cpu{c}/topology")
+        try:
+            cores.add(((base / "physical_package_id").read_text().strip(),
+                       (base / "core_id").read_text().strip()))
+        except OSError:
+            cores.add(("?", str(c)))
+    return {"logical_cpus": len(cpus), "physical_cores": len(cores),
+            "machine_logical_cpus": os.cpu_count()}
+
+
 def cpu_spmv_baseline(R, seconds: float):
     """The oracle's OpenMP DIA loop over full SpMVs of the same matrix on the
     host cores, repeated until `seconds` elapse (1 warm-up run first)."""
@@ -255,9 +275,54 @@ def cpu_spgemm_baseline(plan, A, B, seconds: float):
     # bytes: the sample's C values once plus the A and B values its pairs read
     byt = 4 * (2 * float(ov[: ptr[k]].sum()) + out.size)
     return {"value": round(flops / sec / 1e9, 2), "unit": "GFLOP/s", "GBs": round(byt / sec / 1e9, 2),
-            "cores": threads, "kind": "port",
+            "cores": threads, **host_cores(), "kind": "port",
             "sample": f"C diagonals 0..{k - 1} of {nC} ({100.0 * flops / max(1.0, float(fl_k.sum())):.1f}% "
                       f"of the flops), {reps} runs of {sec * 1e3:.1f} ms, oracle OpenMP loop"}
+
+
+def compare_kernels(plan, sets, reps: int, alg: int, flops: int) -> dict:
+    """Every numeric kernel that takes this fp32 plan, forced, on the same
+    rotated operand sets (the side-by-side run of spmspm/bench_spmspm.cu:
+    518-653): time per product, GFLOP/s, fraction of HBM peak, and whether C
+    is bit for bit the gather's (checked where one more C fits in 4 GB)."""
+    import torch
+    from diagpu_amd import _lib
+    names = ["gather"]
+    if plan.band_info()[1].eligible:
+        names.append("band")
+    if plan.A.offsets.numel() <= _lib.ASTAT_MAX_A:
+        try:
+            plan.astat_records()
+            names.append("astat")
+        except _lib.DiagpuError:
+            pass
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    nsets = len(sets)
+    ref = None
+    check = plan.info.c_nnz * 4 <= (4 << 30)
+    out = {}
+    for k in names:
+        for i in range(2):
+            plan.numeric(*sets[i % nsets], kernel=k)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for i in range(reps):
+            plan.numeric(*sets[i % nsets], kernel=k)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        kms = e0.elapsed_time(e1) / reps
+        rec = {"numeric_ms": round(kms, 5), "GFLOPs": round(flops / (kms * 1e6), 1),
+               "frac_hbm": round(alg / (kms * 1e6) / HBM_PEAK_GBS, 4), "same_bits_as_gather": None}
+        if check:
+            plan.numeric(*sets[0], kernel=k)
+            torch.cuda.synchronize()
+            c = sets[0][2][: plan.info.c_nnz].view(torch.int32)
+            if ref is None:
+                ref = c.clone()
+            rec["same_bits_as_gather"] = bool(torch.equal(ref, c))
+        out[k] = rec
+    return out
 
 
 def time_spgemm(cfg: int, seed: int, reps: int, complex_values: bool = False,
@@ -302,6 +367,7 @@ def time_spgemm(cfg: int, seed: int, reps: int, complex_values: bool = False,
     ms = e0.elapsed_time(e1) / reps
     alg = esz * (A.nnz + B.nnz + plan.info.c_nnz)
     flops = plan.info.useful_flops * (4 if complex_values else 1)   # complex MAC = 4 real
+    kernels = {} if complex_values else compare_kernels(plan, sets, max(3, reps // 2), alg, flops)
     return {
         "workload": f"spgemm_cfg{cfg}" if cfg >= 4 else f"spgemm_HxH_cfg{cfg}",
         "dtype": "c64" if complex_values else "f32", "n": A.n,
@@ -314,6 +380,7 @@ def time_spgemm(cfg: int, seed: int, reps: int, complex_values: bool = False,
         "GBs": round(alg / (ms * 1e6), 1), "frac_hbm": round(alg / (ms * 1e6) / HBM_PEAK_GBS, 4),
         "alg_bytes": alg, "buffer_sets": nsets,
         "total_ms": round(ms + sym_ms, 5),
+        "kernels": kernels,
         "cpu_baseline": (cpu_spgemm_baseline(plan, A, B, cpu_seconds)
                          if cpu_seconds > 0 and not complex_values else None),
     }
@@ -543,7 +610,7 @@ def main(argv=None) -> int:
         log(f"CPU baseline ({args.cpu_seconds:.0f} s budget)")
         c = cpu_spmv_baseline(R, args.cpu_seconds)
         cpu = {"value": round(c["gbs"], 2), "unit": "GB/s", "cores": c["threads"],
-               "kind": "port",
+               **host_cores(), "kind": "port",
                "sample": f"{c['reps']} full SpMVs of the config-2 matrix (n=4194304, fp32) "
                          f"with the oracle's OpenMP DIA loop, {c['ms']:.2f} ms each, "
                          f"{os.cpu_count()} logical CPUs visible"}

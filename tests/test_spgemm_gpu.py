@@ -125,34 +125,61 @@ def test_config4_full_size(dev, oracle):
     check_values(Cv, want, ab)
 
 
-def _row_sums_gpu(plan, Cv, n):
-    """C 1 on the device in fp64: each C diagonal adds into its rows."""
-    rs = torch.zeros(n, dtype=torch.float64, device=Cv.device)
+def _c_matvec_gpu(plan, Cv, v, transpose=False):
+    """C v (or v^T C) on the device in fp64, diagonal by diagonal."""
+    n = plan.n
+    vd = torch.as_tensor(v, dtype=torch.float64, device=Cv.device)
+    y = torch.zeros(n, dtype=torch.float64, device=Cv.device)
     offs = plan.c_offsets().cpu().tolist()
     lens = plan.c_lengths().cpu().tolist()
     sts = plan.c_starts().cpu().tolist()
     for d, ln, s in zip(offs, lens, sts):
-        r0 = -d if d < 0 else 0
-        rs[r0:r0 + ln] += Cv[s:s + ln].double()
-    return rs.cpu().numpy()
+        r0, c0 = (0, d) if d >= 0 else (-d, 0)
+        if transpose:
+            r0, c0 = c0, r0
+        y[r0:r0 + ln] += Cv[s:s + ln].double() * vd[c0:c0 + ln]
+    return y.cpu().numpy()
 
 
-def _hm_matvec(n, M, v):
-    """(M v) and (|M| |v|) in fp64 for an HM matrix on the host."""
+def _hm_matvec(n, M, v, transpose=False):
+    """(M v) and (|M| |v|) in fp64 for an HM matrix on the host (M^T with
+    transpose)."""
     off, ln, st, val = M
     y = np.zeros(n)
     ya = np.zeros(n)
     for d, l, s in zip(off, ln, st):
         r0, c0 = (0, d) if d >= 0 else (-d, 0)
+        if transpose:
+            r0, c0 = c0, r0
         seg = val[s:s + l].astype(np.float64)
         y[r0:r0 + l] += seg * v[c0:c0 + l]
         ya[r0:r0 + l] += np.abs(seg) * np.abs(v[c0:c0 + l])
     return y, ya
 
 
+def _check_products(plan, Cv, A, B, seed):
+    """All of C through C v = A (B v) and v^T C = (v^T A) B for a random v:
+    a value written to a wrong position or diagonal changes both (a row sum
+    alone misses a value moved between two C diagonals of one row).  Bound:
+    1e-5 |A| |B| |v| (each C element is within 1e-5 of its term sum)."""
+    n = A.n
+    v = np.random.default_rng(seed).standard_normal(n)
+    got = _c_matvec_gpu(plan, Cv, v)
+    bv, bva = _hm_matvec(n, host(B), v)
+    want, _ = _hm_matvec(n, host(A), bv)
+    _, bound = _hm_matvec(n, host(A), bva)
+    assert np.all(np.abs(got - want) <= TOL * bound + 1e-300), "C v"
+    got = _c_matvec_gpu(plan, Cv, v, transpose=True)
+    av, ava = _hm_matvec(n, host(A), v, transpose=True)
+    want, _ = _hm_matvec(n, host(B), av, transpose=True)
+    _, bound = _hm_matvec(n, host(B), ava, transpose=True)
+    assert np.all(np.abs(got - want) <= TOL * bound + 1e-300), "v^T C"
+
+
 def test_config5_full_size(dev, oracle):
     """n = 262144, 128 x 128 random offsets: plan exact; values exact to the
-    bound on a sample of C diagonals; all of C through C 1 = A (B 1)."""
+    bound on a sample of C diagonals; all of C through C v = A (B v) and
+    v^T C = (v^T A) B."""
     A, B = workloads.spgemm_config(5, seed=5, device=dev)
     plan = SpgemmPlan(A, B)
     c_off, c_len, c_st, nnz, ptr, pairs = check_plan(oracle, plan, A, B)
@@ -167,12 +194,7 @@ def test_config5_full_size(dev, oracle):
         want, ab = oracle.spgemm_pairs_f64(Av, Bv, c_len, c_st, ptr, pairs, k, k + 1)
         got = Cv[int(c_st[k]):int(c_st[k]) + int(c_len[k])].cpu().numpy()
         check_values(got, want, ab)
-    n = A.n
-    rs = _row_sums_gpu(plan, Cv, n)
-    b1, b1a = _hm_matvec(n, host(B), np.ones(n))
-    ab1, bound = _hm_matvec(n, host(A), b1)
-    _, bound = _hm_matvec(n, host(A), b1a)
-    assert np.all(np.abs(rs - ab1) <= TOL * bound + 1e-300)
+    _check_products(plan, Cv, A, B, seed=5)
 
 
 @pytest.mark.parametrize("n,offs_a,offs_b", [
@@ -252,7 +274,7 @@ def test_square_of_spmv_configs(dev, oracle, cfg):
     """H H for the SpMV configs' matrices (full size): plan exact; values to
     the bound on every C diagonal (configs 1, 2) or on a sample of them
     (config 3, about 1400 C diagonals of 4.2M values), and all of C through
-    C 1 = H (H 1)."""
+    C v = H (H v) and v^T C = (v^T H) H."""
     A, B = workloads.spgemm_config(cfg, seed=cfg, device=dev)
     plan = SpgemmPlan(A, B)
     c_off, c_len, c_st, nnz, ptr, pairs = check_plan(oracle, plan, A, B)
@@ -270,12 +292,7 @@ def test_square_of_spmv_configs(dev, oracle, cfg):
         want, ab = oracle.spgemm_pairs_f64(Av, Bv, c_len, c_st, ptr, pairs, k, k + 1)
         got = Cv[int(c_st[k]):int(c_st[k]) + int(c_len[k])].cpu().numpy()
         check_values(got, want, ab)
-    n = A.n
-    rs = _row_sums_gpu(plan, Cv, n)
-    b1, b1a = _hm_matvec(n, host(B), np.ones(n))
-    ab1, _ = _hm_matvec(n, host(A), b1)
-    _, bound = _hm_matvec(n, host(A), b1a)
-    assert np.all(np.abs(rs - ab1) <= TOL * bound + 1e-300)
+    _check_products(plan, Cv, A, B, seed=cfg)
 
 
 @pytest.mark.parametrize("n,offs_a,offs_b", [
