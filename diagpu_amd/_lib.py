@@ -65,7 +65,8 @@ class BandInfo(C.Structure):
 
 class SpgemmInfo(C.Structure):
     _fields_ = [("c_ndiag", C.c_int64), ("c_nnz", C.c_int64), ("n_pairs", C.c_int64),
-                ("max_pairs", C.c_int64), ("useful_flops", C.c_int64)]
+                ("max_pairs", C.c_int64), ("useful_flops", C.c_int64), ("a_extent", C.c_int64),
+                ("b_extent", C.c_int64)]
 
 
 _vp, _i32, _i64, _sz = C.c_void_p, C.c_int32, C.c_int64, C.c_size_t

@@ -142,7 +142,8 @@ def multiply(A: HM, B: HM, stats: ChainStats | None = None) -> HM:
     t0 = time.perf_counter()
     plan = SpgemmPlan(A, B)
     inf = plan.info
-    C = HM(A.n, plan.c_offsets().clone(), plan.c_lengths().clone(), plan.c_starts().clone(),
+    # C's structure arrays are views of the plan's buffer (kept alive by them)
+    C = HM(A.n, plan.c_offsets(), plan.c_lengths(), plan.c_starts(),
            torch.empty(max(1, inf.c_nnz), dtype=A.values.dtype, device=A.values.device)[: inf.c_nnz])
     if stats is not None:
         torch.cuda.synchronize()

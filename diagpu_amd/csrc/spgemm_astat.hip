@@ -219,8 +219,7 @@ DIAGPU_API int diagpu_spgemm_astat_prepare(int32_t n, const int64_t* A_starts, i
                            reinterpret_cast<int4*>(records), flag);
         st = check_launch(fn);
     }
-    if (!st) st = check_hip(hipMemcpyAsync(host, flag, sizeof(host), hipMemcpyDeviceToHost, s), fn);
-    if (!st) st = check_hip(hipStreamSynchronize(s), fn);
+    if (!st) st = check_hip(hipMemcpyWithStream(host, flag, sizeof(host), hipMemcpyDeviceToHost, s), fn);
     if (st) return st;
     if (host[0]) return fail(DIAGPU_ERR_ARG, "%s: a plan entry's A start is not an A diagonal's start", fn);
     if (host[1]) return fail(DIAGPU_ERR_CAPACITY, "%s: B indices beyond 2^31 - 1", fn);

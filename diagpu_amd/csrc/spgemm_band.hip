@@ -342,8 +342,7 @@ DIAGPU_API int diagpu_spgemm_band_prepare(int32_t n, const int32_t* A_off,
                            B_starts, nB, reinterpret_cast<int4*>(entries), dev);
         st = check_launch(fn);
     }
-    if (!st) st = check_hip(hipMemcpyAsync(host, dev, sizeof(host), hipMemcpyDeviceToHost, s), fn);
-    if (!st) st = check_hip(hipStreamSynchronize(s), fn);
+    if (!st) st = check_hip(hipMemcpyWithStream(host, dev, sizeof(host), hipMemcpyDeviceToHost, s), fn);
     if (st) return st;
     if (host[2])
         return fail(DIAGPU_ERR_ARG, "%s: a plan entry's starts are no operand diagonals' starts, or "

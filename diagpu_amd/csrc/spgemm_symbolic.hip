@@ -14,7 +14,15 @@
 //               da + min0(db) - min0(dc), A_len[ai], B_len[bi]}.
 //
 // GPU formulation (every step is integer and order-independent, so the
-// result does not depend on scheduling):
+// result does not depend on scheduling).  Two paths:
+//
+// One launch (k_sym_fast, below): for operand products of up to 2^20
+// (a, b) pairs whose offset spans fit in a workgroup's LDS (bitmaps over the
+// spans, not over the 2n - 1 offsets).  A kernel launch costs about 10 us of
+// dispatch here, more than any of the small kernels of the path below, so
+// this path's single launch plus one copy is the whole phase.
+//
+// Multi-launch, for everything else:
 //   1 init        fill the A lookup with -1 and clear the bitmaps
 //   2 operands    validate A/B offsets and lengths, scatter the A lookup,
 //                 detect duplicates (atomicExch / atomicOr old values)
@@ -29,7 +37,7 @@
 //   9 scan top    one workgroup: exclusive scan of the block sums
 //  10 scan final  C_starts and pair_ptr
 //  11 fill        one lane per C diagonal: the GPairs in B order
-// then one 64-byte device-to-host copy of the counts and a stream sync.
+// then one synchronous device-to-host copy of the counts on the stream.
 #include <climits>
 #include <mutex>
 
@@ -41,6 +49,15 @@ namespace {
 
 constexpr int kBlock = 256;
 
+// One-launch path (k_sym_fast): workgroup size, dynamic LDS per workgroup,
+// largest grid, and the largest operand product it takes.
+constexpr int kFastBlock = 512;
+constexpr int kFastWaves = kFastBlock / 64;
+constexpr int kFastLdsBytes = 128 * 1024;
+constexpr int kFastLdsWords = kFastLdsBytes / 4;
+constexpr int kMaxFastGroups = 1024;
+constexpr int64_t kFastMaxProducts = int64_t(1) << 20;
+
 enum : int32_t {
     kFlagAOffset = 1,
     kFlagBOffset = 2,
@@ -48,6 +65,7 @@ enum : int32_t {
     kFlagBDup = 8,
     kFlagCCapacity = 16,
     kFlagPairCapacity = 32,
+    kFlagFallback = 64,   // the one-launch path cannot hold the operands in LDS
 };
 
 struct SymState {
@@ -58,7 +76,8 @@ struct SymState {
     int64_t useful_flops;
     int32_t flags;
     int32_t pad;
-    int64_t reserved[2];
+    int64_t a_extent;     // values A's starts and lengths address: max(start + length)
+    int64_t b_extent;
 };
 static_assert(sizeof(SymState) == 64, "state is one 64-byte record");
 
@@ -90,7 +109,7 @@ Layout layout_for(int32_t n, int32_t na, int32_t nb)
     L.off_wprefix = o; o = align256(o + sizeof(int32_t) * L.nwords);
     L.off_wsum = o;    o = align256(o + sizeof(int64_t) * L.nwblocks);
     L.off_part = o;    o = align256(o + 2 * sizeof(int64_t) * L.nkblocks);
-    L.off_state = o;   o = align256(o + sizeof(SymState));
+    L.off_state = o;   o = align256(o + sizeof(SymState) + sizeof(int32_t) * kMaxFastGroups);
     L.total = o;
     return L;
 }
@@ -120,13 +139,17 @@ __global__ __launch_bounds__(kBlock) void k_init(int32_t* __restrict__ alk, int6
         st->useful_flops = 0;
         st->flags = 0;
         st->pad = 0;
+        st->a_extent = 0;
+        st->b_extent = 0;
     }
 }
 
 __global__ __launch_bounds__(kBlock) void k_operands(int32_t n, const int32_t* __restrict__ A_off,
-                                                     const int32_t* __restrict__ A_len, int32_t na,
+                                                     const int32_t* __restrict__ A_len,
+                                                     const int64_t* __restrict__ A_starts, int32_t na,
                                                      const int32_t* __restrict__ B_off,
-                                                     const int32_t* __restrict__ B_len, int32_t nb,
+                                                     const int32_t* __restrict__ B_len,
+                                                     const int64_t* __restrict__ B_starts, int32_t nb,
                                                      int32_t* __restrict__ alk,
                                                      uint32_t* __restrict__ bbits,
                                                      SymState* __restrict__ st)
@@ -136,8 +159,10 @@ __global__ __launch_bounds__(kBlock) void k_operands(int32_t n, const int32_t* _
         const int d = A_off[t];
         if (d <= -n || d >= n || A_len[t] != n - iabs_(d)) {
             raise_flag(st, kFlagAOffset);
-        } else if (atomicExch(&alk[d + (n - 1)], t) != -1) {
-            raise_flag(st, kFlagADup);
+        } else {
+            if (atomicExch(&alk[d + (n - 1)], t) != -1) raise_flag(st, kFlagADup);
+            atomicMax((unsigned long long*)&st->a_extent,
+                      (unsigned long long)(A_starts[t] + A_len[t]));
         }
     }
     if (t < nb) {
@@ -148,6 +173,8 @@ __global__ __launch_bounds__(kBlock) void k_operands(int32_t n, const int32_t* _
             const int64_t pos = d + (int64_t)(n - 1);
             const uint32_t m = 1u << (pos & 31);
             if (atomicOr(&bbits[pos >> 5], m) & m) raise_flag(st, kFlagBDup);
+            atomicMax((unsigned long long*)&st->b_extent,
+                      (unsigned long long)(B_starts[t] + B_len[t]));
         }
     }
 }
@@ -367,6 +394,463 @@ __global__ __launch_bounds__(kBlock) void k_pair_fill(
     }
 }
 
+// ---------------------------------------------------------------------------
+// One-launch symbolic phase.
+//
+// Every workgroup builds, in LDS, presence bitmaps over the span of A's
+// offsets, of B's offsets and of the pair sums [min da + min db, max da +
+// max db] clipped to (-n, n), each with an exclusive popcount prefix per
+// 32-bit word (rank of an offset = prefix + popcount of the lower bits),
+// plus A's index by rank (perm).  Spans, not n, size these structures, so
+// they are small for banded operands at any n.  The C diagonals are then
+// split into G equal slices, one per workgroup; a workgroup computes the
+// global prefixes its slice starts from directly:
+//   pair_ptr base  = #{(a, b) : -n < da + db < dc_k0} = sum over A of
+//                    rank_B(dc_k0 - da) - rank_B(1 - n - da)
+//   C_starts base  = sum over the C offsets below dc_k0 of n - |dc|
+// so no workgroup waits for another (no grid barrier, no device-scope
+// fence, no global atomics).  Within the slice each wave takes a contiguous
+// run of C diagonals: it counts each one's entries (B diagonals 64 at a
+// time, da = dc - db present in A, counted with a ballot), the waves
+// exchange their totals once, and each wave then writes its diagonals'
+// starts, pair_ptr and GPairs (slot ranks from the same ballot: B order).
+// Everything a workgroup combines goes through one LDS exchange and one
+// barrier per step (eight in all).  Counts, nnz, useful flops and the
+// operands' value extents are computed by every workgroup and written by
+// workgroup 0; each workgroup writes its largest entry count (wg_max) and
+// the host takes the maximum.  If the structures exceed the LDS budget the
+// kernel only raises kFlagFallback.
+// ---------------------------------------------------------------------------
+
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_reduce(T v, Op op)
+{
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) v = op(v, __shfl_xor(v, s, 64));
+    return v;
+}
+
+// Combination of the kFastWaves per-wave values in slot[] (after a barrier).
+template <typename T, typename Op>
+__device__ __forceinline__ T combine_waves(const T* slot, Op op)
+{
+    T r = slot[0];
+#pragma unroll
+    for (int w = 1; w < kFastWaves; ++w) r = op(r, slot[w]);
+    return r;
+}
+
+// Set bits of `bits` below position q (q >= 0 within the span).
+__device__ __forceinline__ int32_t fast_rank(const uint32_t* bits, const int32_t* pfx, int64_t q)
+{
+    const int64_t w = q >> 5;
+    return pfx[w] + __popc(bits[w] & ((1u << (q & 31)) - 1u));
+}
+
+__device__ __forceinline__ bool fast_test(const uint32_t* bits, int64_t q)
+{
+    return (bits[q >> 5] >> (q & 31)) & 1u;
+}
+
+// Position (within the span) of the k-th set bit, 0 <= k < total.
+__device__ int64_t fast_select(const uint32_t* bits, const int32_t* pfx, int32_t nwords, int64_t k)
+{
+    int32_t lo = 0, hi = nwords - 1;
+    while (lo < hi) {                     // last word whose prefix is <= k
+        const int32_t mid = (lo + hi + 1) >> 1;
+        if (pfx[mid] <= k) lo = mid; else hi = mid - 1;
+    }
+    uint32_t m = bits[lo];
+    for (int64_t r = k - pfx[lo]; r > 0; --r) m &= m - 1u;
+    return (int64_t)lo * 32 + (__ffs(m) - 1);
+}
+
+__device__ __forceinline__ int32_t i32min(int32_t x, int32_t y) { return x < y ? x : y; }
+__device__ __forceinline__ int32_t i32max(int32_t x, int32_t y) { return x > y ? x : y; }
+__device__ __forceinline__ int32_t i32or(int32_t x, int32_t y) { return x | y; }
+__device__ __forceinline__ int64_t i64add(int64_t x, int64_t y) { return x + y; }
+__device__ __forceinline__ int64_t i64max(int64_t x, int64_t y) { return x > y ? x : y; }
+
+// Words of LDS the operand tables take: A and B starts (int64), lengths,
+// offsets, and A's index by rank.
+__host__ __device__ constexpr int64_t fast_table_words(int64_t na, int64_t nb)
+{
+    return 5 * na + 4 * nb;
+}
+
+__global__ __launch_bounds__(kFastBlock) void k_sym_fast(
+    int32_t n, const int32_t* __restrict__ A_off, const int32_t* __restrict__ A_len,
+    const int64_t* __restrict__ A_starts, int32_t na, const int32_t* __restrict__ B_off,
+    const int32_t* __restrict__ B_len, const int64_t* __restrict__ B_starts, int32_t nb,
+    int32_t* __restrict__ C_off, int32_t* __restrict__ C_len, int64_t* __restrict__ C_starts,
+    int64_t c_cap, int64_t* __restrict__ pair_ptr, diagpu_gpair* __restrict__ pairs,
+    int64_t p_cap, int32_t* __restrict__ lookup, SymState* __restrict__ st,
+    int32_t* __restrict__ wg_max)
+{
+    extern __shared__ uint32_t lds[];
+    __shared__ int32_t s32[8][kFastWaves];        // one slot per combined value
+    __shared__ int64_t s64[10][kFastWaves];
+    __shared__ int32_t sscan[3][kFastWaves];
+    const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = (int)gridDim.x, wg = (int)blockIdx.x;
+    const bool lane0 = lane == 0;
+
+    // LDS: the operand tables, then the bitmaps and this slice's C offsets
+    int64_t* ast = reinterpret_cast<int64_t*>(lds);
+    int64_t* bst = ast + na;
+    int32_t* alen = reinterpret_cast<int32_t*>(bst + nb);
+    int32_t* blen = alen + na;
+    int32_t* aoff = blen + nb;
+    int32_t* boff = aoff + na;
+    int32_t* perm = boff + nb;
+    uint32_t* bitbase = reinterpret_cast<uint32_t*>(perm + na);
+    const int64_t free_words = kFastLdsWords - fast_table_words(na, nb);
+
+    // 1. operand tables into LDS; validity, ranges, value extents.  The
+    //    bitmap area is cleared meanwhile (whatever part the spans use).
+    int32_t amin = INT_MAX, amax = INT_MIN, bmin = INT_MAX, bmax = INT_MIN, bad = 0;
+    int64_t aext = 0, bext = 0;
+    for (int a = tid; a < na; a += kFastBlock) {
+        const int d = A_off[a], l = A_len[a];
+        const int64_t s0 = A_starts[a];
+        aoff[a] = d;
+        alen[a] = l;
+        ast[a] = s0;
+        if (d <= -n || d >= n || l != n - iabs_(d)) {
+            bad |= kFlagAOffset;
+        } else {
+            amin = i32min(amin, d);
+            amax = i32max(amax, d);
+            aext = i64max(aext, s0 + l);
+        }
+    }
+    for (int b = tid; b < nb; b += kFastBlock) {
+        const int d = B_off[b], l = B_len[b];
+        const int64_t s0 = B_starts[b];
+        boff[b] = d;
+        blen[b] = l;
+        bst[b] = s0;
+        if (d <= -n || d >= n || l != n - iabs_(d)) {
+            bad |= kFlagBOffset;
+        } else {
+            bmin = i32min(bmin, d);
+            bmax = i32max(bmax, d);
+            bext = i64max(bext, s0 + l);
+        }
+    }
+    {   // bitbase is 16-byte aligned when the tables are (5 na + 4 nb words)
+        const int64_t lead = (4 - (fast_table_words(na, nb) & 3)) & 3;
+        for (int64_t w = tid; w < lead && w < free_words; w += kFastBlock) bitbase[w] = 0u;
+        uint4* q = reinterpret_cast<uint4*>(bitbase + lead);
+        const int64_t nq = (free_words - lead) >> 2;
+        for (int64_t w = tid; w < nq; w += kFastBlock) q[w] = uint4{0u, 0u, 0u, 0u};
+        for (int64_t w = lead + 4 * nq + tid; w < free_words; w += kFastBlock) bitbase[w] = 0u;
+    }
+    bad = wave_reduce(bad, i32or);
+    amin = wave_reduce(amin, i32min);
+    amax = wave_reduce(amax, i32max);
+    bmin = wave_reduce(bmin, i32min);
+    bmax = wave_reduce(bmax, i32max);
+    aext = wave_reduce(aext, i64max);
+    bext = wave_reduce(bext, i64max);
+    if (lane0) {
+        s32[0][wave] = bad;
+        s32[1][wave] = amin;
+        s32[2][wave] = amax;
+        s32[3][wave] = bmin;
+        s32[4][wave] = bmax;
+        s64[0][wave] = aext;
+        s64[1][wave] = bext;
+    }
+    __syncthreads();                                                   // barrier 1
+    bad = combine_waves(s32[0], i32or);
+    amin = combine_waves(s32[1], i32min);
+    amax = combine_waves(s32[2], i32max);
+    bmin = combine_waves(s32[3], i32min);
+    bmax = combine_waves(s32[4], i32max);
+    aext = combine_waves(s64[0], i64max);
+    bext = combine_waves(s64[1], i64max);
+    auto report = [&](int32_t flags, int64_t nc, int64_t nnz, int64_t np, int64_t fl) {
+        if (wg == 0 && tid == 0) {
+            st->c_ndiag = nc;
+            st->c_nnz = nnz;
+            st->n_pairs = np;
+            st->max_pairs = 0;
+            st->useful_flops = fl;
+            st->flags = flags;
+            st->pad = 0;
+            st->a_extent = aext;
+            st->b_extent = bext;
+        }
+    };
+    if (bad) {
+        report(bad, 0, 0, 0, 0);
+        return;
+    }
+
+    // 2. bitmaps of the A, B and sum spans, their word prefixes, and room for
+    //    the slice's C offsets (at most ceil(min(na nb, span) / G) of them)
+    const int64_t SA = na ? (int64_t)amax - amin + 1 : 0;
+    const int64_t SB = nb ? (int64_t)bmax - bmin + 1 : 0;
+    int64_t clo = 0, chi = -1;
+    if (na && nb) {
+        clo = (int64_t)amin + bmin;
+        chi = (int64_t)amax + bmax;
+        if (clo < 1 - (int64_t)n) clo = 1 - (int64_t)n;
+        if (chi > (int64_t)n - 1) chi = (int64_t)n - 1;
+    }
+    const int64_t SC = chi >= clo ? chi - clo + 1 : 0;
+    const int64_t wa = (SA + 31) >> 5, wb = (SB + 31) >> 5, wc = (SC + 31) >> 5;
+    const int64_t cmax = (int64_t)na * nb < SC ? (int64_t)na * nb : SC;
+    const int64_t rmax = (cmax + G - 1) / G;
+    if (2 * (wa + wb + wc) + rmax > free_words) {
+        report(kFlagFallback, 0, 0, 0, 0);
+        return;
+    }
+    uint32_t* abits = bitbase;
+    int32_t* apfx = reinterpret_cast<int32_t*>(abits + wa);
+    uint32_t* bbits = reinterpret_cast<uint32_t*>(apfx + wa);
+    int32_t* bpfx = reinterpret_cast<int32_t*>(bbits + wb);
+    uint32_t* cbits = reinterpret_cast<uint32_t*>(bpfx + wb);
+    int32_t* cpfx = reinterpret_cast<int32_t*>(cbits + wc);
+    int32_t* rows = cpfx + wc;                       // the slice's C offsets
+
+    // a bit already set is a repeated offset
+    int32_t dup = 0;
+    for (int a = tid; a < na; a += kFastBlock) {
+        const int64_t q = (int64_t)aoff[a] - amin;
+        const uint32_t m = 1u << (q & 31);
+        if (atomicOr(&abits[q >> 5], m) & m) dup |= kFlagADup;
+    }
+    for (int b = tid; b < nb; b += kFastBlock) {
+        const int64_t q = (int64_t)boff[b] - bmin;
+        const uint32_t m = 1u << (q & 31);
+        if (atomicOr(&bbits[q >> 5], m) & m) dup |= kFlagBDup;
+    }
+    // sums: lanes over B (offsets held in registers, 4 per lane at a time),
+    // waves over A; pair count, useful flops
+    int64_t np = 0, fl = 0;
+    for (int b0 = 0; b0 < nb; b0 += 4 * 64) {
+        int db[4];
+        bool has[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int b = b0 + j * 64 + lane;
+            has[j] = b < nb;
+            db[j] = has[j] ? boff[b] : 0;
+        }
+        // this wave's A offsets (a = wave + kFastWaves i) one per lane, then
+        // taken lane by lane with readlane: no LDS read between the atomics
+        for (int a0 = wave; a0 < na; a0 += 64 * kFastWaves) {
+            const int ai = a0 + lane * kFastWaves;
+            const int mine = ai < na ? aoff[ai] : 0;
+            const int cnt = (na - a0 + kFastWaves - 1) / kFastWaves < 64
+                                ? (na - a0 + kFastWaves - 1) / kFastWaves : 64;
+            for (int i = 0; i < cnt; ++i) {
+                const int da = __builtin_amdgcn_readlane(mine, i);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int64_t dc = (int64_t)da + db[j];
+                    if (has[j] && dc > -(int64_t)n && dc < n) {
+                        const int64_t q = dc - clo;
+                        atomicOr(&cbits[q >> 5], 1u << (q & 31));
+                        ++np;
+                        int m = iabs_(da) > iabs_(db[j]) ? iabs_(da) : iabs_(db[j]);
+                        m = iabs_((int)dc) > m ? iabs_((int)dc) : m;
+                        fl += 2 * (int64_t)(n - m);
+                    }
+                }
+            }
+        }
+    }
+    dup = wave_reduce(dup, i32or);
+    np = wave_reduce(np, i64add);
+    fl = wave_reduce(fl, i64add);
+    if (lane0) {
+        s32[5][wave] = dup;
+        s64[2][wave] = np;
+        s64[3][wave] = fl;
+    }
+    __syncthreads();                                                   // barrier 2
+    dup = combine_waves(s32[5], i32or);
+    np = combine_waves(s64[2], i64add);
+    fl = combine_waves(s64[3], i64add);
+    if (dup) {
+        report(dup, 0, 0, 0, 0);
+        return;
+    }
+
+    // word prefixes of the three bitmaps together: each thread takes kPer
+    // consecutive words per step
+    constexpr int kPer = 4;
+    int32_t carry[3] = {0, 0, 0};
+    const int64_t wmax = wa > wb ? (wa > wc ? wa : wc) : (wb > wc ? wb : wc);
+    for (int64_t base = 0; base < wmax; base += (int64_t)kFastBlock * kPer) {
+        const int64_t w0 = base + (int64_t)tid * kPer;
+        const uint32_t* bm[3] = {abits, bbits, cbits};
+        int32_t* pf[3] = {apfx, bpfx, cpfx};
+        const int64_t nw[3] = {wa, wb, wc};
+        int32_t loc[3][kPer], tot[3], incl[3];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            int32_t t = 0;
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) {
+                loc[j][i] = t;
+                t += (w0 + i < nw[j]) ? __popc(bm[j][w0 + i]) : 0;
+            }
+            tot[j] = t;
+            incl[j] = wave_inclusive_scan(t);
+            if (lane == 63) sscan[j][wave] = incl[j];
+        }
+        __syncthreads();
+        int32_t before[3] = {0, 0, 0}, sum[3] = {0, 0, 0};
+        for (int v = 0; v < kFastWaves; ++v)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                const int32_t t = sscan[j][v];
+                before[j] += v < wave ? t : 0;
+                sum[j] += t;
+            }
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int32_t first = carry[j] + before[j] + incl[j] - tot[j];
+#pragma unroll
+            for (int i = 0; i < kPer; ++i)
+                if (w0 + i < nw[j]) pf[j][w0 + i] = first + loc[j][i];
+            carry[j] += sum[j];
+        }
+        __syncthreads();   // sscan is rewritten by the next step
+    }
+    const int64_t nC = carry[2];
+    if (wmax == 0) __syncthreads();                 // the prefix step's barrier
+
+    // 3. A index by rank; this workgroup's C diagonals [k0, k1) into `rows`
+    //    and the prefixes they start from; the C value count
+    for (int a = tid; a < na; a += kFastBlock) perm[fast_rank(abits, apfx, (int64_t)aoff[a] - amin)] = a;
+    auto rank_b = [&](int64_t x) -> int64_t {       // B offsets below x
+        if (x <= bmin) return 0;
+        if (x > bmax) return nb;
+        return fast_rank(bbits, bpfx, x - bmin);
+    };
+    const int64_t k0 = nC * wg / G, k1 = nC * (wg + 1) / G;
+    int64_t lb = 0, nz = 0;
+    for (int64_t w = tid; w < wc; w += kFastBlock) {
+        int64_t r = cpfx[w];
+        for (uint32_t m = cbits[w]; m; m &= m - 1u, ++r) {
+            const int64_t o = clo + w * 32 + (__ffs(m) - 1);
+            const int64_t len = (int64_t)n - (o < 0 ? -o : o);
+            nz += len;
+            lb += r < k0 ? len : 0;
+            if (r >= k0 && r < k1) rows[r - k0] = (int32_t)o;
+        }
+    }
+    lb = wave_reduce(lb, i64add);
+    nz = wave_reduce(nz, i64add);
+    if (lane0) {
+        s64[5][wave] = lb;
+        s64[6][wave] = nz;
+    }
+    __syncthreads();                                                   // barrier 3
+    const int64_t nnz = combine_waves(s64[6], i64add);
+    int64_t pbase = np, lbase = nnz;
+    if (k0 < nC) {
+        const int64_t d0 = rows[0];
+        int64_t pb = 0;
+        for (int a = tid; a < na; a += kFastBlock)
+            pb += rank_b(d0 - aoff[a]) - rank_b(1 - (int64_t)n - aoff[a]);
+        pb = wave_reduce(pb, i64add);
+        if (lane0) s64[4][wave] = pb;
+        lbase = combine_waves(s64[5], i64add);
+    }
+    int32_t flags = 0;
+    if (nC > c_cap) flags |= kFlagCCapacity;
+    if (np > p_cap) flags |= kFlagPairCapacity;
+    report(flags, nC, nnz, np, fl);
+    if (flags) return;
+
+    // 4. each wave's run of C diagonals: counts, then one exchange
+    const int64_t R = k1 - k0;
+    const int64_t r0 = R * wave / kFastWaves, r1 = R * (wave + 1) / kFastWaves;
+    auto entry = [&](int dc, int b, int64_t& da) -> bool {   // B diagonal b feeds dc
+        if (b >= nb) return false;
+        da = (int64_t)dc - boff[b];
+        return da >= amin && da <= amax && fast_test(abits, da - amin);
+    };
+    int64_t wcnt = 0, wlen = 0;
+    int32_t wmx = 0;
+    for (int64_t r = r0; r < r1; ++r) {
+        const int dc = rows[r];
+        int32_t cnt = 0;
+        for (int b0 = 0; b0 < nb; b0 += 64) {
+            int64_t da;
+            cnt += __popcll(__ballot(entry(dc, b0 + lane, da)));
+        }
+        wcnt += cnt;
+        wlen += n - iabs_(dc);
+        wmx = cnt > wmx ? cnt : wmx;
+    }
+    if (lane0) {
+        s64[7][wave] = wcnt;
+        s64[8][wave] = wlen;
+        s32[6][wave] = wmx;
+    }
+    __syncthreads();                                                   // barrier 4
+    if (k0 < nC) pbase = combine_waves(s64[4], i64add);
+    int64_t slot = pbase, lpos = lbase;
+    for (int v = 0; v < wave; ++v) {
+        slot += s64[7][v];
+        lpos += s64[8][v];
+    }
+    if (tid == 0) wg_max[wg] = combine_waves(s32[6], i32max);
+    if (wg == G - 1 && tid == 0) pair_ptr[nC] = np;
+
+    // 5. the run's starts, pair_ptr, C offsets and lengths, and GPairs (B
+    //    order within each C diagonal)
+    for (int64_t r = r0; r < r1; ++r) {
+        const int64_t k = k0 + r;
+        const int dc = rows[r];
+        const int minc = imin0(dc);
+        if (lane0) {
+            C_off[k] = dc;
+            C_len[k] = n - iabs_(dc);
+            C_starts[k] = lpos;
+            pair_ptr[k] = slot;
+        }
+        lpos += n - iabs_(dc);
+        for (int b0 = 0; b0 < nb; b0 += 64) {
+            const int b = b0 + lane;
+            int64_t da = 0;
+            const bool v = entry(dc, b, da);
+            const uint64_t m = __ballot(v);
+            if (v) {
+                const int ai = perm[fast_rank(abits, apfx, da - amin)];
+                const int db = boff[b];
+                diagpu_gpair g;
+                g.ab = (uint64_t)ast[ai];
+                g.bb = (uint64_t)bst[b];
+                g.ash = imin0((int)da) - minc;
+                g.bsh = (int)da + imin0(db) - minc;
+                g.al = alen[ai];
+                g.bl = blen[b];
+                pairs[slot + __popcll(m & ((1ull << lane) - 1ull))] = g;
+            }
+            slot += __popcll(m);
+        }
+    }
+
+    // 6. lookup: every offset of the 2n - 1, grid-stride over all workgroups
+    if (lookup) {
+        const int64_t nlk = 2 * (int64_t)n - 1;
+        for (int64_t p = (int64_t)wg * kFastBlock + tid; p < nlk; p += (int64_t)G * kFastBlock) {
+            const int64_t o = p - (n - 1);
+            int32_t v = -1;
+            if (o >= clo && o <= chi && fast_test(cbits, o - clo)) v = fast_rank(cbits, cpfx, o - clo);
+            lookup[p] = v;
+        }
+    }
+}
+
 int grid_for(int64_t work, int64_t cap = 65536)
 {
     int64_t g = ceil_div<int64_t>(work, kBlock);
@@ -403,6 +887,27 @@ int scratch_ptr(const char* fn, void** out)
         addr[dev] = p;
     }
     *out = addr[dev];
+    return DIAGPU_OK;
+}
+
+// k_sym_fast takes kFastLdsBytes of dynamic LDS; more than 64 KiB must be
+// allowed explicitly (once per device).
+int fast_lds_allowed(const char* fn)
+{
+    static std::mutex mu;
+    static bool done[64] = {};
+    int dev = 0;
+    int rc = check_hip(hipGetDevice(&dev), fn);
+    if (rc) return rc;
+    if (dev < 0 || dev >= 64) return fail(DIAGPU_ERR_ARG, "%s: device %d out of range", fn, dev);
+    std::lock_guard<std::mutex> lock(mu);
+    if (!done[dev]) {
+        rc = check_hip(hipFuncSetAttribute((const void*)k_sym_fast,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           kFastLdsBytes), fn);
+        if (rc) return rc;
+        done[dev] = true;
+    }
     return DIAGPU_OK;
 }
 
@@ -456,44 +961,85 @@ int run_symbolic(
     int64_t* part = reinterpret_cast<int64_t*>(ws + L.off_part);
     SymState* st = reinterpret_cast<SymState*>(ws + L.off_state);
     hipStream_t s = as_stream(stream);
-    const int64_t c_cap = c_capacity < L.cmax ? c_capacity : L.cmax;
-    const int64_t nkb = ceil_div<int64_t>(c_cap + 1, kBlock);
+    int32_t* wg_max = reinterpret_cast<int32_t*>(st + 1);   // after the state record
+    struct {
+        SymState h;
+        int32_t m[kMaxFastGroups];
+    } back;
+    SymState& h = back.h;
+    int rc = DIAGPU_OK;
 
-    hipLaunchKernelGGL(k_init, dim3(grid_for(L.nlk, 4096)), dim3(kBlock), 0, s, alk, L.nlk, bbits,
-                       cbits, L.nwords, st);
-    hipLaunchKernelGGL(k_operands, dim3(grid_for(a_ndiag > b_ndiag ? a_ndiag : b_ndiag)),
-                       dim3(kBlock), 0, s, n, A_off, A_len, a_ndiag, B_off, B_len, b_ndiag, alk,
-                       bbits, st);
-    hipLaunchKernelGGL(k_mark, dim3(grid_for((int64_t)a_ndiag * b_ndiag, 8192)), dim3(kBlock), 0,
-                       s, n, A_off, a_ndiag, B_off, b_ndiag, cbits);
-    hipLaunchKernelGGL(k_word_sums, dim3((unsigned)L.nwblocks), dim3(kBlock), 0, s, cbits,
-                       L.nwords, wsum);
-    hipLaunchKernelGGL(k_word_scan, dim3(1), dim3(kBlock), 0, s, wsum, L.nwblocks, st);
-    hipLaunchKernelGGL(k_emit, dim3((unsigned)L.nwblocks), dim3(kBlock), 0, s, n, cbits, L.nwords,
-                       wsum, wprefix, C_off, C_len, c_cap, st);
-    if (c_lookup)
-        hipLaunchKernelGGL(k_lookup, dim3(grid_for(L.nlk, 8192)), dim3(kBlock), 0, s, cbits,
-                           wprefix, L.nlk, c_lookup);
-    hipLaunchKernelGGL(k_pair_count, dim3((unsigned)nkb), dim3(kBlock), 0, s, n, C_off, C_len,
-                       c_cap, B_off, b_ndiag, alk, pair_ptr, part, nkb, st);
-    hipLaunchKernelGGL(k_scan_top, dim3(1), dim3(kBlock), 0, s, part, nkb, st);
-    hipLaunchKernelGGL(k_scan_final, dim3((unsigned)nkb), dim3(kBlock), 0, s, C_len, pair_ptr,
-                       C_starts, part, nkb, c_cap, st);
-    hipLaunchKernelGGL(k_pair_fill, dim3((unsigned)nkb), dim3(kBlock), 0, s, n, C_off, c_cap,
-                       A_len, A_starts, B_off, B_len, B_starts, b_ndiag, alk, pair_ptr, pairs,
-                       pair_capacity, st);
-    int rc = check_launch(fn);
-    if (rc) return rc;
-    SymState h;
-    rc = check_hip(hipMemcpyAsync(&h, st, sizeof(h), hipMemcpyDeviceToHost, s), fn);
-    if (rc) return rc;
-    rc = check_hip(hipStreamSynchronize(s), fn);
-    if (rc) return rc;
+    // The one-launch path where the operand product is small enough for each
+    // workgroup to enumerate (it reports kFlagFallback when the spans do not
+    // fit in its LDS); the multi-launch path below otherwise.
+    bool done = false;
+    if ((int64_t)a_ndiag * b_ndiag <= kFastMaxProducts &&
+        fast_table_words(a_ndiag, b_ndiag) <= kFastLdsWords / 2) {
+        rc = fast_lds_allowed(fn);
+        if (rc) return rc;
+        int64_t ub = (int64_t)a_ndiag * b_ndiag;
+        if (ub > 2 * (int64_t)n - 1) ub = 2 * (int64_t)n - 1;
+        int64_t G = ceil_div<int64_t>(ub, 32);
+        const int64_t gmax = cu_count() < kMaxFastGroups ? cu_count() : kMaxFastGroups;
+        G = G < 1 ? 1 : (G > gmax ? gmax : G);
+        hipLaunchKernelGGL(k_sym_fast, dim3((unsigned)G), dim3(kFastBlock), kFastLdsBytes, s, n,
+                           A_off, A_len, A_starts, a_ndiag, B_off, B_len, B_starts, b_ndiag,
+                           C_off, C_len, C_starts, c_capacity, pair_ptr, pairs, pair_capacity,
+                           c_lookup, st, wg_max);
+        rc = check_launch(fn);
+        if (rc) return rc;
+        // one synchronous, stream-ordered copy: the kernel and everything
+        // before it on `s` are complete when it returns (it costs about
+        // 9 us less than an asynchronous copy plus a stream synchronisation)
+        rc = check_hip(hipMemcpyWithStream(&back, st, sizeof(SymState) + sizeof(int32_t) * G,
+                                           hipMemcpyDeviceToHost, s), fn);
+        if (rc) return rc;
+        if (!(h.flags & kFlagFallback)) {
+            int32_t mx = 0;
+            for (int64_t g = 0; g < G && !h.flags; ++g) mx = back.m[g] > mx ? back.m[g] : mx;
+            h.max_pairs = mx;
+            done = true;
+        }
+    }
+    if (!done) {
+        const int64_t c_cap = c_capacity < L.cmax ? c_capacity : L.cmax;
+        const int64_t nkb = ceil_div<int64_t>(c_cap + 1, kBlock);
+
+        hipLaunchKernelGGL(k_init, dim3(grid_for(L.nlk, 4096)), dim3(kBlock), 0, s, alk, L.nlk, bbits,
+                           cbits, L.nwords, st);
+        hipLaunchKernelGGL(k_operands, dim3(grid_for(a_ndiag > b_ndiag ? a_ndiag : b_ndiag)),
+                           dim3(kBlock), 0, s, n, A_off, A_len, A_starts, a_ndiag, B_off, B_len,
+                           B_starts, b_ndiag, alk, bbits, st);
+        hipLaunchKernelGGL(k_mark, dim3(grid_for((int64_t)a_ndiag * b_ndiag, 8192)), dim3(kBlock), 0,
+                           s, n, A_off, a_ndiag, B_off, b_ndiag, cbits);
+        hipLaunchKernelGGL(k_word_sums, dim3((unsigned)L.nwblocks), dim3(kBlock), 0, s, cbits,
+                           L.nwords, wsum);
+        hipLaunchKernelGGL(k_word_scan, dim3(1), dim3(kBlock), 0, s, wsum, L.nwblocks, st);
+        hipLaunchKernelGGL(k_emit, dim3((unsigned)L.nwblocks), dim3(kBlock), 0, s, n, cbits, L.nwords,
+                           wsum, wprefix, C_off, C_len, c_cap, st);
+        if (c_lookup)
+            hipLaunchKernelGGL(k_lookup, dim3(grid_for(L.nlk, 8192)), dim3(kBlock), 0, s, cbits,
+                               wprefix, L.nlk, c_lookup);
+        hipLaunchKernelGGL(k_pair_count, dim3((unsigned)nkb), dim3(kBlock), 0, s, n, C_off, C_len,
+                           c_cap, B_off, b_ndiag, alk, pair_ptr, part, nkb, st);
+        hipLaunchKernelGGL(k_scan_top, dim3(1), dim3(kBlock), 0, s, part, nkb, st);
+        hipLaunchKernelGGL(k_scan_final, dim3((unsigned)nkb), dim3(kBlock), 0, s, C_len, pair_ptr,
+                           C_starts, part, nkb, c_cap, st);
+        hipLaunchKernelGGL(k_pair_fill, dim3((unsigned)nkb), dim3(kBlock), 0, s, n, C_off, c_cap,
+                           A_len, A_starts, B_off, B_len, B_starts, b_ndiag, alk, pair_ptr, pairs,
+                           pair_capacity, st);
+        rc = check_launch(fn);
+        if (rc) return rc;
+        rc = check_hip(hipMemcpyWithStream(&h, st, sizeof(h), hipMemcpyDeviceToHost, s), fn);
+        if (rc) return rc;
+    }
     info->c_ndiag = h.c_ndiag;
     info->c_nnz = h.c_nnz;
     info->n_pairs = h.n_pairs;
     info->max_pairs = h.max_pairs;
     info->useful_flops = h.useful_flops;
+    info->a_extent = h.a_extent;
+    info->b_extent = h.b_extent;
     if (h.flags & (kFlagAOffset | kFlagBOffset))
         return fail(DIAGPU_ERR_OFFSET, "%s: an %s offset has |d| >= n=%d or length != n - |d|",
                     fn, (h.flags & kFlagAOffset) ? "A" : "B", n);

@@ -40,24 +40,28 @@ class SpgemmPlan:
             _check_dev(M.starts, torch.int64, f"{nm}.starts")
         self.A, self.B, self.n = A, B, A.n
         self.stream = stream
-        # values each operand must hold: the end of its furthest diagonal
-        self.a_need, self.b_need = (
-            int((M.starts + M.lengths).max().item()) if M.offsets.numel() else 0
-            for M in (A, B))
         dev = A.offsets.device
         na, nb = A.offsets.numel(), B.offsets.numel()
         self.c_cap = max(1, min(na * nb, 2 * self.n - 1))
         self.p_cap = max(1, na * nb)
         ws = C.c_size_t(0)
         _lib.call("diagpu_spgemm_symbolic_workspace", self.n, na, nb, C.byref(ws))
-        self.workspace = torch.empty(ws.value, dtype=torch.uint8, device=dev)
-        self.C_off = torch.empty(self.c_cap, dtype=torch.int32, device=dev)
-        self.C_len = torch.empty(self.c_cap, dtype=torch.int32, device=dev)
-        self.C_starts = torch.empty(self.c_cap, dtype=torch.int64, device=dev)
-        self.ptr = torch.empty(self.c_cap + 1, dtype=torch.int64, device=dev)
-        self.pairs = torch.empty(self.p_cap * GPAIR_BYTES, dtype=torch.uint8, device=dev)
-        self.lookup = (torch.empty(2 * self.n - 1, dtype=torch.int32, device=dev)
-                       if want_lookup else None)
+        # the workspace and every plan array in one allocation, 256-byte aligned parts
+        parts = [("workspace", torch.uint8, ws.value), ("C_off", torch.int32, self.c_cap),
+                 ("C_len", torch.int32, self.c_cap), ("C_starts", torch.int64, self.c_cap),
+                 ("ptr", torch.int64, self.c_cap + 1),
+                 ("pairs", torch.uint8, self.p_cap * GPAIR_BYTES)]
+        if want_lookup:
+            parts.append(("lookup", torch.int32, 2 * self.n - 1))
+        esz = {torch.uint8: 1, torch.int32: 4, torch.int64: 8}
+        sizes = [-(-cnt * esz[dt] // 256) * 256 for _, dt, cnt in parts]
+        buf = torch.empty(sum(sizes), dtype=torch.uint8, device=dev)
+        o = 0
+        for (name, dt, cnt), sz in zip(parts, sizes):
+            setattr(self, name, buf[o: o + cnt * esz[dt]].view(dt))
+            o += sz
+        if not want_lookup:
+            self.lookup = None
         self.info = _lib.SpgemmInfo()
         self._band = None
         self._astat = None
@@ -185,9 +189,10 @@ class SpgemmPlan:
         _check_dev(A_vals, dt, "A_vals")
         _check_dev(B_vals, dt, "B_vals")
         _check_dev(C_vals, dt, "C_vals")
-        if A_vals.numel() < self.a_need or B_vals.numel() < self.b_need:
+        if A_vals.numel() < self.info.a_extent or B_vals.numel() < self.info.b_extent:
             raise ValueError(f"A_vals / B_vals hold {A_vals.numel()} / {B_vals.numel()} values; "
-                             f"the plan's operands need {self.a_need} / {self.b_need}")
+                             f"the plan's operands need {self.info.a_extent} / "
+                             f"{self.info.b_extent}")
         if C_vals.numel() < self.info.c_nnz:
             raise ValueError(f"C_vals has {C_vals.numel()} elements, needs {self.info.c_nnz}")
         if kernel == "auto":

@@ -26,8 +26,13 @@ def _on_stream(stream):
     return torch.cuda.stream(stream)
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream_handle(stream) -> int:
     if stream is None:
+        if _raw_stream is not None:      # the current stream's handle, without a Stream object
+            return _raw_stream(torch.cuda.current_device())
         return torch.cuda.current_stream().cuda_stream
     if isinstance(stream, torch.cuda.Stream):
         return stream.cuda_stream

@@ -183,6 +183,8 @@ typedef struct diagpu_spgemm_info {
     int64_t n_pairs;         /* number of pair-plan entries                 */
     int64_t max_pairs;       /* largest pair count of one C diagonal        */
     int64_t useful_flops;    /* 2 * sum over pairs of the overlap length    */
+    int64_t a_extent;        /* values A_vals must hold: max(start + length) */
+    int64_t b_extent;        /* values B_vals must hold                     */
 } diagpu_spgemm_info;
 
 /* Device workspace the symbolic phase needs for dimension n and operand
@@ -205,8 +207,9 @@ DIAGPU_API int diagpu_spgemm_symbolic_workspace(int32_t n, int32_t a_ndiag, int3
  *                pair_ptr has c_ndiag + 1 entries.
  * Operand offsets may be in any order but must be distinct with |d| < n, and
  * lengths must equal n - |d| (DIAGPU_ERR_DUPLICATE / DIAGPU_ERR_OFFSET).
- * Synchronises `stream` and writes *info (host).  The C starts of the
- * operands are only copied into the plan (ab, bb), never dereferenced. */
+ * Synchronises `stream` and writes *info (host), including the value
+ * extents max(start + length) of A and B (how many values A_vals and B_vals
+ * must hold for the numeric phase).  Operand values are not read. */
 DIAGPU_API int diagpu_spgemm_symbolic(
     int32_t n,
     const int32_t* A_off, const int32_t* A_len, const int64_t* A_starts, int32_t a_ndiag,

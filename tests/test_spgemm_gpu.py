@@ -39,6 +39,8 @@ def check_plan(oracle, plan, A, B):
         assert np.array_equal(got[f], pairs[f]), f
     counts = np.diff(ptr)
     assert plan.info.max_pairs == (counts.max() if len(counts) else 0)
+    for M, ext in ((a, plan.info.a_extent), (b, plan.info.b_extent)):
+        assert ext == (int((M[2] + M[1]).max()) if len(M[0]) else 0)
     # useful flops: 2 * sum over pairs of n - max(|da|, |db|, |dc|)
     dc = np.repeat(c_off.astype(np.int64), counts)
     b_of = {int(s): int(o) for s, o in zip(b[2], b[0])}
@@ -94,6 +96,36 @@ def test_random_products(dev, oracle, seed, n, na, nb, span):
             sr, sc = (0, d) if d >= 0 else (-d, 0)
             assert np.allclose(g[s:s + ln], P[sr + np.arange(ln), sc + np.arange(ln)],
                                rtol=0, atol=1e-5)
+
+
+@pytest.mark.parametrize("n,offs_a,offs_b", [
+    # offset spans beyond the one-launch path's LDS: the multi-launch symbolic path
+    ((1 << 22) + 3, [-(1 << 22) - 2, -5, 0, 7, (1 << 22) + 2], [-3, 0, 1, (1 << 21)]),
+    (600_000, [-599_999, 0, 599_999], [-599_999, -1, 2, 599_999]),
+])
+def test_symbolic_wide_spans(dev, oracle, n, offs_a, offs_b):
+    A = workloads.hm_random(n, offs_a, seed=81, device=dev)
+    B = workloads.hm_random(n, offs_b, seed=82, device=dev)
+    plan = SpgemmPlan(A, B, want_lookup=True)
+    c_off, c_len, c_st, nnz, ptr, pairs = check_plan(oracle, plan, A, B)
+    Cv = plan.multiply(A.values, B.values)
+    want, ab = oracle.spgemm_pairs_f64(A.values.cpu().numpy(), B.values.cpu().numpy(), c_len,
+                                       c_st, ptr, pairs, 0, len(c_off))
+    check_values(Cv.cpu().numpy(), want, ab)
+
+
+def test_symbolic_large_product(dev, oracle):
+    """1100 x 1000 diagonals (1.1M pairs, more than the one-launch path
+    enumerates): the multi-launch path, bit-exact."""
+    n = 1200
+    rng = np.random.default_rng(17)
+    oa = rng.choice(np.arange(-n + 1, n), size=1100, replace=False)
+    ob = rng.choice(np.arange(-n + 1, n), size=1000, replace=False)
+    A = workloads.hm_random(n, oa, seed=83, device=dev)
+    B = workloads.hm_random(n, ob, seed=84, device=dev)
+    plan = SpgemmPlan(A, B, want_lookup=True)
+    assert plan.info.n_pairs > 1 << 20 or len(oa) * len(ob) > 1 << 20
+    check_plan(oracle, plan, A, B)
 
 
 def test_reference_bench_operands(dev, oracle):

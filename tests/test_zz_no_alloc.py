@@ -57,7 +57,8 @@ def _symbolic(A, B, noalloc):
         "pairs": out["pairs"][:npair * C.sizeof(_lib.GPair)].cpu().numpy(),
         "lookup": out["lookup"].cpu().numpy(),
     }
-    counts = (info.c_ndiag, info.c_nnz, info.n_pairs, info.max_pairs, info.useful_flops)
+    counts = (info.c_ndiag, info.c_nnz, info.n_pairs, info.max_pairs, info.useful_flops,
+              info.a_extent, info.b_extent)
     return res, counts
 
 
