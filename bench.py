@@ -290,6 +290,8 @@ def compare_kernels(plan, sets, reps: int, alg: int, flops: int) -> dict:
     names = ["gather"]
     if plan.band_info()[1].eligible:
         names.append("band")
+    if plan.band_info()[1].mfma_eligible:
+        names.append("band_mfma")
     if plan.A.offsets.numel() <= _lib.ASTAT_MAX_A:
         try:
             plan.astat_records()
@@ -314,13 +316,18 @@ def compare_kernels(plan, sets, reps: int, alg: int, flops: int) -> dict:
         kms = e0.elapsed_time(e1) / reps
         rec = {"numeric_ms": round(kms, 5), "GFLOPs": round(flops / (kms * 1e6), 1),
                "frac_hbm": round(alg / (kms * 1e6) / HBM_PEAK_GBS, 4), "same_bits_as_gather": None}
+        if k == "band_mfma":
+            rec["mfma_utilisation"] = round(plan.mfma_utilisation(), 4)
+            rec["mfma_blocks_per_16_rows"] = plan.band_info()[1].mfma_blocks
         if check:
             plan.numeric(*sets[0], kernel=k)
             torch.cuda.synchronize()
-            c = sets[0][2][: plan.info.c_nnz].view(torch.int32)
+            c = sets[0][2][: plan.info.c_nnz]
             if ref is None:
                 ref = c.clone()
-            rec["same_bits_as_gather"] = bool(torch.equal(ref, c))
+            rec["same_bits_as_gather"] = bool(torch.equal(ref.view(torch.int32), c.view(torch.int32)))
+            if not rec["same_bits_as_gather"]:
+                rec["max_abs_diff_vs_gather"] = float((c - ref).abs().max())
         out[k] = rec
     return out
 
@@ -487,12 +494,11 @@ def time_gemm_diag(n: int = 4096, hb: int = 10, reps: int = 100):
     """gemm_diag on row-packed operands (gemm_diag/gemm_diag.cu:9-15) with the
     reference driver's default shape (n = 4096, offsets -hb..hb, values
     U(0.5, 1.5), gemm_diag.cu:467-486): the plan once, then `reps` timed
-    numeric phases.  The reference kernel has no tensor-core instructions
-    (products in shared memory, a sequential reduction and atomicAdd); here
-    the product runs on the SpGEMM numeric kernels (the gather, or the
-    LDS-tiled band kernel at large n), so MFMA utilisation is 0: at
-    <= 0.84 flop/B every config is HBM-bound, and fp32 MFMA peak equals the
-    fp32 vector peak on MI355X."""
+    numeric phases, then every kernel that takes the plan side by side,
+    including the fp32 MFMA band kernel with its utilisation (useful /
+    issued flops from its tile geometry).  The reference kernel has no
+    tensor-core instructions (products in shared memory, a sequential
+    reduction and atomicAdd)."""
     import torch
     from diagpu_amd.spgemm import gemm_diag
     offs = list(range(-hb, hb + 1))
@@ -524,14 +530,18 @@ def time_gemm_diag(n: int = 4096, hb: int = 10, reps: int = 100):
     nnz = sum(n - abs(d) for d in offs)
     alg = 4 * (2 * nnz + plan.info.c_nnz)
     flops = plan.info.useful_flops
+    kernels = compare_kernels(plan, [(DA, DB, C)], max(5, reps // 2), alg, flops)
+    kern = plan.kernel_for()
     return {"workload": f"gemm_diag_n{n}_hb{hb}", "n": n, "A_diags": len(offs),
             "B_diags": len(offs), "C_diags": plan.info.c_ndiag, "numeric_ms": round(ms, 5),
-            "kernel": plan.kernel_for(), "first_call_ms": round(first_ms, 3),
+            "kernel": kern, "first_call_ms": round(first_ms, 3),
             "GFLOPs": round(flops / (ms * 1e6), 1),
             "GBs": round(alg / (ms * 1e6), 1), "frac_hbm": round(alg / (ms * 1e6) / HBM_PEAK_GBS, 4),
-            "alg_bytes": alg, "mfma_utilisation": 0.0,
-            "mfma_note": "no dense tile contraction: banded products at <= 0.84 flop/B are HBM-bound, "
-                         "and the reference kernel uses no tensor-core instructions"}
+            "alg_bytes": alg,
+            # useful / issued flops of the kernel that ran; None when that kernel
+            # issues no MFMA (the MFMA band kernel's figure is under kernels)
+            "mfma_utilisation": (round(plan.mfma_utilisation(), 4) if kern == "band_mfma" else None),
+            "kernels": kernels}
 
 
 def copy_calibration(steps: int):

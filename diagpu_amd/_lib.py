@@ -60,7 +60,10 @@ class GPair(C.Structure):
 class BandInfo(C.Structure):
     _fields_ = [("a_off_min", C.c_int32), ("a_off_max", C.c_int32),
                 ("rows_per_block", C.c_int32), ("eligible", C.c_int32),
-                ("lds_bytes", C.c_int64), ("n_pairs", C.c_int64)]
+                ("lds_bytes", C.c_int64), ("n_pairs", C.c_int64),
+                ("b_off_min", C.c_int32), ("b_off_max", C.c_int32),
+                ("mfma_blocks", C.c_int32), ("mfma_eligible", C.c_int32),
+                ("mfma_lds_bytes", C.c_int64)]
 
 
 class SpgemmInfo(C.Structure):
@@ -130,6 +133,9 @@ PROTOTYPES: dict[str, tuple] = {
     "diagpu_spgemm_numeric_band_f32": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp,
                                                  _vp, _vp, _i64, _vp, _vp, C.POINTER(BandInfo),
                                                  _vp, _vp]),
+    "diagpu_spgemm_numeric_band_mfma_f32": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _i32,
+                                                      _vp, _vp, _vp, _i64, C.POINTER(BandInfo),
+                                                      _vp, _vp]),
     "diagpu_spgemm_astat_prepare": (C.c_int, [_i32, _vp, _i32, _vp, _i64, _vp, _vp]),
     "diagpu_spgemm_numeric_astat_f32": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp,
                                                   _i64, _vp, _vp, _i64, _vp, _vp]),

@@ -27,6 +27,7 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "band_mfma.hpp"
 #include "common.hpp"
 
 namespace diagpu {
@@ -111,16 +112,24 @@ __global__ __launch_bounds__(256) void k_band_prepare(int32_t n,
     entries[g] = int4{a * kRB, b * wb + (da - lo), da, 0};
 }
 
-// min and max of A's offsets, one workgroup
+// min and max of A's offsets (out[0], out[1]) and of B's (out[3], out[4]),
+// one workgroup; out[2] is the bad-entry flag, cleared here
 __global__ __launch_bounds__(256) void k_span(const int32_t* __restrict__ off, int32_t cnt,
+                                              const int32_t* __restrict__ boff, int32_t bcnt,
                                               int32_t* __restrict__ out)
 {
-    __shared__ int lo_s[256], hi_s[256];
-    int lo = 0x7fffffff, hi = -0x7fffffff - 1;
+    __shared__ int lo_s[256], hi_s[256], blo_s[256], bhi_s[256];
+    int lo = 0x7fffffff, hi = -0x7fffffff - 1, blo = 0x7fffffff, bhi = -0x7fffffff - 1;
     for (int i = threadIdx.x; i < cnt; i += 256) {
         lo = off[i] < lo ? off[i] : lo;
         hi = off[i] > hi ? off[i] : hi;
     }
+    for (int i = threadIdx.x; i < bcnt; i += 256) {
+        blo = boff[i] < blo ? boff[i] : blo;
+        bhi = boff[i] > bhi ? boff[i] : bhi;
+    }
+    blo_s[threadIdx.x] = blo;
+    bhi_s[threadIdx.x] = bhi;
     lo_s[threadIdx.x] = lo;
     hi_s[threadIdx.x] = hi;
     __syncthreads();
@@ -128,6 +137,8 @@ __global__ __launch_bounds__(256) void k_span(const int32_t* __restrict__ off, i
         if ((int)threadIdx.x < s) {
             lo_s[threadIdx.x] = lo_s[threadIdx.x + s] < lo_s[threadIdx.x] ? lo_s[threadIdx.x + s] : lo_s[threadIdx.x];
             hi_s[threadIdx.x] = hi_s[threadIdx.x + s] > hi_s[threadIdx.x] ? hi_s[threadIdx.x + s] : hi_s[threadIdx.x];
+            blo_s[threadIdx.x] = blo_s[threadIdx.x + s] < blo_s[threadIdx.x] ? blo_s[threadIdx.x + s] : blo_s[threadIdx.x];
+            bhi_s[threadIdx.x] = bhi_s[threadIdx.x + s] > bhi_s[threadIdx.x] ? bhi_s[threadIdx.x + s] : bhi_s[threadIdx.x];
         }
         __syncthreads();
     }
@@ -135,6 +146,8 @@ __global__ __launch_bounds__(256) void k_span(const int32_t* __restrict__ off, i
         out[0] = lo_s[0];
         out[1] = hi_s[0];
         out[2] = 0;   // bad-entry flag, set by k_band_prepare (launched next)
+        out[3] = blo_s[0];
+        out[4] = bhi_s[0];
     }
 }
 
@@ -332,9 +345,9 @@ DIAGPU_API int diagpu_spgemm_band_prepare(int32_t n, const int32_t* A_off,
     if (!A_off || !A_starts || !B_off || !B_starts || !entries || (n_pairs > 0 && !pairs))
         return fail(DIAGPU_ERR_ARG, "%s: a pointer is NULL", fn);
     hipStream_t s = as_stream(stream);
-    int32_t* dev = entries + 4 * n_pairs;   // caller's 4 scratch ints: A span, bad-entry flag
-    int32_t host[3] = {0, 0, 0};
-    hipLaunchKernelGGL(k_span, dim3(1), dim3(256), 0, s, A_off, nA, dev);
+    int32_t* dev = entries + 4 * n_pairs;   // caller's 8 scratch ints: spans, bad-entry flag
+    int32_t host[5] = {0, 0, 0, 0, 0};
+    hipLaunchKernelGGL(k_span, dim3(1), dim3(256), 0, s, A_off, nA, B_off, nB, dev);
     int st = check_launch(fn);
     if (!st && n_pairs > 0) {
         hipLaunchKernelGGL(k_band_prepare, dim3((unsigned)ceil_div<int64_t>(n_pairs, 256)),
@@ -349,8 +362,16 @@ DIAGPU_API int diagpu_spgemm_band_prepare(int32_t n, const int32_t* A_off,
                     "its shifts or lengths are not the symbolic phase's for those diagonals", fn);
     if (host[0] <= -n || host[1] >= n)
         return fail(DIAGPU_ERR_OFFSET, "%s: an A offset is outside (-n, n)", fn);
+    if (host[3] <= -n || host[4] >= n)
+        return fail(DIAGPU_ERR_OFFSET, "%s: a B offset is outside (-n, n)", fn);
     info->a_off_min = host[0];
     info->a_off_max = host[1];
+    info->b_off_min = host[3];
+    info->b_off_max = host[4];
+    const MfmaGeom g = mfma_geom(host[0], host[1], host[3], host[4]);
+    info->mfma_blocks = g.ok ? g.nblk : 0;
+    info->mfma_eligible = g.ok;
+    info->mfma_lds_bytes = g.ok ? g.lds_bytes : 0;
     info->rows_per_block = kRB;
     info->n_pairs = n_pairs;
     info->lds_bytes = band_lds_bytes(nA, nB, host[1] - host[0], n_pairs);

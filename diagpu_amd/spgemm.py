@@ -102,10 +102,10 @@ class SpgemmPlan:
     # numeric ---------------------------------------------------------------
     def band_info(self):
         """(entries, BandInfo) of diagpu_spgemm_band_prepare for this plan
-        (computed once; one stream sync); entries int32 [4 n_pairs + 4]."""
+        (computed once; one stream sync); entries int32 [4 n_pairs + 8]."""
         if self._band is None:
             A, B = self.A, self.B
-            pab = torch.empty(4 * self.info.n_pairs + 4, dtype=torch.int32,
+            pab = torch.empty(4 * self.info.n_pairs + 8, dtype=torch.int32,
                               device=self.C_off.device)
             info = _lib.BandInfo()
             _lib.call("diagpu_spgemm_band_prepare", self.n, A.offsets.data_ptr(),
@@ -165,6 +165,17 @@ class SpgemmPlan:
             return False
         return True
 
+    def mfma_utilisation(self) -> float | None:
+        """Useful / issued flops of the MFMA band kernel on this plan (issued:
+        2 * 16 * 16 * 4 per block, band_info().mfma_blocks blocks per 16-row
+        tile, the four tiles of every 64-row slab), or None if it does not
+        take the plan."""
+        info = self.band_info()[1]
+        if not info.mfma_eligible or info.mfma_blocks == 0:
+            return None
+        issued = 2 * 16 * 16 * 4 * info.mfma_blocks * 4 * -(-self.n // 64)
+        return self.info.useful_flops / issued
+
     def kernel_for(self, dtype=torch.float32) -> str:
         """The kernel "auto" runs: "band", "astat" or "gather"."""
         if self.uses_band(dtype):
@@ -178,13 +189,15 @@ class SpgemmPlan:
         """C values for the plan's structure; float32 or complex64 (all three
         tensors the same dtype).  kernel: "auto" (kernel_for), "gather" (any
         plan), "band" (fp32, narrow bands) or "astat" (fp32, at most
-        DIAGPU_ASTAT_MAX_A A diagonals); all return the same bits."""
+        DIAGPU_ASTAT_MAX_A A diagonals), which all return the same bits, or
+        "band_mfma" (fp32, narrow bands on the matrix cores: the same values
+        to rounding, finite operands)."""
         dt = A_vals.dtype
         name = {torch.float32: "diagpu_spgemm_numeric_f32",
                 torch.complex64: "diagpu_spgemm_numeric_c64"}.get(dt)
         if name is None:
             raise TypeError(f"unsupported value dtype {dt}")
-        if kernel not in ("auto", "gather", "band", "astat"):
+        if kernel not in ("auto", "gather", "band", "astat", "band_mfma"):
             raise ValueError(f"unknown kernel {kernel!r}")
         _check_dev(A_vals, dt, "A_vals")
         _check_dev(B_vals, dt, "B_vals")
@@ -197,8 +210,18 @@ class SpgemmPlan:
             raise ValueError(f"C_vals has {C_vals.numel()} elements, needs {self.info.c_nnz}")
         if kernel == "auto":
             kernel = self.kernel_for(dt)
-        if kernel in ("band", "astat") and dt != torch.float32:
+        if kernel in ("band", "astat", "band_mfma") and dt != torch.float32:
             raise TypeError(f"the {kernel} kernel is fp32")
+        if kernel == "band_mfma":
+            _, info = self.band_info()
+            A, B = self.A, self.B
+            _lib.call("diagpu_spgemm_numeric_band_mfma_f32", self.n, A.offsets.data_ptr(),
+                      A.starts.data_ptr(), A.offsets.numel(), A_vals.data_ptr(),
+                      B.offsets.data_ptr(), B.starts.data_ptr(), B.offsets.numel(),
+                      B_vals.data_ptr(), self.C_off.data_ptr(), self.C_starts.data_ptr(),
+                      self.info.c_ndiag, C.byref(info), C_vals.data_ptr(),
+                      _stream_handle(self.stream))
+            return
         if kernel == "astat":
             rec = self.astat_records()
             A = self.A

@@ -278,13 +278,21 @@ typedef struct diagpu_band_info {
                                     /* 16 n_pairs, wb = rpb + span rounded up  */
                                     /* to a multiple of 4                      */
     int64_t n_pairs;                /* plan entries                            */
+    int32_t b_off_min, b_off_max;   /* smallest and largest B offset          */
+    int32_t mfma_blocks;            /* MFMA variant: 16x16x4 fp32 blocks       */
+                                    /* issued per 16-row tile of C (issued     */
+                                    /* flops = 2048 * mfma_blocks * 4 *        */
+                                    /* ceil(n / 64): 4 tiles per 64-row slab)  */
+    int32_t mfma_eligible;          /* 1: the MFMA variant takes the plan      */
+    int64_t mfma_lds_bytes;         /* its LDS per workgroup                   */
 } diagpu_band_info;
 
 /* For the band kernel, per plan (once): entries[4g .. 4g+3] = {a rpb,
  * b wb + (da - min da), da, 0} for plan entry g, a and b the
  * indices of its A and B diagonals (looked up from the entry's starts), and
- * A's offset span in *info.  entries holds 4 n_pairs + 4 int32 (the last 4
- * are scratch).  One stream synchronisation (to return *info).
+ * A's and B's offset spans, and the MFMA variant's geometry, in *info.
+ * entries holds 4 n_pairs + 8 int32 (the last 8 are scratch).  One stream
+ * synchronisation (to return *info).
  * DIAGPU_ERR_OFFSET if an A offset lies outside (-n, n); DIAGPU_ERR_ARG if an
  * entry's starts are not the starts of an A and a B diagonal, or if its
  * ash, bsh, al, bl differ from what diagpu_spgemm_symbolic writes for those
@@ -310,6 +318,28 @@ DIAGPU_API int diagpu_spgemm_numeric_band_f32(
     const int32_t* B_off, const int64_t* B_starts, int32_t nB, const float* B_vals,
     const int32_t* C_off, const int64_t* C_starts, int64_t c_ndiag, const int64_t* pair_ptr,
     const int32_t* entries, const diagpu_band_info* info, float* C_vals, void* stream);
+
+/* The numeric phase of diagpu_spgemm_numeric_f32 on the matrix cores, for
+ * narrow bands (gemm_diag's contiguous offsets): each 16-row tile of C is the
+ * sum of the dense 16 x 16 x 4 fp32 MFMA blocks (v_mfma_f32_16x16x4_f32) that
+ * intersect the band, each wave staging the operands of its 64-row slabs in
+ * LDS, elements outside the band read as zeros.  Same C to rounding (1e-5 of
+ * each element's term sum), not bit for bit: the sums run in MFMA order.
+ * Operands must be finite (a dense tile multiplies absent terms by zero).
+ * info from diagpu_spgemm_band_prepare with mfma_eligible set (A's offset
+ * range at most 32 wide, A's plus B's at most 48, LDS at most 80 KiB per
+ * workgroup), else DIAGPU_ERR_CAPACITY.  C offsets must be the plan's (sums
+ * of A's and B's).  Never picked by the plan's automatic choice: on
+ * gemm_diag's -10..10 band it issues 2.9 times the useful flops and is
+ * slower than the band kernel.  No reference counterpart: the reference's
+ * tensor-core kernel is the TF32 SpMV, and gemm_diag/gemm_diag.cu:119-329
+ * runs this product on scalar FMAs; this is that product as a dense tile
+ * contraction. */
+DIAGPU_API int diagpu_spgemm_numeric_band_mfma_f32(
+    int32_t n, const int32_t* A_off, const int64_t* A_starts, int32_t nA, const float* A_vals,
+    const int32_t* B_off, const int64_t* B_starts, int32_t nB, const float* B_vals,
+    const int32_t* C_off, const int64_t* C_starts, int64_t c_ndiag,
+    const diagpu_band_info* info, float* C_vals, void* stream);
 
 /* ----------------------------------------------------------------------
  * Medium bands: the numeric phase with A held in LDS

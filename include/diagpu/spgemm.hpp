@@ -392,7 +392,7 @@ private:
     }
     void prepare_band(hipStream_t stream) const
     {
-        entries_.resize(size_t(4 * info_.n_pairs + 4));
+        entries_.resize(size_t(4 * info_.n_pairs + 8));
         check(diagpu_spgemm_band_prepare(n_, A_off_.data(), A_starts_.data(), nA_, B_off_.data(),
                                          B_starts_.data(), nB_, pairs_.data(), info_.n_pairs,
                                          entries_.data(), &band_, stream));

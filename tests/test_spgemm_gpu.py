@@ -635,3 +635,51 @@ def test_wrappers_reject_short_or_strided_operands(dev):
         expm_krylov(R.offsets, Rc, 1000, psi0, 0.1, m=8, out=psi[::2])
     with pytest.raises(ValueError):
         expm_krylov(R.offsets, Rc, 1000, psi0, 0.1, m=8, out=psi0)
+
+
+@pytest.mark.parametrize("n,offs_a,offs_b", [
+    (4096, list(range(-10, 11)), list(range(-10, 11))),       # gemm_diag.cu:467-486 defaults
+    (1 << 17, list(range(-10, 11)), list(range(-10, 11))),
+    (70001, list(range(-12, 13)), list(range(-7, 8))),         # ragged last block
+    (5000, [-10, -3, 0, 5, 9], [-8, -1, 0, 2, 7]),             # offsets with holes
+    (37, [-10, -3, 0, 2, 10], [-9, -1, 0, 5, 7]),              # smaller than one block
+    (300, [0], [0]),                                           # diagonal times diagonal
+    (1, [0], [0]),                                             # a 1 x 1 matrix
+    (3, [-2, -1, 0, 1, 2], [-2, 0, 1]),                        # every diagonal of 3 x 3
+])
+def test_band_mfma_kernel(dev, oracle, n, offs_a, offs_b):
+    """The MFMA band kernel: every C value within 1e-5 of its fp64 term sum
+    (the same bound as the other kernels; not bit-identical: MFMA order), the
+    reference's own 1e-1 (gemm_diag.cu:544) far inside, and the issued-block
+    count matching the tile geometry."""
+    A = workloads.hm_random(n, offs_a, 91, dev)
+    B = workloads.hm_random(n, offs_b, 92, dev)
+    plan = SpgemmPlan(A, B)
+    _, info = plan.band_info()
+    assert info.mfma_eligible and info.mfma_blocks > 0
+    assert (info.b_off_min, info.b_off_max) == (min(offs_b), max(offs_b))
+    Cm = torch.full((plan.info.c_nnz,), float("nan"), device=dev)
+    plan.numeric(A.values, B.values, Cm, kernel="band_mfma")
+    Cg = plan.multiply(A.values, B.values, kernel="gather")
+    c_len, c_st = plan.c_lengths().cpu().numpy(), plan.c_starts().cpu().numpy()
+    ptr, pairs = plan.pair_ptr().cpu().numpy(), plan.pairs_numpy()
+    want, ab = oracle.spgemm_pairs_f64(A.values.cpu().numpy(), B.values.cpu().numpy(), c_len,
+                                       c_st, ptr, pairs, 0, plan.info.c_ndiag)
+    got = Cm.cpu().numpy()
+    assert np.isfinite(got).all()
+    check_values(got, want, ab)
+    assert np.max(np.abs(got - Cg.cpu().numpy())) < 1e-1
+    u = plan.mfma_utilisation()
+    assert 0 < u <= 1
+
+
+def test_band_mfma_refuses_wide_spans(dev):
+    """Offset ranges beyond the MFMA kernel's tiles (config 4's +-16384) are
+    refused with DIAGPU_ERR_CAPACITY before any launch."""
+    A4, B4 = workloads.spgemm_config(4, seed=4, device=dev)
+    p4 = SpgemmPlan(A4, B4)
+    assert not p4.band_info()[1].mfma_eligible and p4.mfma_utilisation() is None
+    Cv = torch.empty(p4.info.c_nnz, device=dev)
+    with pytest.raises(_lib.DiagpuError) as e:
+        p4.numeric(A4.values, B4.values, Cv, kernel="band_mfma")
+    assert e.value.status == _lib.ERR_CAPACITY
