@@ -142,7 +142,7 @@ PROTOTYPES: dict[str, tuple] = {
 }
 
 # diagpu.h: DIAGPU_ASTAT_MAX_A, DIAGPU_SYMBOLIC_SCRATCH_BYTES
-ASTAT_MAX_A = 71
+ASTAT_MAX_A = 142
 SYMBOLIC_SCRATCH_BYTES = 40 << 20
 
 _lib: C.CDLL | None = None

@@ -42,7 +42,8 @@ constexpr int kRB = 256;                  // rows per block
 constexpr int kLead = 32;                 // rows staged before the block
 constexpr int kStage = kRB + kLead;       // staged rows per A diagonal
 constexpr int kWaves = 16;                // waves per workgroup
-constexpr int kMaxA = DIAGPU_ASTAT_MAX_A; // 4 kStage kMaxA <= 80 KiB: two workgroups per CU
+constexpr int kMaxA = DIAGPU_ASTAT_MAX_A; // 4 kStage kMaxA <= 160 KiB
+constexpr int kMaxA2 = 71;               // 4 kStage kMaxA2 <= 80 KiB: two workgroups per CU
 
 // records[g] = {a, lo, hi, b} for plan entry g; flag[0] set if an entry's A
 // start is no A diagonal's start, flag[1] if its B indices do not fit int32.
@@ -251,10 +252,11 @@ DIAGPU_API int diagpu_spgemm_numeric_astat_f32(
                                                  kStage * kMaxA * (int)sizeof(float)), fn);
     if (st) return st;
     const int32_t blocks = (int32_t)ceil_div<int64_t>((int64_t)n + kLead, kRB);
-    // too few blocks to give every CU two workgroups: split each block's C
-    // diagonals over several (at most one per wave's worth of diagonals)
+    // too few blocks to give every CU its workgroups (two, or one above
+    // kMaxA2 A diagonals): split each block's C diagonals over several (at
+    // most one per wave's worth of diagonals)
     int32_t groups = 1;
-    const int64_t fill = 2 * (int64_t)cu_count();
+    const int64_t fill = (nA <= kMaxA2 ? 2 : 1) * (int64_t)cu_count();
     if (blocks < fill)
         groups = (int32_t)std::max<int64_t>(1, std::min<int64_t>(ceil_div<int64_t>(fill, blocks),
                                                                  ceil_div<int64_t>(c_ndiag, kWaves)));

@@ -345,9 +345,10 @@ DIAGPU_API int diagpu_spgemm_numeric_band_mfma_f32(
  * Medium bands: the numeric phase with A held in LDS
  * ---------------------------------------------------------------------- */
 
-/* Largest A diagonal count diagpu_spgemm_numeric_astat_f32 takes (its
- * workgroups hold 288 rows of every A diagonal in LDS, 80 KiB at most). */
-#define DIAGPU_ASTAT_MAX_A 71
+/* Largest A diagonal count diagpu_spgemm_numeric_astat_f32 takes: its
+ * workgroups hold 288 rows of every A diagonal in LDS, 160 KiB at most (up to
+ * 71 diagonals, 80 KiB, two workgroups share a CU; above, one). */
+#define DIAGPU_ASTAT_MAX_A 142
 
 /* For the A-stationary kernel, per plan (once): records[4g .. 4g+3] =
  * {a, lo, hi, b} for plan entry g: a the index of its A diagonal (looked up

@@ -187,12 +187,12 @@ def test_complex_and_krylov_argument_errors():
 
 def test_astat_max_a_matches_header():
     """The Python constant mirrors DIAGPU_ASTAT_MAX_A, and 288 rows of that
-    many A diagonals fit the kernel's 80 KiB of LDS."""
+    many A diagonals fit a workgroup's 160 KiB of LDS."""
     import re
     hdr = (Path(__file__).resolve().parents[1] / "include" / "diagpu.h").read_text()
     m = re.search(r"#define DIAGPU_ASTAT_MAX_A (\d+)", hdr)
     assert m and int(m.group(1)) == _lib.ASTAT_MAX_A
-    assert 288 * _lib.ASTAT_MAX_A * 4 <= 80 * 1024 < 288 * (_lib.ASTAT_MAX_A + 1) * 4
+    assert 288 * _lib.ASTAT_MAX_A * 4 <= 160 * 1024 < 288 * (_lib.ASTAT_MAX_A + 1) * 4
 
 
 def test_symbolic_noalloc_rejects_beyond_scratch():

@@ -209,14 +209,19 @@ def _check_products(plan, Cv, A, B, seed):
 
 
 def test_config5_full_size(dev, oracle):
-    """n = 262144, 128 x 128 random offsets: plan exact; values exact to the
-    bound on a sample of C diagonals; all of C through C v = A (B v) and
-    v^T C = (v^T A) B."""
+    """n = 262144, 128 x 128 random offsets: plan exact; the automatic choice
+    (the A-stationary kernel, 128 A diagonals in LDS) bit-identical to the
+    gather; values exact to the bound on a sample of C diagonals; all of C
+    through C v = A (B v) and v^T C = (v^T A) B."""
     A, B = workloads.spgemm_config(5, seed=5, device=dev)
     plan = SpgemmPlan(A, B)
     c_off, c_len, c_st, nnz, ptr, pairs = check_plan(oracle, plan, A, B)
     assert nnz > 2**31                       # int64 starts are required
+    assert plan.kernel_for() == "astat"
     Cv = plan.multiply(A.values, B.values)
+    Cg = plan.multiply(A.values, B.values, kernel="gather")
+    assert torch.equal(Cv.view(torch.int32), Cg.view(torch.int32))
+    del Cg
     torch.cuda.synchronize()
     Av, Bv = A.values.cpu().numpy(), B.values.cpu().numpy()
     rng = np.random.default_rng(0)
