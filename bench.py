@@ -48,7 +48,7 @@ def parse_args(argv=None):
                     help="profiling aid: run just one workload (spmv2, spmv2d, spmv2c, "
                          "spmv2rc, spmv1, spmv3, spgemm1..spgemm3 (the squares of the SpMV "
                          "configs' matrices), spgemm4, spgemm5, spgemm4c, spgemm5c, taylor, krylov, "
-                         "propagator, propagator2d, gemmdiag, gemmdiag20, copy) "
+                         "propagator, propagator2d, gemmdiag, gemmdiag20, copy, fill20) "
                          "and print its line")
     return ap.parse_args(argv)
 
@@ -564,6 +564,26 @@ def copy_calibration(steps: int):
             "GBs": 2 * nbytes / (ms * 1e6)}
 
 
+def fill_calibration(steps: int, nbytes: int = 20_000_000_000):
+    """A plain device fill of known size (torch's vectorized fill kernel), for
+    checking the WRITE_SIZE counter at the size of a large C (the square of
+    config 3 writes 20.0 GB)."""
+    import torch
+    buf = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda")
+    for _ in range(2):
+        buf.fill_(1.0)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        buf.fill_(1.0)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    return {"workload": f"fill_{nbytes}", "bytes_written": nbytes, "ms": ms,
+            "GBs": nbytes / (ms * 1e6)}
+
+
 # --------------------------------------------------------------------------
 
 def main(argv=None) -> int:
@@ -583,6 +603,8 @@ def main(argv=None) -> int:
         w = args.only
         if w == "copy":
             print(json.dumps(copy_calibration(args.steps)), flush=True)
+        elif w == "fill20":
+            print(json.dumps(fill_calibration(args.steps)), flush=True)
         elif w.startswith("spmv"):
             cfg = int(w[4])
             suffix = w[5:]
