@@ -19,6 +19,7 @@ from __future__ import annotations
 import time
 from dataclasses import dataclass, field
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -38,12 +39,28 @@ def hm_structure(n: int, offsets, device, dtype=torch.float32) -> HM:
     return HM(n, torch.tensor(offs, dtype=torch.int32, device=device),
               torch.tensor(lens, dtype=torch.int32, device=device),
               torch.tensor(starts, dtype=torch.int64, device=device),
-              torch.empty(max(1, int(sum(lens))), dtype=dtype, device=device)[: int(sum(lens))])
+              torch.empty(max(1, int(sum(lens))), dtype=dtype, device=device)[: int(sum(lens))],
+              offs)
 
 
 def identity(n: int, device, dtype=torch.float32) -> HM:
     I = hm_structure(n, [0], device, dtype)
     I.values.fill_(1.0)
+    return I
+
+
+# Identities the chain reads (never writes), one per (n, device, dtype): a
+# Taylor step adds I without building it again.
+_UNITS: dict = {}
+
+
+def _unit(n: int, device, dtype) -> HM:
+    key = (n, str(torch.device(device)), dtype)
+    I = _UNITS.get(key)
+    if I is None:
+        if len(_UNITS) >= 8:
+            _UNITS.clear()
+        I = _UNITS[key] = identity(n, device, dtype)
     return I
 
 
@@ -57,7 +74,7 @@ def as_complex(M: HM, stream=None) -> HM:
         out = torch.empty(M.values.numel(), dtype=torch.complex64, device=M.values.device)
         _lib.call("diagpu_promote_f32_c64", M.values.numel(), M.values.data_ptr(),
                   out.data_ptr(), _stream_handle(stream))
-    return HM(M.n, M.offsets, M.lengths, M.starts, out)
+    return HM(M.n, M.offsets, M.lengths, M.starts, out, M.host_offsets)
 
 
 def _c64(z) -> "_lib.Complex64":
@@ -66,7 +83,18 @@ def _c64(z) -> "_lib.Complex64":
 
 
 def _host_offsets(M: HM) -> list[int]:
-    return M.offsets.cpu().tolist()
+    """M's offsets on the host: the copy M carries, else read from the device
+    (a stream sync) and kept on M."""
+    if M.host_offsets is None:
+        M.host_offsets = M.offsets.cpu().tolist()
+    return M.host_offsets
+
+
+def _sumset(n: int, a: list[int], b: list[int]) -> list[int]:
+    """The C offsets of A * B as the symbolic phase builds them: every sum
+    da + db with |da + db| < n, ascending, once each."""
+    s = np.unique(np.add.outer(np.asarray(a, dtype=np.int64), np.asarray(b, dtype=np.int64)))
+    return s[(s > -n) & (s < n)].tolist()
 
 
 def axpby(alpha, X: HM, beta, Y: HM | None, stream=None) -> HM:
@@ -92,7 +120,12 @@ def _axpby(alpha, X: HM, beta, Y: HM | None, stream) -> HM:
     for offs, nm in ((ox, "X"), (oy, "Y")):
         if any(b <= a for a, b in zip(offs, offs[1:])):
             raise ValueError(f"{nm} offsets must be ascending and distinct")
-    Z = hm_structure(X.n, sorted(set(ox) | set(oy)), X.values.device, dt)
+    if Y is None or oy == ox:
+        # Z has X's diagonals: X's structure tensors, new values
+        Z = HM(X.n, X.offsets, X.lengths, X.starts,
+               torch.empty(X.values.numel(), dtype=dt, device=X.values.device), ox)
+    else:
+        Z = hm_structure(X.n, sorted(set(ox) | set(oy)), X.values.device, dt)
     for M, nm in ((X, "X"), (Y, "Y")):
         if M is not None:
             _check_dev(M.values, dt, f"{nm}.values")
@@ -142,9 +175,13 @@ def multiply(A: HM, B: HM, stats: ChainStats | None = None) -> HM:
     t0 = time.perf_counter()
     plan = SpgemmPlan(A, B)
     inf = plan.info
-    # C's structure arrays are views of the plan's buffer (kept alive by them)
+    # C's structure arrays are views of the plan's buffer (kept alive by
+    # them); its host offsets follow from the operands' where both are known
+    c_host = (_sumset(A.n, A.host_offsets, B.host_offsets)
+              if A.host_offsets is not None and B.host_offsets is not None else None)
     C = HM(A.n, plan.c_offsets(), plan.c_lengths(), plan.c_starts(),
-           torch.empty(max(1, inf.c_nnz), dtype=A.values.dtype, device=A.values.device)[: inf.c_nnz])
+           torch.empty(max(1, inf.c_nnz), dtype=A.values.dtype, device=A.values.device)[: inf.c_nnz],
+           c_host)
     if stats is not None:
         torch.cuda.synchronize()
     t1 = time.perf_counter()
@@ -180,10 +217,10 @@ def add_identity(S: HM, sigma=1.0, stream=None) -> HM:
 def _add_identity(S: HM, sigma, stream) -> HM:
     offs = _host_offsets(S)
     dt = S.values.dtype
+    I = _unit(S.n, S.values.device, dt)
     if 0 not in offs:
-        return axpby(1.0, S, sigma, identity(S.n, S.values.device, dt), stream)
+        return axpby(1.0, S, sigma, I, stream)
     i = offs.index(0)
-    I = identity(S.n, S.values.device, dt)
     o4, s8 = S.offsets.element_size(), S.starts.element_size()
     if dt == torch.complex64:
         one, sg, name = _c64(1.0), _c64(sigma), "diagpu_dia_axpby_c64"
@@ -217,7 +254,8 @@ def taylor_expm(H: HM, t, order: int, stats: ChainStats | None = None) -> HM:
     if order == 0:
         return identity(H.n, dev, H.values.dtype)
     ax = stats.axpby if stats else None
-    S = _timed(ax, axpby, t / order, H, 1.0, identity(H.n, dev, H.values.dtype))
+    _host_offsets(H)                             # once: every product's offsets follow
+    S = _timed(ax, axpby, t / order, H, 1.0, _unit(H.n, dev, H.values.dtype))
     for j in range(order - 1, 0, -1):
         Hj = _timed(ax, axpby, t / j, H, 0.0, None)
         S = multiply(S, Hj, stats)

@@ -8,7 +8,7 @@ int64 starts).
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import numpy as np
 import torch
@@ -120,6 +120,9 @@ class HM:
     lengths: torch.Tensor      # int32 [D] = n - |d|
     starts: torch.Tensor       # int64 [D]
     values: torch.Tensor       # float32 [sum lengths]
+    # a host copy of `offsets` where the builder knew it (None: not known;
+    # read it from the device when needed)
+    host_offsets: list | None = field(default=None, compare=False, repr=False)
 
     @property
     def ndiag(self) -> int:
@@ -141,7 +144,7 @@ def hm_from_values(n: int, offsets, values: torch.Tensor, device="cuda") -> HM:
     offs, lens, starts = hm_layout(n, offsets)
     return HM(n, torch.tensor(offs, dtype=torch.int32, device=device),
               torch.tensor(lens, dtype=torch.int32, device=device),
-              torch.tensor(starts, dtype=torch.int64, device=device), values)
+              torch.tensor(starts, dtype=torch.int64, device=device), values, offs)
 
 
 def hm_random(n: int, offsets, seed: int, device="cuda") -> HM:

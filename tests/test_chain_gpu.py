@@ -18,7 +18,7 @@ import scipy.linalg
 import torch
 
 from diagpu_amd import chain
-from diagpu_amd.workloads import hm_random, hm_stencil7
+from diagpu_amd.workloads import HM, hm_random, hm_stencil7
 from hm_host import dense_of, matvec64
 
 pytestmark = pytest.mark.gpu
@@ -55,7 +55,8 @@ def test_axpby_zero_factor_does_not_read(dev):
 def test_axpby_rejects_unsorted(dev):
     n = 50
     X = hm_random(n, [0, 1], 5, dev)
-    X.offsets = torch.tensor([1, 0], dtype=torch.int32, device=dev)
+    # the same values under descending offsets (no host copy of them)
+    X = HM(n, torch.tensor([1, 0], dtype=torch.int32, device=dev), X.lengths, X.starts, X.values)
     with pytest.raises(ValueError):
         chain.axpby(1.0, X, 1.0, None)
 
@@ -102,6 +103,20 @@ def test_taylor_against_expm(dev, n, offs, t, order):
         frontier = _sumset(frontier, offs, n)
         reach |= set(frontier)
     assert S.offsets.cpu().tolist() == sorted(reach)
+
+
+def test_host_offsets_follow_the_device(dev):
+    """The host copies of the offsets that products and sums carry (so the
+    chain needs no device read-back per step) equal the device offsets: the
+    sumset for products, sums past n dropped, and the union for axpby."""
+    n = 40
+    A = hm_random(n, [-39, -7, 0, 3, 30], 14, dev)
+    B = hm_random(n, [-20, -1, 0, 9, 39], 15, dev)
+    for M in (chain.multiply(A, B), chain.multiply(B, A), chain.power(A, 3),
+              chain.axpby(1.0, A, 2.0, B), chain.axpby(3.0, A, 0.0, None),
+              chain.taylor_expm(B, 0.1, 3), chain.taylor_expm(A, 0.2j, 2)):
+        assert M.host_offsets is not None
+        assert M.host_offsets == M.offsets.cpu().tolist()
 
 
 def test_add_identity_in_place_and_union(dev):
