@@ -197,13 +197,24 @@ def multiply(A: HM, B: HM, stats: ChainStats | None = None) -> HM:
     return C
 
 
+def _narrow_first(X: HM) -> bool:
+    """Whether a chain step multiplies the narrow factor from the left: for
+    real values it is then the A operand, whose few diagonals the
+    A-stationary kernel holds in LDS (the 7-point stencil's Taylor steps:
+    (H/4) * S_5, 377 C diagonals, 0.97 ms against 1.24 for S_5 * (H/4) on the
+    gather); for complex values the gather takes the product either way and
+    is faster with the wide factor on the left."""
+    return X.values.dtype == torch.float32
+
+
 def power(H: HM, k: int, stats: ChainStats | None = None) -> HM:
-    """H^k (k >= 1) by the chain P_j = P_{j-1} * H."""
+    """H^k (k >= 1) by the chain P_j = H * P_{j-1} (P_{j-1} * H for complex
+    values; the factors commute)."""
     if k < 1:
         raise ValueError("k must be >= 1")
     P = H
     for _ in range(k - 1):
-        P = multiply(P, H, stats)
+        P = multiply(H, P, stats) if _narrow_first(H) else multiply(P, H, stats)
     return P
 
 
@@ -241,11 +252,11 @@ def taylor_expm(H: HM, t, order: int, stats: ChainStats | None = None) -> HM:
 
         S_order = I + (t/order) H,   S_j = I + S_{j+1} * ((t/j) H),   S = S_1,
 
-    so each step is one device-planned SpGEMM, the wide S_{j+1} times the
-    narrow (t/j) H (S_{j+1} is a polynomial in H, so the two commute; this
-    order is the faster one for the numeric kernel), and an in-place add of I
-    to the product's main diagonal (a full union pass only when the product
-    lacks that diagonal)."""
+    so each step is one device-planned SpGEMM of the wide S_{j+1} and the
+    narrow (t/j) H (S_{j+1} is a polynomial in H, so the two commute; the
+    narrow factor goes first for real values, last for complex ones, the
+    faster order of each), and an in-place add of I to the product's main
+    diagonal (a full union pass only when the product lacks that diagonal)."""
     if order < 0:
         raise ValueError("order must be >= 0")
     dev = H.values.device
@@ -258,7 +269,7 @@ def taylor_expm(H: HM, t, order: int, stats: ChainStats | None = None) -> HM:
     S = _timed(ax, axpby, t / order, H, 1.0, _unit(H.n, dev, H.values.dtype))
     for j in range(order - 1, 0, -1):
         Hj = _timed(ax, axpby, t / j, H, 0.0, None)
-        S = multiply(S, Hj, stats)
+        S = multiply(Hj, S, stats) if _narrow_first(Hj) else multiply(S, Hj, stats)
         S = _timed(ax, add_identity, S)
     return S
 
