@@ -267,10 +267,54 @@ def taylor_expm(H: HM, t, order: int, stats: ChainStats | None = None) -> HM:
     ax = stats.axpby if stats else None
     _host_offsets(H)                             # once: every product's offsets follow
     S = _timed(ax, axpby, t / order, H, 1.0, _unit(H.n, dev, H.values.dtype))
+    if stats is None:
+        return _taylor_steps(H, t, order, S)
     for j in range(order - 1, 0, -1):
         Hj = _timed(ax, axpby, t / j, H, 0.0, None)
         S = multiply(Hj, S, stats) if _narrow_first(Hj) else multiply(S, Hj, stats)
         S = _timed(ax, add_identity, S)
+    return S
+
+
+# A stream per device for building plans beside the products (default
+# priority, like every stream here).
+_SIDE: dict = {}
+
+
+def _side_stream(device) -> torch.cuda.Stream:
+    key = str(torch.device(device))
+    st = _SIDE.get(key)
+    if st is None:
+        st = _SIDE[key] = torch.cuda.Stream(device=device)
+    return st
+
+
+def _taylor_steps(H: HM, t, order: int, S: HM) -> HM:
+    """The Horner steps of taylor_expm with each product's plan built on a
+    side stream while the previous product runs: a plan needs only its
+    operands' structure (the previous plan's C arrays, complete once its
+    symbolic phase has returned), so its one stream sync waits for its own
+    symbolic phase, not for the product queued before it.  Products,
+    scalings and identity adds stay on the caller's stream, in order."""
+    main = torch.cuda.current_stream(H.values.device)
+    side = _side_stream(H.values.device)
+    side.wait_stream(main)                      # S's structure, H's values
+    for j in range(order - 1, 0, -1):
+        Hj = axpby(t / j, H, 0.0, None)
+        A, B = (Hj, S) if _narrow_first(Hj) else (S, Hj)
+        with torch.cuda.stream(side):
+            plan = SpgemmPlan(A, B, stream=side)
+            plan.prepare(A.values.dtype)
+        plan.hand_over(main)
+        inf = plan.info
+        C = HM(A.n, plan.c_offsets(), plan.c_lengths(), plan.c_starts(),
+               torch.empty(max(1, inf.c_nnz), dtype=A.values.dtype, device=A.values.device)[: inf.c_nnz],
+               _sumset(A.n, _host_offsets(A), _host_offsets(B)))
+        if inf.c_ndiag:
+            plan.numeric(A.values, B.values, C.values)
+        S = add_identity(C)
+        if S.offsets is not C.offsets:
+            side.wait_stream(main)              # a new structure, written on main
     return S
 
 

@@ -26,6 +26,12 @@ def _check_dev(t: torch.Tensor, dtype, name: str):
         raise TypeError(f"{name} must be a contiguous {dtype} device tensor")
 
 
+# The band kernel's row block and LDS budget (spgemm_band.hip: kRB,
+# kLdsBudget), for telling on the host that a plan cannot fit.
+BAND_ROWS = 256
+BAND_LDS_BUDGET = 64 * 1024
+
+
 class SpgemmPlan:
     """C = A * B for HM operands (objects with n, offsets, lengths, starts,
     int32/int32/int64 device tensors).  Builds the C structure and pair plan
@@ -55,7 +61,7 @@ class SpgemmPlan:
             parts.append(("lookup", torch.int32, 2 * self.n - 1))
         esz = {torch.uint8: 1, torch.int32: 4, torch.int64: 8}
         sizes = [-(-cnt * esz[dt] // 256) * 256 for _, dt, cnt in parts]
-        buf = torch.empty(sum(sizes), dtype=torch.uint8, device=dev)
+        buf = self._buf = torch.empty(sum(sizes), dtype=torch.uint8, device=dev)
         o = 0
         for (name, dt, cnt), sz in zip(parts, sizes):
             setattr(self, name, buf[o: o + cnt * esz[dt]].view(dt))
@@ -99,6 +105,27 @@ class SpgemmPlan:
         raw = self.pairs[: self.info.n_pairs * GPAIR_BYTES].cpu().numpy()
         return raw.view(GPAIR_DTYPE)
 
+    # streams -----------------------------------------------------------------
+    def prepare(self, dtype=torch.float32) -> str:
+        """Runs now, on the plan's stream, the per-plan set-up of the kernel
+        `numeric` takes by default for `dtype` (band or A-stationary
+        prepare, each one stream sync), and returns that kernel's name."""
+        return self.kernel_for(dtype)
+
+    def hand_over(self, stream) -> None:
+        """Continue the plan on `stream` (a torch stream): its buffers are
+        marked in use there, so torch's allocator keeps them until the work
+        queued on `stream` when they are freed has completed, and later
+        launches (numeric, set-up) go there."""
+        bufs = [self._buf]
+        if self._band is not None:
+            bufs.append(self._band[0])
+        if self._astat is not None and self._astat is not False:
+            bufs.append(self._astat)
+        for t in bufs:
+            t.record_stream(stream)
+        self.stream = stream
+
     # numeric ---------------------------------------------------------------
     def band_info(self):
         """(entries, BandInfo) of diagpu_spgemm_band_prepare for this plan
@@ -127,7 +154,22 @@ class SpgemmPlan:
         if (dtype != torch.float32 or self.info.c_ndiag == 0 or na > 65535 or nb > 32767
                 or self.info.n_pairs < 3 * self.info.c_ndiag or self.n < 512 * 256):
             return False
+        est = self.band_lds_estimate()
+        if est is not None and est > BAND_LDS_BUDGET:
+            return False                          # known without the prepare step's sync
         return bool(self.band_info()[1].eligible)
+
+    def band_lds_estimate(self) -> int | None:
+        """The band kernel's LDS bytes per workgroup for this plan, as
+        diagpu_spgemm_band_prepare reports them (4 (nA 256 + nB wb) +
+        16 n_pairs, wb = 256 + A's offset span rounded up to a multiple of
+        4), from A's host offsets when A carries them; else None."""
+        ho = getattr(self.A, "host_offsets", None)
+        if not ho:
+            return None
+        span = max(ho) - min(ho)
+        wb = (BAND_ROWS + span + 3) & ~3
+        return 4 * (len(ho) * BAND_ROWS + self.B.offsets.numel() * wb) + 16 * self.info.n_pairs
 
     def astat_records(self) -> torch.Tensor:
         """Records of diagpu_spgemm_astat_prepare for this plan (computed

@@ -642,6 +642,20 @@ def test_wrappers_reject_short_or_strided_operands(dev):
         expm_krylov(R.offsets, Rc, 1000, psi0, 0.1, m=8, out=psi0)
 
 
+def test_band_lds_estimate_matches_prepare(dev):
+    """The host's estimate of the band kernel's LDS footprint (used to skip
+    the prepare step's sync for plans that cannot fit) equals what
+    diagpu_spgemm_band_prepare reports, on narrow and wide operands."""
+    for n, oa, ob in ((1 << 17, list(range(-10, 11)), list(range(-10, 11))),
+                      (5000, [-300, -3, 0, 7, 250], [-1, 0, 1]),
+                      (70001, list(range(-12, 13)), [-65000, -3, 0, 4, 65000])):
+        A = workloads.hm_random(n, oa, 41, dev)
+        B = workloads.hm_random(n, ob, 42, dev)
+        plan = SpgemmPlan(A, B)
+        assert A.host_offsets == sorted(oa)
+        assert plan.band_lds_estimate() == plan.band_info()[1].lds_bytes
+
+
 @pytest.mark.parametrize("n,offs_a,offs_b", [
     (4096, list(range(-10, 11)), list(range(-10, 11))),       # gemm_diag.cu:467-486 defaults
     (1 << 17, list(range(-10, 11)), list(range(-10, 11))),
