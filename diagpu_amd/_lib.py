@@ -139,10 +139,13 @@ PROTOTYPES: dict[str, tuple] = {
     "diagpu_spgemm_astat_prepare": (C.c_int, [_i32, _vp, _i32, _vp, _i64, _vp, _vp]),
     "diagpu_spgemm_numeric_astat_f32": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp,
                                                   _i64, _vp, _vp, _i64, _vp, _vp]),
+    "diagpu_spgemm_numeric_astat_c64": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp,
+                                                  _i64, _vp, _vp, _i64, _vp, _vp]),
 }
 
-# diagpu.h: DIAGPU_ASTAT_MAX_A, DIAGPU_SYMBOLIC_SCRATCH_BYTES
+# diagpu.h: DIAGPU_ASTAT_MAX_A, DIAGPU_ASTAT_MAX_A_C64, DIAGPU_SYMBOLIC_SCRATCH_BYTES
 ASTAT_MAX_A = 142
+ASTAT_MAX_A_C64 = 75
 SYMBOLIC_SCRATCH_BYTES = 40 << 20
 
 _lib: C.CDLL | None = None

@@ -34,16 +34,26 @@
 #include <climits>
 
 #include "common.hpp"
+#include "elem.hpp"
 
 namespace diagpu {
 namespace {
 
 constexpr int kRB = 256;                  // rows per block
-constexpr int kLead = 32;                 // rows staged before the block
-constexpr int kStage = kRB + kLead;       // staged rows per A diagonal
 constexpr int kWaves = 16;                // waves per workgroup
-constexpr int kMaxA = DIAGPU_ASTAT_MAX_A; // 4 kStage kMaxA <= 160 KiB
-constexpr int kMaxA2 = 71;               // 4 kStage kMaxA2 <= 80 KiB: two workgroups per CU
+
+// Per element type T (fp32 or complex fp32): kLead rows staged before the
+// block (one 128-byte line of C), kStage staged rows per A diagonal, kMax A
+// diagonals in 160 KiB of LDS and kMax2 in 80 KiB (two workgroups per CU).
+template <typename T> struct Astat {
+    static constexpr int kLead = (int)(128 / sizeof(T));
+    static constexpr int kStage = kRB + kLead;
+    static constexpr int kWords = (int)(sizeof(T) / 4);   // dwords per element
+    static constexpr int kMax = (160 * 1024) / (kStage * (int)sizeof(T));
+    static constexpr int kMax2 = (80 * 1024) / (kStage * (int)sizeof(T));
+};
+static_assert(Astat<float>::kMax == DIAGPU_ASTAT_MAX_A, "fp32 A diagonals in 160 KiB of LDS");
+static_assert(Astat<cf32>::kMax == DIAGPU_ASTAT_MAX_A_C64, "complex A diagonals in 160 KiB of LDS");
 
 // records[g] = {a, lo, hi, b} for plan entry g; flag[0] set if an entry's A
 // start is no A diagonal's start, flag[1] if its B indices do not fit int32.
@@ -90,14 +100,31 @@ __global__ __launch_bounds__(64) void k_astat_clear(int32_t* __restrict__ flag)
     if (threadIdx.x < 4) flag[threadIdx.x] = 0;
 }
 
+// Keeps a value in registers at this point: the compiler cannot sink its
+// load into a branch past it.
+__device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(cf32& v) { asm volatile("" : "+v"(v.re), "+v"(v.im)); }
+
+template <typename T>
+__device__ __forceinline__ void store_elem_nt(T* p, T v)
+{
+    typedef typename ElemRaw<T>::type Raw;
+    Raw r;
+    __builtin_memcpy(&r, &v, sizeof(T));
+    __builtin_nontemporal_store(r, reinterpret_cast<Raw*>(p));
+}
+
+template <typename T>
 __global__ __launch_bounds__(64 * kWaves) void k_astat(
     int32_t n, const int32_t* __restrict__ A_off, const int64_t* __restrict__ A_starts, int32_t nA,
-    const float* __restrict__ Av, const float* __restrict__ Bv, const int32_t* __restrict__ C_off,
+    const T* __restrict__ Av, const T* __restrict__ Bv, const int32_t* __restrict__ C_off,
     const int32_t* __restrict__ C_len, const int64_t* __restrict__ C_starts, int32_t nC,
     const int64_t* __restrict__ pair_ptr, const int4* __restrict__ records,
-    float* __restrict__ Cv, int32_t blocks, int32_t groups, int32_t per_xcd)
+    T* __restrict__ Cv, int32_t blocks, int32_t groups, int32_t per_xcd)
 {
-    extern __shared__ float A_l[];   // [nA][kStage]: rows i0 - kLead .. i0 + kRB - 1
+    constexpr int kLead = Astat<T>::kLead, kStage = Astat<T>::kStage, kWords = Astat<T>::kWords;
+    extern __shared__ float A_l[];   // [nA][kStage] elements: rows i0 - kLead .. i0 + kRB - 1
+    const T* A_t = reinterpret_cast<const T*>(A_l);
     // workgroup b on XCD b mod 8: each XCD owns a contiguous range of work
     // units, so neighbouring blocks (whose B windows overlap) share its L2.
     // Unit = (block, group): a block's C diagonals are split over `groups`
@@ -110,19 +137,22 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
     const int wave = __builtin_amdgcn_readfirstlane(r >> 6), lane = r & 63;
     const int i0 = blk * kRB;                       // n <= 2^30: rows fit int32
 
-    // Stage A: one wave-instruction per 64 rows of a diagonal, each lane's
-    // HM position clamped into the diagonal (the address is always valid; a
-    // staged element that does not exist is never used: its terms are
-    // outside [lo, hi)).
+    // Stage A: one wave-instruction per 64 dwords of a diagonal's window
+    // (kWords dwords per element), each lane's HM position clamped into the
+    // diagonal (the address is always valid; a staged element that does not
+    // exist is never used: its terms are outside [lo, hi)).
+    const float* Aw = reinterpret_cast<const float*>(Av);
     for (int d = wave; d < nA; d += kWaves) {
         const int o = A_off[d];
         const int64_t st = A_starts[d];
         const int len = n - (o < 0 ? -o : o);
-        for (int q0 = 0; q0 < kStage; q0 += 64) {
-            if (q0 + lane < kStage) {
-                const int w = i0 - kLead + q0 + lane;
+        for (int q0 = 0; q0 < kStage * kWords; q0 += 64) {
+            const int f = q0 + lane;                // dword of the window
+            if (f < kStage * kWords) {
+                const int w = i0 - kLead + f / kWords;
                 const int pos = min(max(w + (o < 0 ? o : 0), 0), len - 1);
-                __builtin_amdgcn_global_load_lds(Av + st + pos, A_l + d * kStage + q0, 4, 0, 0);
+                __builtin_amdgcn_global_load_lds(Aw + (st + pos) * kWords + f % kWords,
+                                                 A_l + d * kStage * kWords + q0, 4, 0, 0);
             }
         }
     }
@@ -134,27 +164,28 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
         const int len = C_len[kc];
         const int64_t cst = C_starts[kc];
         const int mc = dc < 0 ? dc : 0;
-        const int s = (int)((cst + mc) & 31);       // C(i0 - s, ...) starts a line
+        const int s = (int)((cst + mc) & (kLead - 1));   // C(i0 - s, ...) starts a line
         const int g0 = (int)pair_ptr[kc], g1 = (int)pair_ptr[kc + 1];
         const int pb = i0 - s + lane + mc;          // C position of the lane's first row
         const int ab = kLead - s + lane;            // its staged A row
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        T acc[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = zero_of<T>();
         // one term: B by a clamped (always valid) load, A from LDS, the
         // multiply-add kept where both operands hold the element
-        auto term = [&](const int4& e, int hi, int j, float& b, float& a, bool& ok) {
+        auto term = [&](const int4& e, int hi, int j, T& b, T& a, bool& ok) {
             const int p = pb + 64 * j;
             ok = p >= e.y && p < hi;
-            b = Bv[(int64_t)e.w + min(max(p, e.y), e.z - 1)];
-            a = A_l[e.x * kStage + ab + 64 * j];
+            b = load_elem<T, false>(Bv + (int64_t)e.w + min(max(p, e.y), e.z - 1));
+            a = A_t[e.x * kStage + ab + 64 * j];
         };
-        // Taken once every load of a batch is issued: the values pass through
-        // an empty asm, so the compiler cannot turn a masked multiply-add into
-        // a branch around its own load (each such branch ends in a full
-        // vmcnt(0) drain: gfx9 counts loads in order).
-        auto pin = [](float& b, float& a) { asm volatile("" : "+v"(b), "+v"(a)); };
+        // The values of a batch are pinned once all its loads are issued, so
+        // the compiler cannot turn a masked multiply-add into a branch around
+        // its own load (each such branch ends in a full vmcnt(0) drain: gfx9
+        // counts loads in order).
         int g = g0;
         for (; g + 2 <= g1; g += 2) {               // two entries' loads in flight
-            float bv[2][4], av[2][4];
+            T bv[2][4], av[2][4];
             bool ok[2][4];
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
@@ -166,32 +197,74 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
 #pragma unroll
             for (int u = 0; u < 2; ++u)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) pin(bv[u][j], av[u][j]);
+                for (int j = 0; j < 4; ++j) { pin(bv[u][j]); pin(av[u][j]); }
 #pragma unroll
             for (int u = 0; u < 2; ++u)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    acc[j] = ok[u][j] ? __builtin_fmaf(av[u][j], bv[u][j], acc[j]) : acc[j];
+                    acc[j] = sel(ok[u][j], mad(acc[j], av[u][j], bv[u][j]), acc[j]);
         }
         if (g < g1) {
             const int4 e = records[g];
             const int hi = min(e.z, len);
-            float bv[4], av[4];
+            T bv[4], av[4];
             bool ok[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) term(e, hi, j, bv[j], av[j], ok[j]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) pin(bv[j], av[j]);
+            for (int j = 0; j < 4; ++j) { pin(bv[j]); pin(av[j]); }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[j] = ok[j] ? __builtin_fmaf(av[j], bv[j], acc[j]) : acc[j];
+            for (int j = 0; j < 4; ++j) acc[j] = sel(ok[j], mad(acc[j], av[j], bv[j]), acc[j]);
         }
-        float* __restrict__ cp = Cv + cst;
+        T* __restrict__ cp = Cv + cst;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int p = pb + 64 * j;
-            if (p >= 0 && p < len) __builtin_nontemporal_store(acc[j], cp + p);
+            if (p >= 0 && p < len) store_elem_nt(cp + p, acc[j]);
         }
     }
+}
+
+template <typename T>
+int launch_astat(const char* fn, int32_t n, const int32_t* A_off, const int64_t* A_starts,
+                 int32_t nA, const T* A_vals, const T* B_vals, const int32_t* C_off,
+                 const int32_t* C_len, const int64_t* C_starts, int64_t c_ndiag,
+                 const int64_t* pair_ptr, const int32_t* records, int64_t n_pairs, T* C_vals,
+                 void* stream)
+{
+    constexpr int kLead = Astat<T>::kLead, kStage = Astat<T>::kStage;
+    constexpr int kMax = Astat<T>::kMax, kMax2 = Astat<T>::kMax2;
+    if (n < 1 || n > (1 << 30) || nA < 1 || c_ndiag < 0 || c_ndiag > 2 * (int64_t)n - 1 ||
+        n_pairs < 0 || n_pairs > INT_MAX)
+        return fail(DIAGPU_ERR_ARG, "%s: bad sizes (n=%d nA=%d c_ndiag=%lld n_pairs=%lld)", fn,
+                    n, nA, (long long)c_ndiag, (long long)n_pairs);
+    if (nA > kMax)
+        return fail(DIAGPU_ERR_CAPACITY, "%s: %d A diagonals, at most %d fit in LDS", fn, nA, kMax);
+    if (c_ndiag == 0) return DIAGPU_OK;
+    if (!A_off || !A_starts || !A_vals || !B_vals || !C_off || !C_len || !C_starts || !pair_ptr ||
+        !records || !C_vals)
+        return fail(DIAGPU_ERR_ARG, "%s: a pointer is NULL", fn);
+    const size_t lds = (size_t)nA * kStage * sizeof(T);
+    // more than 64 KiB of dynamic LDS must be allowed explicitly
+    const int st = check_hip(hipFuncSetAttribute((const void*)k_astat<T>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 kStage * kMax * (int)sizeof(T)), fn);
+    if (st) return st;
+    const int32_t blocks = (int32_t)ceil_div<int64_t>((int64_t)n + kLead, kRB);
+    // too few blocks to give every CU its workgroups (two, or one above
+    // kMax2 A diagonals): split each block's C diagonals over several (at
+    // most one per wave's worth of diagonals)
+    int32_t groups = 1;
+    const int64_t fill = (nA <= kMax2 ? 2 : 1) * (int64_t)cu_count();
+    if (blocks < fill)
+        groups = (int32_t)std::max<int64_t>(1, std::min<int64_t>(ceil_div<int64_t>(fill, blocks),
+                                                                 ceil_div<int64_t>(c_ndiag, kWaves)));
+    const int32_t per_xcd = (int32_t)ceil_div<int64_t>((int64_t)blocks * groups, kNumXcd);
+    hipLaunchKernelGGL(k_astat<T>, dim3((unsigned)(per_xcd * kNumXcd)), dim3(64 * kWaves), lds,
+                       as_stream(stream), n, A_off, A_starts, nA, A_vals, B_vals, C_off, C_len,
+                       C_starts, (int32_t)c_ndiag, pair_ptr,
+                       reinterpret_cast<const int4*>(records), C_vals, blocks, groups, per_xcd);
+    return check_launch(fn);
 }
 
 }  // namespace
@@ -233,39 +306,23 @@ DIAGPU_API int diagpu_spgemm_numeric_astat_f32(
     int64_t c_ndiag, const int64_t* pair_ptr, const int32_t* records, int64_t n_pairs,
     float* C_vals, void* stream)
 {
-    using namespace diagpu;
-    const char* fn = "diagpu_spgemm_numeric_astat_f32";
-    if (n < 1 || n > (1 << 30) || nA < 1 || c_ndiag < 0 || c_ndiag > 2 * (int64_t)n - 1 ||
-        n_pairs < 0 || n_pairs > INT_MAX)
-        return fail(DIAGPU_ERR_ARG, "%s: bad sizes (n=%d nA=%d c_ndiag=%lld n_pairs=%lld)", fn,
-                    n, nA, (long long)c_ndiag, (long long)n_pairs);
-    if (nA > kMaxA)
-        return fail(DIAGPU_ERR_CAPACITY, "%s: %d A diagonals, at most %d fit in LDS", fn, nA, kMaxA);
-    if (c_ndiag == 0) return DIAGPU_OK;
-    if (!A_off || !A_starts || !A_vals || !B_vals || !C_off || !C_len || !C_starts || !pair_ptr ||
-        !records || !C_vals)
-        return fail(DIAGPU_ERR_ARG, "%s: a pointer is NULL", fn);
-    const size_t lds = (size_t)nA * kStage * sizeof(float);
-    // more than 64 KiB of dynamic LDS must be allowed explicitly
-    const int st = check_hip(hipFuncSetAttribute((const void*)k_astat,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 kStage * kMaxA * (int)sizeof(float)), fn);
-    if (st) return st;
-    const int32_t blocks = (int32_t)ceil_div<int64_t>((int64_t)n + kLead, kRB);
-    // too few blocks to give every CU its workgroups (two, or one above
-    // kMaxA2 A diagonals): split each block's C diagonals over several (at
-    // most one per wave's worth of diagonals)
-    int32_t groups = 1;
-    const int64_t fill = (nA <= kMaxA2 ? 2 : 1) * (int64_t)cu_count();
-    if (blocks < fill)
-        groups = (int32_t)std::max<int64_t>(1, std::min<int64_t>(ceil_div<int64_t>(fill, blocks),
-                                                                 ceil_div<int64_t>(c_ndiag, kWaves)));
-    const int32_t per_xcd = (int32_t)ceil_div<int64_t>((int64_t)blocks * groups, kNumXcd);
-    hipLaunchKernelGGL(k_astat, dim3((unsigned)(per_xcd * kNumXcd)), dim3(64 * kWaves), lds,
-                       as_stream(stream), n, A_off, A_starts, nA, A_vals, B_vals, C_off, C_len,
-                       C_starts, (int32_t)c_ndiag, pair_ptr,
-                       reinterpret_cast<const int4*>(records), C_vals, blocks, groups, per_xcd);
-    return check_launch(fn);
+    return diagpu::launch_astat<float>("diagpu_spgemm_numeric_astat_f32", n, A_off, A_starts, nA,
+                                       A_vals, B_vals, C_off, C_len, C_starts, c_ndiag, pair_ptr,
+                                       records, n_pairs, C_vals, stream);
+}
+
+DIAGPU_API int diagpu_spgemm_numeric_astat_c64(
+    int32_t n, const int32_t* A_off, const int64_t* A_starts, int32_t nA,
+    const diagpu_complex64* A_vals, const diagpu_complex64* B_vals, const int32_t* C_off,
+    const int32_t* C_len, const int64_t* C_starts, int64_t c_ndiag, const int64_t* pair_ptr,
+    const int32_t* records, int64_t n_pairs, diagpu_complex64* C_vals, void* stream)
+{
+    using diagpu::cf32;
+    return diagpu::launch_astat<cf32>("diagpu_spgemm_numeric_astat_c64", n, A_off, A_starts, nA,
+                                      reinterpret_cast<const cf32*>(A_vals),
+                                      reinterpret_cast<const cf32*>(B_vals), C_off, C_len,
+                                      C_starts, c_ndiag, pair_ptr, records, n_pairs,
+                                      reinterpret_cast<cf32*>(C_vals), stream);
 }
 
 }  // extern "C"

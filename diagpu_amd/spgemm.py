@@ -186,14 +186,16 @@ class SpgemmPlan:
 
     def uses_astat(self, dtype=torch.float32) -> bool:
         """The automatic choice after the band kernel: the A-stationary kernel
-        for fp32 plans whose A diagonals fit its LDS (at most
-        DIAGPU_ASTAT_MAX_A) and each feed at least 16 plan entries on average
-        (the reuse that pays for staging them: gemm_diag's band, 21 per A
-        diagonal, runs faster than on the gather at every n from 4096 up;
-        config 4, 7 per A diagonal, slower), with n >= 4096; B values must
-        be addressable with int32."""
+        for fp32 and complex64 plans whose A diagonals fit its LDS (at most
+        DIAGPU_ASTAT_MAX_A, DIAGPU_ASTAT_MAX_A_C64 for complex values) and
+        each feed at least 16 plan entries on average (the reuse that pays
+        for staging them: gemm_diag's band, 21 per A diagonal, runs faster
+        than on the gather at every n from 4096 up; config 4, 7 per A
+        diagonal, slower), with n >= 4096; B values must be addressable with
+        int32."""
         na = self.A.offsets.numel()
-        if not (dtype == torch.float32 and self.info.c_ndiag > 0 and na <= _lib.ASTAT_MAX_A
+        cap = {torch.float32: _lib.ASTAT_MAX_A, torch.complex64: _lib.ASTAT_MAX_A_C64}.get(dtype)
+        if not (cap is not None and self.info.c_ndiag > 0 and na <= cap
                 and self.info.n_pairs >= 16 * na and self.n >= 4096):
             return False
         if self._astat is False:                  # refused before: B indices beyond int32
@@ -230,8 +232,9 @@ class SpgemmPlan:
                 kernel: str = "auto") -> None:
         """C values for the plan's structure; float32 or complex64 (all three
         tensors the same dtype).  kernel: "auto" (kernel_for), "gather" (any
-        plan), "band" (fp32, narrow bands) or "astat" (fp32, at most
-        DIAGPU_ASTAT_MAX_A A diagonals), which all return the same bits, or
+        plan), "band" (fp32, narrow bands) or "astat" (at most
+        DIAGPU_ASTAT_MAX_A A diagonals, DIAGPU_ASTAT_MAX_A_C64 for complex
+        values), which all return the same bits, or
         "band_mfma" (fp32, narrow bands on the matrix cores: the same values
         to rounding, finite operands)."""
         dt = A_vals.dtype
@@ -252,7 +255,7 @@ class SpgemmPlan:
             raise ValueError(f"C_vals has {C_vals.numel()} elements, needs {self.info.c_nnz}")
         if kernel == "auto":
             kernel = self.kernel_for(dt)
-        if kernel in ("band", "astat", "band_mfma") and dt != torch.float32:
+        if kernel in ("band", "band_mfma") and dt != torch.float32:
             raise TypeError(f"the {kernel} kernel is fp32")
         if kernel == "band_mfma":
             _, info = self.band_info()
@@ -267,7 +270,8 @@ class SpgemmPlan:
         if kernel == "astat":
             rec = self.astat_records()
             A = self.A
-            _lib.call("diagpu_spgemm_numeric_astat_f32", self.n, A.offsets.data_ptr(),
+            _lib.call("diagpu_spgemm_numeric_astat_f32" if dt == torch.float32
+                      else "diagpu_spgemm_numeric_astat_c64", self.n, A.offsets.data_ptr(),
                       A.starts.data_ptr(), A.offsets.numel(), A_vals.data_ptr(), B_vals.data_ptr(),
                       self.C_off.data_ptr(), self.C_len.data_ptr(), self.C_starts.data_ptr(),
                       self.info.c_ndiag, self.ptr.data_ptr(), rec.data_ptr(), self.info.n_pairs,

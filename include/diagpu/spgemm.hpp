@@ -300,14 +300,17 @@ public:
         if (band_auto_) prepare_band(stream);
         // The A-stationary kernel's records where the automatic choice may
         // take it: A fits its LDS and each A diagonal feeds >= 16 entries.
-        astat_auto_ = !uses_band() && info_.c_ndiag > 0 && a_ndiag <= DIAGPU_ASTAT_MAX_A &&
-                      info_.n_pairs >= 16 * int64_t(a_ndiag) && int64_t(n) >= 4096;
-        if (astat_auto_) {
+        // The records serve both value types (the band kernel is fp32 only).
+        const bool reuse = info_.c_ndiag > 0 && info_.n_pairs >= 16 * int64_t(a_ndiag) &&
+                           int64_t(n) >= 4096;
+        astat_auto_ = !uses_band() && reuse && a_ndiag <= DIAGPU_ASTAT_MAX_A;
+        astat_auto_c64_ = reuse && a_ndiag <= DIAGPU_ASTAT_MAX_A_C64;
+        if (astat_auto_ || astat_auto_c64_) {
             try {
                 prepare_astat(stream);
             } catch (const Error& e) {
                 if (e.status != DIAGPU_ERR_CAPACITY) throw;   // B indices beyond int32
-                astat_auto_ = false;
+                astat_auto_ = astat_auto_c64_ = false;
             }
         }
     }
@@ -322,6 +325,9 @@ public:
     // kernel does not take the plan, A has at most DIAGPU_ASTAT_MAX_A
     // diagonals, each feeding >= 16 plan entries on average, and n >= 4096.
     bool uses_astat() const { return astat_auto_; }
+    // The same for complex64 values: A has at most DIAGPU_ASTAT_MAX_A_C64
+    // diagonals, each feeding >= 16 plan entries on average, and n >= 4096.
+    bool uses_astat_c64() const { return astat_auto_c64_; }
 
     // C_vals (device, info().c_nnz values) = A * B; asynchronous on `stream`
     // (NumericKernel::Band or AStationary on a plan not yet prepared for it
@@ -353,10 +359,25 @@ public:
                                         info_.max_pairs, dC_vals, stream));
     }
 
-    // The same product with complex64 operands and C (same plan).
+    // The same product with complex64 operands and C (same plan): Auto runs
+    // the A-stationary kernel where uses_astat_c64(), else the gather; Band
+    // is refused (fp32 only) with DIAGPU_ERR_ARG.
     void numeric(const diagpu_complex64* dA_vals, const diagpu_complex64* dB_vals,
-                 diagpu_complex64* dC_vals, hipStream_t stream = 0) const
+                 diagpu_complex64* dC_vals, hipStream_t stream = 0,
+                 NumericKernel kernel = NumericKernel::Auto) const
     {
+        if (kernel == NumericKernel::Auto)
+            kernel = uses_astat_c64() ? NumericKernel::AStationary : NumericKernel::Gather;
+        if (kernel == NumericKernel::Band)
+            throw Error(DIAGPU_ERR_ARG, "SpgemmPlan::numeric: the band kernel takes fp32 values only");
+        if (kernel == NumericKernel::AStationary) {
+            if (!astat_prepared_) prepare_astat(stream);
+            check(diagpu_spgemm_numeric_astat_c64(
+                n_, A_off_.data(), A_starts_.data(), nA_, dA_vals, dB_vals, C_off_.data(),
+                C_len_.data(), C_starts_.data(), info_.c_ndiag, ptr_.data(), records_.data(),
+                info_.n_pairs, dC_vals, stream));
+            return;
+        }
         check(diagpu_spgemm_numeric_c64(n_, dA_vals, dB_vals, C_off_.data(), C_len_.data(),
                                         C_starts_.data(), info_.c_ndiag, ptr_.data(), pairs_.data(),
                                         info_.max_pairs, dC_vals, stream));
@@ -414,6 +435,7 @@ private:
     diagpu_spgemm_info info_{};
     bool band_auto_ = false;
     bool astat_auto_ = false;
+    bool astat_auto_c64_ = false;
     mutable DeviceArray<int32_t> records_;
     mutable bool astat_prepared_ = false;
     mutable DeviceArray<int32_t> entries_;

@@ -329,6 +329,26 @@ static void test_astat_kernel()
     const auto hg = cg.download(), ha = ca.download(), hf = cf.download();
     report("astat: Auto == Gather, bit for bit", std::memcmp(hg.data(), ha.data(), nnz * 4) == 0);
     report("astat: AStationary == Gather", std::memcmp(hg.data(), hf.data(), nnz * 4) == 0);
+
+    // complex values v + i v' on the same plan: Auto takes the complex
+    // A-stationary kernel (40 A diagonals <= DIAGPU_ASTAT_MAX_A_C64)
+    std::vector<diagpu_complex64> cv((size_t)tot);
+    for (size_t p = 0; p < cv.size(); ++p) cv[p] = diagpu_complex64{vals[p], vals[(p + 7) % cv.size()]};
+    diagpu::DeviceArray<diagpu_complex64> dcv(cv), zg(nnz), za(nnz);
+    report("astat: Auto takes complex values too", plan.uses_astat_c64());
+    plan.numeric(dcv.data(), dcv.data(), zg.data(), 0, diagpu::NumericKernel::Gather);
+    plan.numeric(dcv.data(), dcv.data(), za.data());
+    diagpu::check_hip(hipDeviceSynchronize(), "sync");
+    const auto hzg = zg.download(), hza = za.download();
+    report("astat: complex Auto == Gather, bit for bit",
+           std::memcmp(hzg.data(), hza.data(), nnz * sizeof(diagpu_complex64)) == 0);
+    bool refused = false;
+    try {
+        plan.numeric(dcv.data(), dcv.data(), za.data(), 0, diagpu::NumericKernel::Band);
+    } catch (const diagpu::Error& e) {
+        refused = e.status == DIAGPU_ERR_ARG;
+    }
+    report("astat: complex Band refused", refused);
 }
 
 // The reference benchmarks' operand generators against the oracle's

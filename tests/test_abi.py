@@ -183,16 +183,26 @@ def test_complex_and_krylov_argument_errors():
     assert astat(_lib.ASTAT_MAX_A + 1, 5) == _lib.ERR_CAPACITY
     assert astat(3, 200) == _lib.ERR_ARG           # c_ndiag > 2n - 1
     assert astat(3, 0) == _lib.OK                   # empty C: nothing to do
+    astat_c = lambda nA, nC: _status("diagpu_spgemm_numeric_astat_c64", 100, fake, fake, nA, fake,
+                                     fake, fake, fake, fake, nC, fake, fake, 1, fake, None)
+    assert astat_c(0, 5) == _lib.ERR_ARG
+    assert astat_c(_lib.ASTAT_MAX_A_C64 + 1, 5) == _lib.ERR_CAPACITY
+    assert astat_c(3, 200) == _lib.ERR_ARG
+    assert astat_c(3, 0) == _lib.OK
 
 
 def test_astat_max_a_matches_header():
-    """The Python constant mirrors DIAGPU_ASTAT_MAX_A, and 288 rows of that
-    many A diagonals fit a workgroup's 160 KiB of LDS."""
+    """The Python constants mirror DIAGPU_ASTAT_MAX_A and _C64, and the
+    staged rows of that many A diagonals (288 fp32, 272 complex64) fit a
+    workgroup's 160 KiB of LDS, one more does not."""
     import re
     hdr = (Path(__file__).resolve().parents[1] / "include" / "diagpu.h").read_text()
     m = re.search(r"#define DIAGPU_ASTAT_MAX_A (\d+)", hdr)
     assert m and int(m.group(1)) == _lib.ASTAT_MAX_A
     assert 288 * _lib.ASTAT_MAX_A * 4 <= 160 * 1024 < 288 * (_lib.ASTAT_MAX_A + 1) * 4
+    m = re.search(r"#define DIAGPU_ASTAT_MAX_A_C64 (\d+)", hdr)
+    assert m and int(m.group(1)) == _lib.ASTAT_MAX_A_C64
+    assert 272 * _lib.ASTAT_MAX_A_C64 * 8 <= 160 * 1024 < 272 * (_lib.ASTAT_MAX_A_C64 + 1) * 8
 
 
 def test_symbolic_noalloc_rejects_beyond_scratch():

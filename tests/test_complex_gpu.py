@@ -356,3 +356,100 @@ def test_complex_spgemm_config4_and_config5(dev, oracle):
                 _check_complex(got, want, ab)
         del Cv, plan
         torch.cuda.empty_cache()
+
+
+def _bits(C):
+    return torch.view_as_real(C).contiguous().view(torch.int32)
+
+
+def _offsets(rng, cnt, lo, hi):
+    return sorted(rng.choice(np.arange(lo, hi + 1), size=cnt, replace=False).tolist())
+
+
+@pytest.mark.parametrize("n,case", [
+    (4096, "band32"),       # 32 random offsets over +-512 squared: 32 entries per A diagonal
+    (37, "edges"),          # smaller than one block, offsets reaching +-(n-1)
+    (1000, "wideB"),        # narrow A, B spanning the matrix
+    (70001, "ragged"),      # ragged last block, B beyond the A window
+    (5000, "maxA"),         # DIAGPU_ASTAT_MAX_A_C64 A diagonals
+    (1, "one"),             # a 1 x 1 matrix: one block, 16 lead rows before row 0
+    (3, "three"),           # every diagonal of a 3 x 3 matrix
+])
+def test_complex_astat_same_bits_as_gather(dev, oracle, n, case):
+    """The complex A-stationary kernel returns the complex gather's C bit for
+    bit (same plan order, same four fused multiply-adds per term, same
+    skipped terms), and both agree with the oracle's complex128 products."""
+    from diagpu_amd import _lib
+    from diagpu_amd.spgemm import SpgemmPlan
+    rng = np.random.default_rng(n + 7)
+    if case == "band32":
+        oa = ob = _offsets(rng, 32, -512, 512)
+    elif case == "edges":
+        oa, ob = [-36, -3, 0, 2, 36], [-30, -1, 0, 5, 36]
+    elif case == "wideB":
+        oa, ob = list(range(-40, 41, 3)), [-999, -7, 0, 1, 998]
+    elif case == "ragged":
+        oa, ob = list(range(-12, 13)), [-65000, -3, 0, 4, 65000]
+    elif case == "one":
+        oa, ob = [0], [0]
+    elif case == "three":
+        oa, ob = [-2, -1, 0, 1, 2], [-2, 0, 1]
+    else:
+        oa, ob = _offsets(rng, _lib.ASTAT_MAX_A_C64, -2000, 2000), _offsets(rng, 9, -100, 100)
+    A = _complexify(workloads.hm_random(n, oa, seed=31, device=dev), 3)
+    B = _complexify(workloads.hm_random(n, ob, seed=32, device=dev), 5)
+    plan = SpgemmPlan(A, B)
+    Cg = plan.multiply(A.values, B.values, kernel="gather")
+    Ca = plan.multiply(A.values, B.values, kernel="astat")
+    assert Ca.dtype == torch.complex64
+    assert torch.equal(_bits(Cg), _bits(Ca))
+    if n <= 5000:
+        c_len, c_st, ptr, pairs = _plan_host(oracle, plan, A, B)
+        want, ab = oracle.spgemm_pairs_complex(A.values.cpu().numpy(), B.values.cpu().numpy(),
+                                               c_len, c_st, ptr, pairs, 0, len(c_len))
+        _check_complex(Ca.cpu().numpy(), want, ab)
+
+
+def test_complex_astat_real_values_equal_real_kernel(dev):
+    """Zero imaginary parts: the complex A-stationary kernel's real part is
+    the real A-stationary kernel's C bit for bit, its imaginary part zero."""
+    from diagpu_amd.spgemm import SpgemmPlan
+    rng = np.random.default_rng(11)
+    offs = _offsets(rng, 24, -300, 300)
+    A = workloads.hm_random(20000, offs, seed=1, device=dev)
+    B = workloads.hm_random(20000, offs, seed=2, device=dev)
+    plan = SpgemmPlan(A, B)
+    Cr = plan.multiply(A.values, B.values, kernel="astat")
+    Ac = torch.complex(A.values, torch.zeros_like(A.values)).contiguous()
+    Bc = torch.complex(B.values, torch.zeros_like(B.values)).contiguous()
+    Cc = plan.multiply(Ac, Bc, kernel="astat")
+    assert torch.equal(Cc.real.contiguous().view(torch.int32), Cr.view(torch.int32))
+    assert torch.count_nonzero(Cc.imag) == 0
+
+
+def test_complex_astat_choice_and_capacity(dev):
+    """auto takes the complex A-stationary kernel for complex plans whose A
+    fits (at most DIAGPU_ASTAT_MAX_A_C64 diagonals, >= 16 entries each,
+    n >= 4096) and the gather otherwise; more A diagonals are refused with
+    DIAGPU_ERR_CAPACITY before any launch, the band kernel takes fp32 only."""
+    from diagpu_amd import _lib
+    from diagpu_amd.spgemm import SpgemmPlan
+    rng = np.random.default_rng(5)
+    offs = _offsets(rng, 40, -512, 512)
+    H = _complexify(workloads.hm_random(1 << 16, offs, seed=4, device=dev), 1)
+    p = SpgemmPlan(H, H)
+    assert p.kernel_for(torch.complex64) == "astat"
+    assert torch.equal(_bits(p.multiply(H.values, H.values)),
+                       _bits(p.multiply(H.values, H.values, kernel="gather")))
+    A4, B4 = workloads.spgemm_config(4, seed=4, device=dev)      # 7 entries per A diagonal
+    assert SpgemmPlan(A4, B4).kernel_for(torch.complex64) == "gather"
+    wide = _complexify(workloads.hm_random(4096, _offsets(rng, _lib.ASTAT_MAX_A_C64 + 1, -300, 300),
+                                           seed=6, device=dev), 2)
+    pw = SpgemmPlan(wide, wide)
+    assert pw.kernel_for(torch.complex64) == "gather"
+    assert pw.kernel_for(torch.float32) == "astat"               # the fp32 kernel holds 142
+    with pytest.raises(_lib.DiagpuError) as e:
+        pw.multiply(wide.values, wide.values, kernel="astat")
+    assert e.value.status == _lib.ERR_CAPACITY
+    with pytest.raises(TypeError):
+        pw.multiply(wide.values, wide.values, kernel="band")
