@@ -280,19 +280,20 @@ def cpu_spgemm_baseline(plan, A, B, seconds: float):
                       f"of the flops), {reps} runs of {sec * 1e3:.1f} ms, oracle OpenMP loop"}
 
 
-def compare_kernels(plan, sets, reps: int, alg: int, flops: int) -> dict:
-    """Every numeric kernel that takes this fp32 plan, forced, on the same
-    rotated operand sets (the side-by-side run of spmspm/bench_spmspm.cu:
-    518-653): time per product, GFLOP/s, fraction of HBM peak, and whether C
-    is bit for bit the gather's (checked where one more C fits in 4 GB)."""
+def compare_kernels(plan, sets, reps: int, alg: int, flops: int, complex_values: bool = False) -> dict:
+    """Every numeric kernel that takes this plan (fp32 or complex64 values),
+    forced, on the same rotated operand sets (the side-by-side run of
+    spmspm/bench_spmspm.cu:518-653): time per product, GFLOP/s, fraction of
+    HBM peak, and whether C is bit for bit the gather's (checked where one
+    more C fits in 4 GB)."""
     import torch
     from diagpu_amd import _lib
     names = ["gather"]
-    if plan.band_info()[1].eligible:
+    if not complex_values and plan.band_info()[1].eligible:
         names.append("band")
-    if plan.band_info()[1].mfma_eligible:
+    if not complex_values and plan.band_info()[1].mfma_eligible:
         names.append("band_mfma")
-    if plan.A.offsets.numel() <= _lib.ASTAT_MAX_A:
+    if plan.A.offsets.numel() <= (_lib.ASTAT_MAX_A_C64 if complex_values else _lib.ASTAT_MAX_A):
         try:
             plan.astat_records()
             names.append("astat")
@@ -302,7 +303,8 @@ def compare_kernels(plan, sets, reps: int, alg: int, flops: int) -> dict:
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     nsets = len(sets)
     ref = None
-    check = plan.info.c_nnz * 4 <= (4 << 30)
+    esz = 8 if complex_values else 4
+    check = plan.info.c_nnz * esz <= (4 << 30)
     out = {}
     for k in names:
         for i in range(2):
@@ -323,6 +325,7 @@ def compare_kernels(plan, sets, reps: int, alg: int, flops: int) -> dict:
             plan.numeric(*sets[0], kernel=k)
             torch.cuda.synchronize()
             c = sets[0][2][: plan.info.c_nnz]
+            c = torch.view_as_real(c) if complex_values else c
             if ref is None:
                 ref = c.clone()
             rec["same_bits_as_gather"] = bool(torch.equal(ref.view(torch.int32), c.view(torch.int32)))
@@ -374,7 +377,7 @@ def time_spgemm(cfg: int, seed: int, reps: int, complex_values: bool = False,
     ms = e0.elapsed_time(e1) / reps
     alg = esz * (A.nnz + B.nnz + plan.info.c_nnz)
     flops = plan.info.useful_flops * (4 if complex_values else 1)   # complex MAC = 4 real
-    kernels = {} if complex_values else compare_kernels(plan, sets, max(3, reps // 2), alg, flops)
+    kernels = compare_kernels(plan, sets, max(3, reps // 2), alg, flops, complex_values)
     return {
         "workload": f"spgemm_cfg{cfg}" if cfg >= 4 else f"spgemm_HxH_cfg{cfg}",
         "dtype": "c64" if complex_values else "f32", "n": A.n,

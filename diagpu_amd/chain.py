@@ -198,18 +198,21 @@ def multiply(A: HM, B: HM, stats: ChainStats | None = None) -> HM:
 
 
 def _narrow_first(X: HM) -> bool:
-    """Whether a chain step multiplies the narrow factor from the left: for
-    real values it is then the A operand, whose few diagonals the
-    A-stationary kernel holds in LDS (the 7-point stencil's last Taylor step,
-    (t H) * S_2 with 377 C diagonals: 0.97 ms, against 1.24 for S_2 * (t H)
-    on the gather); for complex values the gather takes the product either
-    way and is faster with the wide factor on the left."""
-    return X.values.dtype == torch.float32
+    """Whether a chain step multiplies the narrow factor X from the left: it
+    is then the A operand, whose few diagonals the A-stationary kernel holds
+    in LDS (the 7-point stencil's last Taylor step, (t H) * S_2 with 377 C
+    diagonals: 0.97 ms against 1.24 for S_2 * (t H) on the gather; the
+    complex propagator of the same stencil: 4.46 ms against 5.89).  Always
+    for real values; for complex values where X fits the complex kernel
+    (DIAGPU_ASTAT_MAX_A_C64 diagonals), else the gather takes the product,
+    which is faster with the wide factor on the left."""
+    return X.values.dtype == torch.float32 or X.ndiag <= _lib.ASTAT_MAX_A_C64
 
 
 def power(H: HM, k: int, stats: ChainStats | None = None) -> HM:
     """H^k (k >= 1) by the chain P_j = H * P_{j-1} (P_{j-1} * H for complex
-    values; the factors commute)."""
+    values when H is too wide for the complex A-stationary kernel; the
+    factors commute)."""
     if k < 1:
         raise ValueError("k must be >= 1")
     P = H
@@ -254,8 +257,8 @@ def taylor_expm(H: HM, t, order: int, stats: ChainStats | None = None) -> HM:
 
     so each step is one device-planned SpGEMM of the wide S_{j+1} and the
     narrow (t/j) H (S_{j+1} is a polynomial in H, so the two commute; the
-    narrow factor goes first for real values, last for complex ones, the
-    faster order of each), and an in-place add of I to the product's main
+    narrow factor goes first where the A-stationary kernel holds it:
+    _narrow_first), and an in-place add of I to the product's main
     diagonal (a full union pass only when the product lacks that diagonal)."""
     if order < 0:
         raise ValueError("order must be >= 0")

@@ -18,20 +18,24 @@
 // the element: the gather kernel's exact sequence of roundings, so both
 // kernels return the same bits.
 //
-// Per C diagonal the rows a wave evaluates start kLead - s rows before the
-// block, s = (C start + min(dc, 0)) mod 32: the block's C values then start
-// on a 128-byte line, so no line is written in two parts by two workgroups
-// (a read-modify-write in HBM).  The kLead rows staged before the block
-// cover that shift.
+// Per C diagonal the rows a wave evaluates start s rows before the block,
+// s = (C start + min(dc, 0)) mod kLead, kLead = the elements of a 128-byte
+// line: the block's C values then start on a line, so no line is written in
+// two parts by two workgroups (a read-modify-write in HBM).  The kLead rows
+// staged before the block cover that shift.  The last of the ceil(n / kRB)
+// blocks also takes the rows [i0 + kRB - s, n) left after the shift: its
+// staged window holds them, since n <= i0 + kRB.
 //
 // A workgroup has kWaves waves; wave w evaluates C diagonals w, w + kWaves,
 // ... over the block's kRB rows, 4 rows per lane (lane l: rows l, l + 64,
-// l + 128, l + 192 of the shifted window).  The plan entries come as records
+// l + 128, l + 192 of the shifted window; a 5th, l + 256, in the last
+// block).  The plan entries come as records
 // {a, lo, hi, b} (diagpu_spgemm_astat_prepare): a the A diagonal's index,
 // [lo, hi) the C positions where both operands hold an element, b the B
 // index of C position 0.
 #include <algorithm>
 #include <climits>
+#include <type_traits>
 
 #include "common.hpp"
 #include "elem.hpp"
@@ -114,8 +118,9 @@ __device__ __forceinline__ void store_elem_nt(T* p, T v)
     __builtin_nontemporal_store(r, reinterpret_cast<Raw*>(p));
 }
 
+// 8 waves per SIMD (at most 64 VGPRs): two 16-wave workgroups per CU.
 template <typename T>
-__global__ __launch_bounds__(64 * kWaves) void k_astat(
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(8))) void k_astat(
     int32_t n, const int32_t* __restrict__ A_off, const int64_t* __restrict__ A_starts, int32_t nA,
     const T* __restrict__ Av, const T* __restrict__ Bv, const int32_t* __restrict__ C_off,
     const int32_t* __restrict__ C_len, const int64_t* __restrict__ C_starts, int32_t nC,
@@ -132,7 +137,9 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
     // GPU), each staging the block's A rows.
     const int unit = (int)(blockIdx.x % kNumXcd) * per_xcd + (int)(blockIdx.x / kNumXcd);
     if (unit >= blocks * groups) return;
-    const int blk = unit / groups, grp = unit % groups;
+    // the last block (5 rows per lane) first: dispatched with the first
+    // wave of workgroups, its longer work overlaps the others'
+    const int blk = (unit / groups + blocks - 1) % blocks, grp = unit % groups;
     const int r = (int)threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(r >> 6), lane = r & 63;
     const int i0 = blk * kRB;                       // n <= 2^30: rows fit int32
@@ -159,70 +166,85 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
     __builtin_amdgcn_s_waitcnt(0);   // this wave's direct loads have landed in LDS
     __syncthreads();
 
-    for (int kc = grp * kWaves + wave; kc < nC; kc += groups * kWaves) {
-        const int dc = C_off[kc];
-        const int len = C_len[kc];
-        const int64_t cst = C_starts[kc];
-        const int mc = dc < 0 ? dc : 0;
-        const int s = (int)((cst + mc) & (kLead - 1));   // C(i0 - s, ...) starts a line
-        const int g0 = (int)pair_ptr[kc], g1 = (int)pair_ptr[kc + 1];
-        const int pb = i0 - s + lane + mc;          // C position of the lane's first row
-        const int ab = kLead - s + lane;            // its staged A row
-        T acc[4];
+    // R rows per lane: 4, and 5 in the last block, whose staged window also
+    // holds the rows [i0 + kRB - s, n) that no later block covers (n <= i0 +
+    // kRB there): an extra block for them would cost a whole workgroup's
+    // time, which is set by the per-diagonal chain of loads, not by rows.
+    auto run = [&](auto rows) {
+        constexpr int R = decltype(rows)::value;
+        for (int kc = grp * kWaves + wave; kc < nC; kc += groups * kWaves) {
+            const int dc = C_off[kc];
+            const int len = C_len[kc];
+            const int64_t cst = C_starts[kc];
+            const int mc = dc < 0 ? dc : 0;
+            const int s = (int)((cst + mc) & (kLead - 1));   // C(i0 - s, ...) starts a line
+            const int g0 = (int)pair_ptr[kc], g1 = (int)pair_ptr[kc + 1];
+            const int pb = i0 - s + lane + mc;          // C position of the lane's first row
+            const int ab = kLead - s + lane;            // its staged A row
+            T acc[R];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[j] = zero_of<T>();
-        // one term: B by a clamped (always valid) load, A from LDS, the
-        // multiply-add kept where both operands hold the element
-        auto term = [&](const int4& e, int hi, int j, T& b, T& a, bool& ok) {
-            const int p = pb + 64 * j;
-            ok = p >= e.y && p < hi;
-            b = load_elem<T, false>(Bv + (int64_t)e.w + min(max(p, e.y), e.z - 1));
-            a = A_t[e.x * kStage + ab + 64 * j];
-        };
-        // The values of a batch are pinned once all its loads are issued, so
-        // the compiler cannot turn a masked multiply-add into a branch around
-        // its own load (each such branch ends in a full vmcnt(0) drain: gfx9
-        // counts loads in order).
-        int g = g0;
-        for (; g + 2 <= g1; g += 2) {               // two entries' loads in flight
-            T bv[2][4], av[2][4];
-            bool ok[2][4];
+            for (int j = 0; j < R; ++j) acc[j] = zero_of<T>();
+            // one term: B by a clamped (always valid) load, A from LDS (row
+            // 4 of a lane past the window, p >= len there, reads row 0), the
+            // multiply-add kept where both operands hold the element
+            auto term = [&](const int4& e, int hi, int j, T& b, T& a, bool& ok) {
+                const int p = pb + 64 * j;
+                ok = p >= e.y && p < hi;
+                b = load_elem<T, false>(Bv + (int64_t)e.w + min(max(p, e.y), e.z - 1));
+                a = A_t[e.x * kStage + (j < 4 || lane < s ? ab + 64 * j : ab)];
+            };
+            // The values of a batch are pinned once all its loads are issued,
+            // so the compiler cannot turn a masked multiply-add into a branch
+            // around its own load (each such branch ends in a full vmcnt(0)
+            // drain: gfx9 counts loads in order).
+            // two entries' loads in flight (one for complex values with 5
+            // rows: 64 VGPRs)
+            constexpr int U = (R == 5 && sizeof(T) == 8) ? 1 : 2;
+            int g = g0;
+            for (; U == 2 && g + 2 <= g1; g += 2) {
+                T bv[2][R], av[2][R];
+                bool ok[2][R];
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int4 e = records[g + u];
-                const int hi = min(e.z, len);
+                for (int u = 0; u < 2; ++u) {
+                    const int4 e = records[g + u];
+                    const int hi = min(e.z, len);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) term(e, hi, j, bv[u][j], av[u][j], ok[u][j]);
+                    for (int j = 0; j < R; ++j) term(e, hi, j, bv[u][j], av[u][j], ok[u][j]);
+                }
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int j = 0; j < R; ++j) { pin(bv[u][j]); pin(av[u][j]); }
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int j = 0; j < R; ++j)
+                        acc[j] = sel(ok[u][j], mad(acc[j], av[u][j], bv[u][j]), acc[j]);
             }
+            for (; g < g1; ++g) {
+                const int4 e = records[g];
+                const int hi = min(e.z, len);
+                T bv[R], av[R];
+                bool ok[R];
 #pragma unroll
-            for (int u = 0; u < 2; ++u)
+                for (int j = 0; j < R; ++j) term(e, hi, j, bv[j], av[j], ok[j]);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) { pin(bv[u][j]); pin(av[u][j]); }
+                for (int j = 0; j < R; ++j) { pin(bv[j]); pin(av[j]); }
 #pragma unroll
-            for (int u = 0; u < 2; ++u)
+                for (int j = 0; j < R; ++j) acc[j] = sel(ok[j], mad(acc[j], av[j], bv[j]), acc[j]);
+            }
+            T* __restrict__ cp = Cv + cst;
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[j] = sel(ok[u][j], mad(acc[j], av[u][j], bv[u][j]), acc[j]);
+            for (int j = 0; j < R; ++j) {
+                const int p = pb + 64 * j;
+                if (p >= 0 && p < len) store_elem_nt(cp + p, acc[j]);
+            }
         }
-        if (g < g1) {
-            const int4 e = records[g];
-            const int hi = min(e.z, len);
-            T bv[4], av[4];
-            bool ok[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) term(e, hi, j, bv[j], av[j], ok[j]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) { pin(bv[j]); pin(av[j]); }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[j] = sel(ok[j], mad(acc[j], av[j], bv[j]), acc[j]);
-        }
-        T* __restrict__ cp = Cv + cst;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int p = pb + 64 * j;
-            if (p >= 0 && p < len) store_elem_nt(cp + p, acc[j]);
-        }
-    }
+    };
+    if (blk == blocks - 1)
+        run(std::integral_constant<int, 5>{});
+    else
+        run(std::integral_constant<int, 4>{});
 }
 
 template <typename T>
@@ -250,7 +272,7 @@ int launch_astat(const char* fn, int32_t n, const int32_t* A_off, const int64_t*
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  kStage * kMax * (int)sizeof(T)), fn);
     if (st) return st;
-    const int32_t blocks = (int32_t)ceil_div<int64_t>((int64_t)n + kLead, kRB);
+    const int32_t blocks = (int32_t)ceil_div<int64_t>(n, kRB);
     // too few blocks to give every CU its workgroups (two, or one above
     // kMax2 A diagonals): split each block's C diagonals over several (at
     // most one per wave's worth of diagonals)

@@ -186,17 +186,43 @@ class SpgemmPlan:
 
     def uses_astat(self, dtype=torch.float32) -> bool:
         """The automatic choice after the band kernel: the A-stationary kernel
-        for fp32 and complex64 plans whose A diagonals fit its LDS (at most
-        DIAGPU_ASTAT_MAX_A, DIAGPU_ASTAT_MAX_A_C64 for complex values) and
-        each feed at least 16 plan entries on average (the reuse that pays
-        for staging them: gemm_diag's band, 21 per A diagonal, runs faster
-        than on the gather at every n from 4096 up; config 4, 7 per A
-        diagonal, slower), with n >= 4096; B values must be addressable with
-        int32."""
+        where A's diagonals fit its LDS (at most DIAGPU_ASTAT_MAX_A, or
+        DIAGPU_ASTAT_MAX_A_C64 for complex values), n >= 4096, B values are
+        addressable with int32, and the plan reuses the staged A runs:
+
+          fp32:      >= 16 entries per A diagonal, or >= 32 entries with
+                     >= 4 per A diagonal and >= 1.5 per C diagonal;
+          complex64: n >= 2^18 with >= 16 C diagonals (every wave of a
+                     workgroup busy), or >= 32 entries with >= 4 per A
+                     diagonal.
+
+        The thresholds separate what was measured against the gather on
+        MI355X: fp32 stencil products gain 26-30 % (9-point square at
+        n = 2^22: 135 vs 183 us), while config 4 (63 entries over 47 C
+        diagonals: a near-streaming product that the gather runs at the
+        write-bound rate) ties and config 2's square (25 entries: too little
+        work per staged block) loses (80 vs 58 us); random plans with 2-3
+        entries per A diagonal went either way (time ratios 0.73-1.22) and
+        are left to the gather.  Complex values gained at every measured shape from
+        n = 2^18 up with >= 16 C diagonals (the complex gather re-reads the
+        operand runs at its items' edges), and below that where each A
+        diagonal feeds >= 4 entries.  (Ratios measured one buffer set at a
+        time; under the benchmark's rotating sets complex config 4 gains
+        4 %: 128 vs 133 us.)"""
         na = self.A.offsets.numel()
-        cap = {torch.float32: _lib.ASTAT_MAX_A, torch.complex64: _lib.ASTAT_MAX_A_C64}.get(dtype)
-        if not (cap is not None and self.info.c_ndiag > 0 and na <= cap
-                and self.info.n_pairs >= 16 * na and self.n >= 4096):
+        inf = self.info
+        if inf.c_ndiag == 0 or self.n < 4096:
+            return False
+        reuse = inf.n_pairs >= 32 and inf.n_pairs >= 4 * na
+        if dtype == torch.float32:
+            ok = na <= _lib.ASTAT_MAX_A and (inf.n_pairs >= 16 * na
+                                             or (reuse and 2 * inf.n_pairs >= 3 * inf.c_ndiag))
+        elif dtype == torch.complex64:
+            ok = na <= _lib.ASTAT_MAX_A_C64 and ((self.n >= 1 << 18 and inf.c_ndiag >= 16)
+                                                 or reuse)
+        else:
+            ok = False
+        if not ok:
             return False
         if self._astat is False:                  # refused before: B indices beyond int32
             return False

@@ -221,22 +221,28 @@ inline DeviceHMT<T> multiply(const DeviceHMT<T>& A, const DeviceHMT<T>& B, hipSt
     return C;
 }
 
-// Whether a chain step multiplies the narrow factor from the left: for fp32
-// it is then the A operand, whose few diagonals the A-stationary kernel holds
-// in LDS (the 7-point stencil's order-6 Taylor chain: 2.12 ms of products
-// against 2.58 with the wide factor first, on the gather); complex products
-// run on the gather either way, which is faster with the wide factor first.
-template <typename T> constexpr bool narrow_first() { return std::is_same<T, float>::value; }
+// Whether a chain step multiplies the narrow factor X from the left: it is
+// then the A operand, whose few diagonals the A-stationary kernel holds in
+// LDS (the 7-point stencil's order-6 Taylor chain: fp32 products 2.12 ms
+// against 2.58 with the wide factor first; complex propagator 4.46 ms against
+// 5.89).  Always for fp32; for complex values where X fits the complex
+// kernel (DIAGPU_ASTAT_MAX_A_C64 diagonals), else the gather takes the
+// product, which is faster with the wide factor first.
+template <typename T> inline bool narrow_first(const DeviceHMT<T>& X)
+{
+    return std::is_same<T, float>::value || X.ndiag() <= DIAGPU_ASTAT_MAX_A_C64;
+}
 
 // H^k (k >= 1) by the chain P_j = H * P_{j-1} (P_{j-1} * H for complex
-// values; the factors commute).
+// values when H is too wide for the complex A-stationary kernel; the factors
+// commute).
 template <typename T>
 inline DeviceHMT<T> power(const DeviceHMT<T>& H, int k, hipStream_t stream = 0)
 {
     if (k < 1) throw Error(DIAGPU_ERR_ARG, "power: k must be >= 1");
     DeviceHMT<T> P = axpby<T>(HMScalar<T>(1), H, HMScalar<T>(0), nullptr, stream);
     for (int j = 1; j < k; ++j)    // multiply syncs before P is freed
-        P = narrow_first<T>() ? multiply(H, P, stream) : multiply(P, H, stream);
+        P = narrow_first(H) ? multiply(H, P, stream) : multiply(P, H, stream);
     check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
     return P;
 }
@@ -268,7 +274,7 @@ inline void add_identity(DeviceHMT<T>& S, typename NoDeduce<HMScalar<T>>::type s
 //   S_order = I + (t/order) H,  S_j = I + S_{j+1} * ((t/j) H),  S = S_1,
 // one device-planned SpGEMM per step of the wide S_{j+1} and the narrow
 // (t/j) H (S_{j+1} is a polynomial in H, so they commute; the narrow factor
-// goes first for fp32, last for complex values: narrow_first).  t is real
+// goes first where the A-stationary kernel holds it: narrow_first).  t is real
 // for DeviceHM, complex for DeviceHMC.
 template <typename T>
 inline DeviceHMT<T> taylor_expm(const DeviceHMT<T>& H, typename NoDeduce<HMScalar<T>>::type t,
@@ -282,7 +288,7 @@ inline DeviceHMT<T> taylor_expm(const DeviceHMT<T>& H, typename NoDeduce<HMScala
     for (int j = order - 1; j >= 1; --j) {
         const DeviceHMT<T> Hj = axpby<T>(t / static_cast<float>(j), H, S_t(0), nullptr, stream);
         // multiply syncs before the old S is freed
-        S = narrow_first<T>() ? multiply(Hj, S, stream) : multiply(S, Hj, stream);
+        S = narrow_first(Hj) ? multiply(Hj, S, stream) : multiply(S, Hj, stream);
         add_identity<T>(S, S_t(1), stream);
     }
     check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");

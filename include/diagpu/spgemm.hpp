@@ -300,11 +300,15 @@ public:
         if (band_auto_) prepare_band(stream);
         // The A-stationary kernel's records where the automatic choice may
         // take it: A fits its LDS and each A diagonal feeds >= 16 entries.
-        // The records serve both value types (the band kernel is fp32 only).
-        const bool reuse = info_.c_ndiag > 0 && info_.n_pairs >= 16 * int64_t(a_ndiag) &&
-                           int64_t(n) >= 4096;
-        astat_auto_ = !uses_band() && reuse && a_ndiag <= DIAGPU_ASTAT_MAX_A;
-        astat_auto_c64_ = reuse && a_ndiag <= DIAGPU_ASTAT_MAX_A_C64;
+        // The records serve both value types (the band kernel is fp32 only);
+        // the rules are SpgemmPlan.uses_astat's in diagpu_amd/spgemm.py.
+        const int64_t np = info_.n_pairs, nc = info_.c_ndiag, na = a_ndiag;
+        const bool sized = nc > 0 && int64_t(n) >= 4096;
+        const bool reuse = np >= 32 && np >= 4 * na;
+        astat_auto_ = !uses_band() && sized && na <= DIAGPU_ASTAT_MAX_A &&
+                      (np >= 16 * na || (reuse && 2 * np >= 3 * nc));
+        astat_auto_c64_ = sized && na <= DIAGPU_ASTAT_MAX_A_C64 &&
+                          ((int64_t(n) >= (1 << 18) && nc >= 16) || reuse);
         if (astat_auto_ || astat_auto_c64_) {
             try {
                 prepare_astat(stream);
@@ -321,12 +325,16 @@ public:
     // are >= 512 row blocks of 256 (below that the A-stationary kernel or
     // the gather is faster).
     bool uses_band() const { return band_auto_ && band_.eligible; }
-    // True where NumericKernel::Auto runs the A-stationary kernel: the band
-    // kernel does not take the plan, A has at most DIAGPU_ASTAT_MAX_A
-    // diagonals, each feeding >= 16 plan entries on average, and n >= 4096.
+    // True where NumericKernel::Auto runs the A-stationary kernel for fp32
+    // values: the band kernel does not take the plan, A has at most
+    // DIAGPU_ASTAT_MAX_A diagonals, n >= 4096, and the plan has >= 16
+    // entries per A diagonal, or >= 32 entries with >= 4 per A diagonal and
+    // >= 1.5 per C diagonal (config 4, 63 entries over 47 C diagonals, is a
+    // near-streaming product that the gather runs as fast).
     bool uses_astat() const { return astat_auto_; }
     // The same for complex64 values: A has at most DIAGPU_ASTAT_MAX_A_C64
-    // diagonals, each feeding >= 16 plan entries on average, and n >= 4096.
+    // diagonals, n >= 4096, and n >= 2^18 with >= 16 C diagonals, or >= 32
+    // entries with >= 4 per A diagonal.
     bool uses_astat_c64() const { return astat_auto_c64_; }
 
     // C_vals (device, info().c_nnz values) = A * B; asynchronous on `stream`

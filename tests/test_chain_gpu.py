@@ -157,3 +157,25 @@ def test_taylor_stencil_2pow20(dev):
     # the stencil's absolute row sums are <= 12, so sum_k t^k/k! (|H|^k |x|) <= this
     abs_bound = sum((t * 12) ** k / math.factorial(k) for k in range(order + 1)) * np.abs(x).max()
     assert np.all(np.abs(got - want) <= 1e-5 * order * abs_bound)
+
+
+def test_complex_chain_order_and_kernel(dev):
+    """Complex chain steps put the narrow factor first where the complex
+    A-stationary kernel holds it (at most DIAGPU_ASTAT_MAX_A_C64 diagonals),
+    and that kernel then takes the 7-point stencil's steps at n = 2^20; the
+    narrow-first product equals the wide-first one to fp32 rounding (the
+    factors commute; only the order of the terms differs)."""
+    from diagpu_amd import _lib
+    from diagpu_amd.spgemm import SpgemmPlan
+    H = chain.as_complex(hm_stencil7(128, 128, 64, dev))
+    Hj = chain.axpby(-0.01j, H, 0.0, None)
+    S = chain.axpby(1.0, chain.multiply(Hj, Hj), 1.0, chain.identity(H.n, dev, torch.complex64))
+    assert chain._narrow_first(Hj)
+    assert SpgemmPlan(Hj, S).kernel_for(torch.complex64) == "astat"
+    C1, C2 = chain.multiply(Hj, S), chain.multiply(S, Hj)
+    assert C1.offsets.cpu().tolist() == C2.offsets.cpu().tolist()
+    err = (C1.values - C2.values).abs().max().item()
+    assert err <= 1e-6 * C1.values.abs().max().item()
+    wide = chain.as_complex(hm_random(4096, list(range(-_lib.ASTAT_MAX_A_C64, 1)), 3, dev))
+    assert not chain._narrow_first(wide)
+    assert chain._narrow_first(hm_random(4096, list(range(-200, 1)), 3, dev))   # fp32: always

@@ -457,9 +457,10 @@ def test_astat_kernel_same_bits_as_gather(dev, oracle, n, case):
 
 def test_astat_kernel_choice_and_capacity(dev):
     """auto picks the A-stationary kernel for the square of a 64-diagonal
-    band over +-512 (64 entries per A diagonal) and for gemm_diag's band
-    below 512 row blocks (21 per A diagonal), the band kernel above, the
-    gather for config 4 (7 per A diagonal); more than
+    band over +-512 (64 entries per A diagonal), for gemm_diag's band below
+    512 row blocks (21 per A diagonal) and for the 9-point stencil's square,
+    the band kernel above 512 row blocks, the gather for config 4 (63
+    entries over 47 C diagonals) and the 5-point square (25 entries); more than
     DIAGPU_ASTAT_MAX_A A diagonals are refused with DIAGPU_ERR_CAPACITY."""
     rng = np.random.default_rng(3)
     n = 1 << 18
@@ -478,6 +479,16 @@ def test_astat_kernel_choice_and_capacity(dev):
     assert SpgemmPlan(g5, g5).kernel_for() == "gather"
     A4, B4 = workloads.spgemm_config(4, seed=4, device=dev)
     assert SpgemmPlan(A4, B4).kernel_for() == "gather"
+    # stencil products: >= 32 entries, >= 4 per A diagonal, >= 1.5 per C
+    # diagonal (the 9-point square: 81 entries over 25 C diagonals)
+    nine = sorted({dy * 256 + dx for dx in (-1, 0, 1) for dy in (-1, 0, 1)})
+    S9 = workloads.hm_random(1 << 16, nine, 8, dev)
+    p9 = SpgemmPlan(S9, S9)
+    assert p9.kernel_for() == "astat"
+    assert torch.equal(p9.multiply(S9.values, S9.values).view(torch.int32),
+                       p9.multiply(S9.values, S9.values, kernel="gather").view(torch.int32))
+    S5 = workloads.hm_random(1 << 16, [-256, -1, 0, 1, 256], 8, dev)
+    assert SpgemmPlan(S5, S5).kernel_for() == "gather"          # 25 entries
     wide = workloads.hm_random(4096, _random_offsets(rng, _lib.ASTAT_MAX_A + 1, -300, 300), 6, dev)
     pw = SpgemmPlan(wide, wide)
     assert pw.kernel_for() != "astat"
