@@ -172,13 +172,29 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(8))
     // time, which is set by the per-diagonal chain of loads, not by rows.
     auto run = [&](auto rows) {
         constexpr int R = decltype(rows)::value;
-        for (int kc = grp * kWaves + wave; kc < nC; kc += groups * kWaves) {
-            const int dc = C_off[kc];
-            const int len = C_len[kc];
-            const int64_t cst = C_starts[kc];
+        // A diagonal's metadata is loaded while the diagonal before it runs
+        // (index clamped rather than tested: a load under a branch is
+        // waited for where the branch joins).
+        const int stride = groups * kWaves;
+        int kc = grp * kWaves + wave;
+        if (kc >= nC) return;
+        int dcn = C_off[kc], lenn = C_len[kc];
+        int64_t cstn = C_starts[kc], g0n = pair_ptr[kc], g1n = pair_ptr[kc + 1];
+        for (; kc < nC; kc += stride) {
+            const int dc = dcn;
+            const int len = lenn;
+            const int64_t cst = cstn;
+            const int g0 = (int)g0n, g1 = (int)g1n;
+            {
+                const int kn = min(kc + stride, nC - 1);
+                dcn = C_off[kn];
+                lenn = C_len[kn];
+                cstn = C_starts[kn];
+                g0n = pair_ptr[kn];
+                g1n = pair_ptr[kn + 1];
+            }
             const int mc = dc < 0 ? dc : 0;
             const int s = (int)((cst + mc) & (kLead - 1));   // C(i0 - s, ...) starts a line
-            const int g0 = (int)pair_ptr[kc], g1 = (int)pair_ptr[kc + 1];
             const int pb = i0 - s + lane + mc;          // C position of the lane's first row
             const int ab = kLead - s + lane;            // its staged A row
             T acc[R];
