@@ -45,6 +45,7 @@ namespace {
 
 constexpr int kRB = 256;                  // rows per block
 constexpr int kWaves = 16;                // waves per workgroup
+constexpr int kPrefetchDiagsPerWave = 4;  // C diagonals per wave from which the metadata is prefetched
 
 // Per element type T (fp32 or complex fp32): kLead rows staged before the
 // block (one 128-byte line of C), kStage staged rows per A diagonal, kMax A
@@ -118,14 +119,17 @@ __device__ __forceinline__ void store_elem_nt(T* p, T v)
     __builtin_nontemporal_store(r, reinterpret_cast<Raw*>(p));
 }
 
-// 8 waves per SIMD (at most 64 VGPRs): two 16-wave workgroups per CU.
-template <typename T>
-__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(8))) void k_astat(
+// Prefetch: each diagonal's metadata loaded while the one before it runs
+// (for waves that walk many diagonals).  tail5: the last block also takes
+// the rows the line-aligned shift leaves after it (else one more block of
+// at most kLead - 1 rows per diagonal covers them).
+template <typename T, bool Prefetch>
+__global__ __launch_bounds__(64 * kWaves) void k_astat(
     int32_t n, const int32_t* __restrict__ A_off, const int64_t* __restrict__ A_starts, int32_t nA,
     const T* __restrict__ Av, const T* __restrict__ Bv, const int32_t* __restrict__ C_off,
     const int32_t* __restrict__ C_len, const int64_t* __restrict__ C_starts, int32_t nC,
     const int64_t* __restrict__ pair_ptr, const int4* __restrict__ records,
-    T* __restrict__ Cv, int32_t blocks, int32_t groups, int32_t per_xcd)
+    T* __restrict__ Cv, int32_t blocks, int32_t groups, int32_t per_xcd, int32_t tail5)
 {
     constexpr int kLead = Astat<T>::kLead, kStage = Astat<T>::kStage, kWords = Astat<T>::kWords;
     extern __shared__ float A_l[];   // [nA][kStage] elements: rows i0 - kLead .. i0 + kRB - 1
@@ -137,9 +141,10 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(8))
     // GPU), each staging the block's A rows.
     const int unit = (int)(blockIdx.x % kNumXcd) * per_xcd + (int)(blockIdx.x / kNumXcd);
     if (unit >= blocks * groups) return;
-    // the last block (5 rows per lane) first: dispatched with the first
-    // wave of workgroups, its longer work overlaps the others'
-    const int blk = (unit / groups + blocks - 1) % blocks, grp = unit % groups;
+    // with tail5 the last block (5 rows per lane) goes first: dispatched
+    // with the first wave of workgroups, its longer work overlaps the others'
+    const int blk = tail5 ? (unit / groups + blocks - 1) % blocks : unit / groups;
+    const int grp = unit % groups;
     const int r = (int)threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(r >> 6), lane = r & 63;
     const int i0 = blk * kRB;                       // n <= 2^30: rows fit int32
@@ -166,32 +171,40 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(8))
     __builtin_amdgcn_s_waitcnt(0);   // this wave's direct loads have landed in LDS
     __syncthreads();
 
-    // R rows per lane: 4, and 5 in the last block, whose staged window also
-    // holds the rows [i0 + kRB - s, n) that no later block covers (n <= i0 +
-    // kRB there): an extra block for them would cost a whole workgroup's
-    // time, which is set by the per-diagonal chain of loads, not by rows.
+    // R rows per lane: 4, and with tail5 5 in the last block, whose staged
+    // window also holds the rows [i0 + kRB - s, n) that no later block covers
+    // (n <= i0 + kRB there).
     auto run = [&](auto rows) {
         constexpr int R = decltype(rows)::value;
-        // A diagonal's metadata is loaded while the diagonal before it runs
-        // (index clamped rather than tested: a load under a branch is
-        // waited for where the branch joins).
+        // With Prefetch, a diagonal's metadata is loaded while the diagonal
+        // before it runs (index clamped rather than tested: a load under a
+        // branch is waited for where the branch joins).
         const int stride = groups * kWaves;
         int kc = grp * kWaves + wave;
         if (kc >= nC) return;
         int dcn = C_off[kc], lenn = C_len[kc];
         int64_t cstn = C_starts[kc], g0n = pair_ptr[kc], g1n = pair_ptr[kc + 1];
         for (; kc < nC; kc += stride) {
-            const int dc = dcn;
-            const int len = lenn;
-            const int64_t cst = cstn;
-            const int g0 = (int)g0n, g1 = (int)g1n;
-            {
+            int dc, len, g0, g1;
+            int64_t cst;
+            if constexpr (Prefetch) {
+                dc = dcn;
+                len = lenn;
+                cst = cstn;
+                g0 = (int)g0n;
+                g1 = (int)g1n;
                 const int kn = min(kc + stride, nC - 1);
                 dcn = C_off[kn];
                 lenn = C_len[kn];
                 cstn = C_starts[kn];
                 g0n = pair_ptr[kn];
                 g1n = pair_ptr[kn + 1];
+            } else {
+                dc = C_off[kc];
+                len = C_len[kc];
+                cst = C_starts[kc];
+                g0 = (int)pair_ptr[kc];
+                g1 = (int)pair_ptr[kc + 1];
             }
             const int mc = dc < 0 ? dc : 0;
             const int s = (int)((cst + mc) & (kLead - 1));   // C(i0 - s, ...) starts a line
@@ -257,7 +270,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(8))
             }
         }
     };
-    if (blk == blocks - 1)
+    if (tail5 && blk == blocks - 1)
         run(std::integral_constant<int, 5>{});
     else
         run(std::integral_constant<int, 4>{});
@@ -283,25 +296,54 @@ int launch_astat(const char* fn, int32_t n, const int32_t* A_off, const int64_t*
         !records || !C_vals)
         return fail(DIAGPU_ERR_ARG, "%s: a pointer is NULL", fn);
     const size_t lds = (size_t)nA * kStage * sizeof(T);
+    // Row blocks and their split: too few blocks to give every CU its
+    // workgroups (two, or one above kMax2 A diagonals) split each block's C
+    // diagonals over several workgroups (at most one per wave's worth of
+    // diagonals).
+    const int64_t slots = (nA <= kMax2 ? 2 : 1) * (int64_t)cu_count();
+    auto split = [&](int64_t blocks) {
+        if (blocks >= slots) return (int64_t)1;
+        return std::max<int64_t>(1, std::min<int64_t>(ceil_div<int64_t>(slots, blocks),
+                                                      ceil_div<int64_t>(c_ndiag, kWaves)));
+    };
+    // ceil((n + kLead) / kRB) blocks of 4 rows per lane, the last covering
+    // the rows the line-aligned shift leaves (at most kLead - 1 per
+    // diagonal); or ceil(n / kRB), the last block taking those rows as a 5th
+    // per lane, where that saves one of at most 8 rounds of workgroups on
+    // the GPU (config 5: 1025 blocks on 256 CUs take 5 rounds, 1024 take
+    // 4).  A workgroup's time is set by its waves' chains of loads per
+    // diagonal, not by its rows, so the short block can cost a full round;
+    // over more rounds the saving shrinks below the 5-row block's own cost
+    // (the 7-point stencil's square, 4097 blocks in 9 rounds: 1 us slower).
+    int64_t blocks = ceil_div<int64_t>((int64_t)n + kLead, kRB), groups = split(blocks);
+    int32_t tail5 = 0;
+    const int64_t b5 = ceil_div<int64_t>(n, kRB), g5 = split(b5);
+    const int64_t rounds = ceil_div<int64_t>(blocks * groups, slots);
+    if (b5 < blocks && ceil_div<int64_t>(b5 * g5, slots) < rounds && rounds <= 8) {
+        blocks = b5;
+        groups = g5;
+        tail5 = 1;
+    }
+    const int32_t per_xcd = (int32_t)ceil_div<int64_t>(blocks * groups, kNumXcd);
+    // the metadata prefetch pays where waves walk many diagonals (config 5:
+    // ~575 each) and costs where they walk one or two (the 7-point stencil's
+    // square: 25 C diagonals over 16 waves, 31 -> 34 us)
+    const bool prefetch = c_ndiag >= kPrefetchDiagsPerWave * groups * kWaves;
+    const void* kern = prefetch ? (const void*)k_astat<T, true> : (const void*)k_astat<T, false>;
     // more than 64 KiB of dynamic LDS must be allowed explicitly
-    const int st = check_hip(hipFuncSetAttribute((const void*)k_astat<T>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+    const int st = check_hip(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  kStage * kMax * (int)sizeof(T)), fn);
     if (st) return st;
-    const int32_t blocks = (int32_t)ceil_div<int64_t>(n, kRB);
-    // too few blocks to give every CU its workgroups (two, or one above
-    // kMax2 A diagonals): split each block's C diagonals over several (at
-    // most one per wave's worth of diagonals)
-    int32_t groups = 1;
-    const int64_t fill = (nA <= kMax2 ? 2 : 1) * (int64_t)cu_count();
-    if (blocks < fill)
-        groups = (int32_t)std::max<int64_t>(1, std::min<int64_t>(ceil_div<int64_t>(fill, blocks),
-                                                                 ceil_div<int64_t>(c_ndiag, kWaves)));
-    const int32_t per_xcd = (int32_t)ceil_div<int64_t>((int64_t)blocks * groups, kNumXcd);
-    hipLaunchKernelGGL(k_astat<T>, dim3((unsigned)(per_xcd * kNumXcd)), dim3(64 * kWaves), lds,
-                       as_stream(stream), n, A_off, A_starts, nA, A_vals, B_vals, C_off, C_len,
-                       C_starts, (int32_t)c_ndiag, pair_ptr,
-                       reinterpret_cast<const int4*>(records), C_vals, blocks, groups, per_xcd);
+    const dim3 grid((unsigned)(per_xcd * kNumXcd)), block(64 * kWaves);
+    const int4* rec = reinterpret_cast<const int4*>(records);
+    if (prefetch)
+        hipLaunchKernelGGL((k_astat<T, true>), grid, block, lds, as_stream(stream), n, A_off,
+                           A_starts, nA, A_vals, B_vals, C_off, C_len, C_starts, (int32_t)c_ndiag,
+                           pair_ptr, rec, C_vals, (int32_t)blocks, (int32_t)groups, per_xcd, tail5);
+    else
+        hipLaunchKernelGGL((k_astat<T, false>), grid, block, lds, as_stream(stream), n, A_off,
+                           A_starts, nA, A_vals, B_vals, C_off, C_len, C_starts, (int32_t)c_ndiag,
+                           pair_ptr, rec, C_vals, (int32_t)blocks, (int32_t)groups, per_xcd, tail5);
     return check_launch(fn);
 }
 

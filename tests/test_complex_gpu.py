@@ -374,6 +374,7 @@ def _offsets(rng, cnt, lo, hi):
     (5000, "maxA"),         # DIAGPU_ASTAT_MAX_A_C64 A diagonals
     (1, "one"),             # a 1 x 1 matrix: one block, 16 lead rows before row 0
     (3, "three"),           # every diagonal of a 3 x 3 matrix
+    (1 << 17, "tail"),      # 512 blocks, the last with 5 rows per lane (513 would take 2 rounds)
 ])
 def test_complex_astat_same_bits_as_gather(dev, oracle, n, case):
     """The complex A-stationary kernel returns the complex gather's C bit for
@@ -394,6 +395,8 @@ def test_complex_astat_same_bits_as_gather(dev, oracle, n, case):
         oa, ob = [0], [0]
     elif case == "three":
         oa, ob = [-2, -1, 0, 1, 2], [-2, 0, 1]
+    elif case == "tail":
+        oa, ob = _offsets(rng, 30, -3000, 3000), _offsets(rng, 10, -600, 600)
     else:
         oa, ob = _offsets(rng, _lib.ASTAT_MAX_A_C64, -2000, 2000), _offsets(rng, 9, -100, 100)
     A = _complexify(workloads.hm_random(n, oa, seed=31, device=dev), 3)

@@ -410,6 +410,7 @@ def _random_offsets(rng, cnt, lo, hi, with_zero=True):
     (5000, "maxA"),         # DIAGPU_ASTAT_MAX_A A diagonals
     (1, "one"),             # a 1 x 1 matrix: one block, 32 lead rows before row 0
     (3, "three"),           # every diagonal of a 3 x 3 matrix
+    (1 << 17, "tail"),      # 512 blocks, the last with 5 rows per lane (513 would take 2 rounds)
 ])
 def test_astat_kernel_same_bits_as_gather(dev, oracle, n, case):
     """The A-stationary kernel returns the gather kernel's C bit for bit
@@ -430,6 +431,9 @@ def test_astat_kernel_same_bits_as_gather(dev, oracle, n, case):
         offs_a, offs_b = [0], [0]
     elif case == "three":
         offs_a, offs_b = [-2, -1, 0, 1, 2], [-2, 0, 1]
+    elif case == "tail":
+        offs_a = _random_offsets(rng, 40, -3000, 3000)
+        offs_b = _random_offsets(rng, 12, -600, 600)
     else:
         offs_a = _random_offsets(rng, _lib.ASTAT_MAX_A, -2000, 2000, with_zero=False)
         offs_b = _random_offsets(rng, 9, -100, 100)
