@@ -499,7 +499,7 @@ def time_propagator(grid: str = "3d", order: int = 6, dt: float = 0.02, m: int =
                                  if kry_ms > apply_ms else None)}
 
 
-def time_gemm_diag(n: int = 4096, hb: int = 10, reps: int = 100):
+def time_gemm_diag(n: int = 4096, hb: int = 10, reps: int = 100, cpu_seconds: float = 0.0):
     """gemm_diag on row-packed operands (gemm_diag/gemm_diag.cu:9-15) with the
     reference driver's default shape (n = 4096, offsets -hb..hb, values
     U(0.5, 1.5), gemm_diag.cu:467-486): the plan once, then `reps` timed
@@ -507,7 +507,10 @@ def time_gemm_diag(n: int = 4096, hb: int = 10, reps: int = 100):
     including the fp32 MFMA band kernel with its utilisation (useful /
     issued flops from its tile geometry).  The reference kernel has no
     tensor-core instructions (products in shared memory, a sequential
-    reduction and atomicAdd)."""
+    reduction and atomicAdd).  With cpu_seconds > 0 the oracle's OpenMP
+    SpGEMM loop runs the same plan over the same row-packed operands on the
+    host cores beside it."""
+    import types
     import torch
     from diagpu_amd.spgemm import gemm_diag
     offs = list(range(-hb, hb + 1))
@@ -550,7 +553,11 @@ def time_gemm_diag(n: int = 4096, hb: int = 10, reps: int = 100):
             # useful / issued flops of the kernel that ran; None when that kernel
             # issues no MFMA (the MFMA band kernel's figure is under kernels)
             "mfma_utilisation": (round(plan.mfma_utilisation(), 4) if kern == "band_mfma" else None),
-            "kernels": kernels}
+            "kernels": kernels,
+            # the plan's pair starts index the row-packed arrays directly
+            "cpu_baseline": (cpu_spgemm_baseline(plan, types.SimpleNamespace(values=DA),
+                                                 types.SimpleNamespace(values=DB), cpu_seconds)
+                             if cpu_seconds > 0 else None)}
 
 
 def copy_calibration(steps: int):
@@ -665,6 +672,13 @@ def main(argv=None) -> int:
             try:
                 res = time_spmv(cfg, dt, 200, 20, args.seed, 0, xt)
                 rec = spmv_record(cfg, dt, res, xt)
+                if cfg in (1, 3) and dt == torch.float32 and args.cpu_seconds > 0:
+                    c = cpu_spmv_baseline(res["R"], min(2.0, args.cpu_seconds))
+                    rec["cpu_baseline"] = {
+                        "value": round(c["gbs"], 2), "unit": "GB/s", "cores": c["threads"],
+                        **host_cores(), "kind": "port",
+                        "sample": f"{c['reps']} full SpMVs of the config-{cfg} matrix with the "
+                                  f"oracle's OpenMP DIA loop, {c['ms']:.3f} ms each"}
                 extras[f"spmv_cfg{cfg}_{rec['dtype']}"] = rec
                 log(f"extra spmv cfg{cfg} {rec['dtype']}: {res['gbs']:.1f} GB/s")
                 del res
@@ -707,7 +721,7 @@ def main(argv=None) -> int:
             extras["taylor_chain"] = {"error": repr(e)}
         for n_gd, reps_gd in ((4096, 100), (1 << 20, 20)):
             try:
-                rec = time_gemm_diag(n_gd, 10, reps_gd)
+                rec = time_gemm_diag(n_gd, 10, reps_gd, cpu_seconds=min(2.0, args.cpu_seconds))
                 extras[rec["workload"]] = rec
                 log(f"extra {rec['workload']}: {rec['numeric_ms']} ms, {rec['GFLOPs']} GFLOP/s")
             except Exception as e:
