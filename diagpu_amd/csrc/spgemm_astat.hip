@@ -43,14 +43,16 @@
 namespace diagpu {
 namespace {
 
-constexpr int kRB = 256;                  // rows per block
 constexpr int kWaves = 16;                // waves per workgroup
+constexpr int kForceR = 0;                // rows per lane forced (0: chosen per launch)
 constexpr int kPrefetchDiagsPerWave = 4;  // C diagonals per wave from which the metadata is prefetched
 
-// Per element type T (fp32 or complex fp32): kLead rows staged before the
-// block (one 128-byte line of C), kStage staged rows per A diagonal, kMax A
-// diagonals in 160 KiB of LDS and kMax2 in 80 KiB (two workgroups per CU).
-template <typename T> struct Astat {
+// Per element type T (fp32 or complex fp32) and R rows per lane: blocks of
+// kRB = 64 R rows, kLead rows staged before the block (one 128-byte line of
+// C), kStage staged rows per A diagonal, kMax A diagonals in 160 KiB of LDS
+// and kMax2 in 80 KiB (two workgroups per CU).
+template <typename T, int R = 4> struct Astat {
+    static constexpr int kRB = 64 * R;
     static constexpr int kLead = (int)(128 / sizeof(T));
     static constexpr int kStage = kRB + kLead;
     static constexpr int kWords = (int)(sizeof(T) / 4);   // dwords per element
@@ -123,7 +125,7 @@ __device__ __forceinline__ void store_elem_nt(T* p, T v)
 // (for waves that walk many diagonals).  tail5: the last block also takes
 // the rows the line-aligned shift leaves after it (else one more block of
 // at most kLead - 1 rows per diagonal covers them).
-template <typename T, bool Prefetch>
+template <typename T, bool Prefetch, int R>
 __global__ __launch_bounds__(64 * kWaves) void k_astat(
     int32_t n, const int32_t* __restrict__ A_off, const int64_t* __restrict__ A_starts, int32_t nA,
     const T* __restrict__ Av, const T* __restrict__ Bv, const int32_t* __restrict__ C_off,
@@ -131,7 +133,8 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
     const int64_t* __restrict__ pair_ptr, const int4* __restrict__ records,
     T* __restrict__ Cv, int32_t blocks, int32_t groups, int32_t per_xcd, int32_t tail5)
 {
-    constexpr int kLead = Astat<T>::kLead, kStage = Astat<T>::kStage, kWords = Astat<T>::kWords;
+    constexpr int kRB = Astat<T, R>::kRB, kLead = Astat<T, R>::kLead;
+    constexpr int kStage = Astat<T, R>::kStage, kWords = Astat<T, R>::kWords;
     extern __shared__ float A_l[];   // [nA][kStage] elements: rows i0 - kLead .. i0 + kRB - 1
     const T* A_t = reinterpret_cast<const T*>(A_l);
     // workgroup b on XCD b mod 8: each XCD owns a contiguous range of work
@@ -171,11 +174,11 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
     __builtin_amdgcn_s_waitcnt(0);   // this wave's direct loads have landed in LDS
     __syncthreads();
 
-    // R rows per lane: 4, and with tail5 5 in the last block, whose staged
-    // window also holds the rows [i0 + kRB - s, n) that no later block covers
-    // (n <= i0 + kRB there).
+    // RR rows per lane: R, and with tail5 R + 1 in the last block, whose
+    // staged window also holds the rows [i0 + kRB - s, n) that no later block
+    // covers (n <= i0 + kRB there).
     auto run = [&](auto rows) {
-        constexpr int R = decltype(rows)::value;
+        constexpr int RR = decltype(rows)::value;
         // With Prefetch, a diagonal's metadata is loaded while the diagonal
         // before it runs (index clamped rather than tested: a load under a
         // branch is waited for where the branch joins).
@@ -210,110 +213,126 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
             const int s = (int)((cst + mc) & (kLead - 1));   // C(i0 - s, ...) starts a line
             const int pb = i0 - s + lane + mc;          // C position of the lane's first row
             const int ab = kLead - s + lane;            // its staged A row
-            T acc[R];
+            T acc[RR];
 #pragma unroll
-            for (int j = 0; j < R; ++j) acc[j] = zero_of<T>();
+            for (int j = 0; j < RR; ++j) acc[j] = zero_of<T>();
             // one term: B by a clamped (always valid) load, A from LDS (row
-            // 4 of a lane past the window, p >= len there, reads row 0), the
+            // R of a lane past the window, p >= len there, reads row 0), the
             // multiply-add kept where both operands hold the element
             auto term = [&](const int4& e, int hi, int j, T& b, T& a, bool& ok) {
                 const int p = pb + 64 * j;
                 ok = p >= e.y && p < hi;
                 b = load_elem<T, false>(Bv + (int64_t)e.w + min(max(p, e.y), e.z - 1));
-                a = A_t[e.x * kStage + (j < 4 || lane < s ? ab + 64 * j : ab)];
+                a = A_t[e.x * kStage + (j < R || lane < s ? ab + 64 * j : ab)];
             };
             // The values of a batch are pinned once all its loads are issued,
             // so the compiler cannot turn a masked multiply-add into a branch
             // around its own load (each such branch ends in a full vmcnt(0)
             // drain: gfx9 counts loads in order).
-            // two entries' loads in flight (one for complex values with 5
-            // rows: 64 VGPRs)
-            constexpr int U = (R == 5 && sizeof(T) == 8) ? 1 : 2;
+            // two entries' loads in flight, or one where two would hold more
+            // than 8 dwords per lane per entry (within 64 VGPRs: two 16-wave
+            // workgroups per CU)
+            constexpr int U = (RR * kWords <= 8) ? 2 : 1;
             int g = g0;
             for (; U == 2 && g + 2 <= g1; g += 2) {
-                T bv[2][R], av[2][R];
-                bool ok[2][R];
+                T bv[2][RR], av[2][RR];
+                bool ok[2][RR];
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
                     const int4 e = records[g + u];
                     const int hi = min(e.z, len);
 #pragma unroll
-                    for (int j = 0; j < R; ++j) term(e, hi, j, bv[u][j], av[u][j], ok[u][j]);
+                    for (int j = 0; j < RR; ++j) term(e, hi, j, bv[u][j], av[u][j], ok[u][j]);
                 }
 #pragma unroll
                 for (int u = 0; u < 2; ++u)
 #pragma unroll
-                    for (int j = 0; j < R; ++j) { pin(bv[u][j]); pin(av[u][j]); }
+                    for (int j = 0; j < RR; ++j) { pin(bv[u][j]); pin(av[u][j]); }
 #pragma unroll
                 for (int u = 0; u < 2; ++u)
 #pragma unroll
-                    for (int j = 0; j < R; ++j)
+                    for (int j = 0; j < RR; ++j)
                         acc[j] = sel(ok[u][j], mad(acc[j], av[u][j], bv[u][j]), acc[j]);
             }
             for (; g < g1; ++g) {
                 const int4 e = records[g];
                 const int hi = min(e.z, len);
-                T bv[R], av[R];
-                bool ok[R];
+                T bv[RR], av[RR];
+                bool ok[RR];
 #pragma unroll
-                for (int j = 0; j < R; ++j) term(e, hi, j, bv[j], av[j], ok[j]);
+                for (int j = 0; j < RR; ++j) term(e, hi, j, bv[j], av[j], ok[j]);
 #pragma unroll
-                for (int j = 0; j < R; ++j) { pin(bv[j]); pin(av[j]); }
+                for (int j = 0; j < RR; ++j) { pin(bv[j]); pin(av[j]); }
 #pragma unroll
-                for (int j = 0; j < R; ++j) acc[j] = sel(ok[j], mad(acc[j], av[j], bv[j]), acc[j]);
+                for (int j = 0; j < RR; ++j) acc[j] = sel(ok[j], mad(acc[j], av[j], bv[j]), acc[j]);
             }
             T* __restrict__ cp = Cv + cst;
 #pragma unroll
-            for (int j = 0; j < R; ++j) {
+            for (int j = 0; j < RR; ++j) {
                 const int p = pb + 64 * j;
                 if (p >= 0 && p < len) store_elem_nt(cp + p, acc[j]);
             }
         }
     };
     if (tail5 && blk == blocks - 1)
-        run(std::integral_constant<int, 5>{});
+        run(std::integral_constant<int, R + 1>{});
     else
-        run(std::integral_constant<int, 4>{});
+        run(std::integral_constant<int, R>{});
 }
 
-template <typename T>
-int launch_astat(const char* fn, int32_t n, const int32_t* A_off, const int64_t* A_starts,
-                 int32_t nA, const T* A_vals, const T* B_vals, const int32_t* C_off,
-                 const int32_t* C_len, const int64_t* C_starts, int64_t c_ndiag,
-                 const int64_t* pair_ptr, const int32_t* records, int64_t n_pairs, T* C_vals,
-                 void* stream)
+// Workgroups of k_astat<T, *, R> that fit a CU by registers (its LDS aside),
+// looked up once per instantiation: the 16-wave workgroups fit twice at up
+// to 64 VGPRs, once above.
+template <typename T, int R> int wgs_by_regs()
 {
-    constexpr int kLead = Astat<T>::kLead, kStage = Astat<T>::kStage;
-    constexpr int kMax = Astat<T>::kMax, kMax2 = Astat<T>::kMax2;
-    if (n < 1 || n > (1 << 30) || nA < 1 || c_ndiag < 0 || c_ndiag > 2 * (int64_t)n - 1 ||
-        n_pairs < 0 || n_pairs > INT_MAX)
-        return fail(DIAGPU_ERR_ARG, "%s: bad sizes (n=%d nA=%d c_ndiag=%lld n_pairs=%lld)", fn,
-                    n, nA, (long long)c_ndiag, (long long)n_pairs);
-    if (nA > kMax)
-        return fail(DIAGPU_ERR_CAPACITY, "%s: %d A diagonals, at most %d fit in LDS", fn, nA, kMax);
-    if (c_ndiag == 0) return DIAGPU_OK;
-    if (!A_off || !A_starts || !A_vals || !B_vals || !C_off || !C_len || !C_starts || !pair_ptr ||
-        !records || !C_vals)
-        return fail(DIAGPU_ERR_ARG, "%s: a pointer is NULL", fn);
+    static const int v = [] {
+        int a = 0, b = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, (const void*)k_astat<T, false, R>,
+                                                        64 * kWaves, 0) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, (const void*)k_astat<T, true, R>,
+                                                        64 * kWaves, 0) != hipSuccess)
+            return 1;
+        return std::max(1, std::min(a, b));
+    }();
+    return v;
+}
+
+// Workgroup slots of k_astat<T, *, R> on the GPU for nA A diagonals: by
+// registers and by the LDS the staged A rows take (160 KiB per CU).
+template <typename T, int R> int64_t astat_slots(int32_t nA)
+{
+    const int64_t lds = (int64_t)nA * Astat<T, R>::kStage * (int64_t)sizeof(T);
+    const int64_t by_lds = std::max<int64_t>(1, (160 * 1024) / lds);
+    return std::min<int64_t>(wgs_by_regs<T, R>(), by_lds) * (int64_t)cu_count();
+}
+
+// One launch of k_astat<T, *, R> (arguments checked by the caller).
+template <typename T, int R>
+int launch_rows(const char* fn, int32_t n, const int32_t* A_off, const int64_t* A_starts,
+                int32_t nA, const T* A_vals, const T* B_vals, const int32_t* C_off,
+                const int32_t* C_len, const int64_t* C_starts, int64_t c_ndiag,
+                const int64_t* pair_ptr, const int32_t* records, T* C_vals, void* stream)
+{
+    constexpr int kRB = Astat<T, R>::kRB, kLead = Astat<T, R>::kLead, kStage = Astat<T, R>::kStage;
+    constexpr int kMax = Astat<T, R>::kMax;
     const size_t lds = (size_t)nA * kStage * sizeof(T);
     // Row blocks and their split: too few blocks to give every CU its
-    // workgroups (two, or one above kMax2 A diagonals) split each block's C
-    // diagonals over several workgroups (at most one per wave's worth of
-    // diagonals).
-    const int64_t slots = (nA <= kMax2 ? 2 : 1) * (int64_t)cu_count();
+    // workgroups split each block's C diagonals over several workgroups (at
+    // most one per wave's worth of diagonals).
+    const int64_t slots = astat_slots<T, R>(nA);
     auto split = [&](int64_t blocks) {
         if (blocks >= slots) return (int64_t)1;
         return std::max<int64_t>(1, std::min<int64_t>(ceil_div<int64_t>(slots, blocks),
                                                       ceil_div<int64_t>(c_ndiag, kWaves)));
     };
-    // ceil((n + kLead) / kRB) blocks of 4 rows per lane, the last covering
+    // ceil((n + kLead) / kRB) blocks of R rows per lane, the last covering
     // the rows the line-aligned shift leaves (at most kLead - 1 per
-    // diagonal); or ceil(n / kRB), the last block taking those rows as a 5th
-    // per lane, where that saves one of at most 8 rounds of workgroups on
-    // the GPU (config 5: 1025 blocks on 256 CUs take 5 rounds, 1024 take
+    // diagonal); or ceil(n / kRB), the last block taking those rows as one
+    // more per lane, where that saves one of at most 8 rounds of workgroups
+    // on the GPU (config 5: 1025 blocks on 256 CUs take 5 rounds, 1024 take
     // 4).  A workgroup's time is set by its waves' chains of loads per
     // diagonal, not by its rows, so the short block can cost a full round;
-    // over more rounds the saving shrinks below the 5-row block's own cost
+    // over more rounds the saving shrinks below the longer block's own cost
     // (the 7-point stencil's square, 4097 blocks in 9 rounds: 1 us slower).
     int64_t blocks = ceil_div<int64_t>((int64_t)n + kLead, kRB), groups = split(blocks);
     int32_t tail5 = 0;
@@ -329,7 +348,7 @@ int launch_astat(const char* fn, int32_t n, const int32_t* A_off, const int64_t*
     // ~575 each) and costs where they walk one or two (the 7-point stencil's
     // square: 25 C diagonals over 16 waves, 31 -> 34 us)
     const bool prefetch = c_ndiag >= kPrefetchDiagsPerWave * groups * kWaves;
-    const void* kern = prefetch ? (const void*)k_astat<T, true> : (const void*)k_astat<T, false>;
+    const void* kern = prefetch ? (const void*)k_astat<T, true, R> : (const void*)k_astat<T, false, R>;
     // more than 64 KiB of dynamic LDS must be allowed explicitly
     const int st = check_hip(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  kStage * kMax * (int)sizeof(T)), fn);
@@ -337,14 +356,71 @@ int launch_astat(const char* fn, int32_t n, const int32_t* A_off, const int64_t*
     const dim3 grid((unsigned)(per_xcd * kNumXcd)), block(64 * kWaves);
     const int4* rec = reinterpret_cast<const int4*>(records);
     if (prefetch)
-        hipLaunchKernelGGL((k_astat<T, true>), grid, block, lds, as_stream(stream), n, A_off,
+        hipLaunchKernelGGL((k_astat<T, true, R>), grid, block, lds, as_stream(stream), n, A_off,
                            A_starts, nA, A_vals, B_vals, C_off, C_len, C_starts, (int32_t)c_ndiag,
                            pair_ptr, rec, C_vals, (int32_t)blocks, (int32_t)groups, per_xcd, tail5);
     else
-        hipLaunchKernelGGL((k_astat<T, false>), grid, block, lds, as_stream(stream), n, A_off,
+        hipLaunchKernelGGL((k_astat<T, false, R>), grid, block, lds, as_stream(stream), n, A_off,
                            A_starts, nA, A_vals, B_vals, C_off, C_len, C_starts, (int32_t)c_ndiag,
                            pair_ptr, rec, C_vals, (int32_t)blocks, (int32_t)groups, per_xcd, tail5);
     return check_launch(fn);
+}
+
+template <typename T>
+int launch_astat(const char* fn, int32_t n, const int32_t* A_off, const int64_t* A_starts,
+                 int32_t nA, const T* A_vals, const T* B_vals, const int32_t* C_off,
+                 const int32_t* C_len, const int64_t* C_starts, int64_t c_ndiag,
+                 const int64_t* pair_ptr, const int32_t* records, int64_t n_pairs, T* C_vals,
+                 void* stream)
+{
+    constexpr int kMax = Astat<T>::kMax;
+    if (n < 1 || n > (1 << 30) || nA < 1 || c_ndiag < 0 || c_ndiag > 2 * (int64_t)n - 1 ||
+        n_pairs < 0 || n_pairs > INT_MAX)
+        return fail(DIAGPU_ERR_ARG, "%s: bad sizes (n=%d nA=%d c_ndiag=%lld n_pairs=%lld)", fn,
+                    n, nA, (long long)c_ndiag, (long long)n_pairs);
+    if (nA > kMax)
+        return fail(DIAGPU_ERR_CAPACITY, "%s: %d A diagonals, at most %d fit in LDS", fn, nA, kMax);
+    if (c_ndiag == 0) return DIAGPU_OK;
+    if (!A_off || !A_starts || !A_vals || !B_vals || !C_off || !C_len || !C_starts || !pair_ptr ||
+        !records || !C_vals)
+        return fail(DIAGPU_ERR_ARG, "%s: a pointer is NULL", fn);
+#define DIAGPU_ASTAT_LAUNCH(RV)                                                                   \
+    launch_rows<T, RV>(fn, n, A_off, A_starts, nA, A_vals, B_vals, C_off, C_len, C_starts, c_ndiag, \
+                       pair_ptr, records, C_vals, stream)
+    // Rows per lane.  A wave's time per C diagonal is a chain of dependent
+    // loads; longer blocks put more rows into each chain and need fewer
+    // rounds of workgroups, where n gives at least 4 rounds of them.
+    // Measured (fp32, us, R = 4 / 8 / 16): config 2's square (13 C
+    // diagonals) 90 / 71 / 60; the 7-point stencil's square 35 / 33 / 28.5
+    // and H H^2 (63 C diagonals) 86.5 / 82 / 75.5, H H^4 and H H^5 (231,
+    // 377) 524 / 483 / 492 and 912 / 856 / 902; config 4 44 / 47 / 43.
+    // Fewer blocks lose at small n (gemm_diag's band at n = 65536: 13.4 /
+    // 18 / 21) and where the longer window costs a workgroup per CU (the
+    // 64-diagonal band at n = 2^18: 379 / 405 / -).  Complex values, R = 8
+    // (80 VGPRs: one workgroup per CU): config 2's square 223 -> 194,
+    // config 4 78 -> 83.
+    auto rounds_ok = [&](int rows, int64_t slots) {
+        return ceil_div<int64_t>(n, 64 * rows) >= 4 * slots;
+    };
+    if constexpr (kForceR == 16 && sizeof(T) == 4) {
+        if (nA <= Astat<T, 16>::kMax) return DIAGPU_ASTAT_LAUNCH(16);
+    } else if constexpr (kForceR == 8) {
+        if (nA <= Astat<T, 8>::kMax) return DIAGPU_ASTAT_LAUNCH(8);
+    } else if constexpr (kForceR == 0 && sizeof(T) == 4) {
+        // few, short C diagonals: 16 rows per lane
+        if (c_ndiag <= 4 * kWaves && n_pairs <= 4 * c_ndiag && nA <= Astat<T, 16>::kMax &&
+            rounds_ok(16, astat_slots<T, 16>(nA)))
+            return DIAGPU_ASTAT_LAUNCH(16);
+        // many C diagonals: 8, where two workgroups still fit a CU
+        if (c_ndiag > 4 * kWaves && nA <= Astat<T, 8>::kMax2 && rounds_ok(8, astat_slots<T, 8>(nA)))
+            return DIAGPU_ASTAT_LAUNCH(8);
+    } else if constexpr (kForceR == 0) {
+        // complex: 8 where every wave has at most one C diagonal
+        if (c_ndiag <= kWaves && nA <= Astat<T, 8>::kMax && rounds_ok(8, astat_slots<T, 8>(nA)))
+            return DIAGPU_ASTAT_LAUNCH(8);
+    }
+    return DIAGPU_ASTAT_LAUNCH(4);
+#undef DIAGPU_ASTAT_LAUNCH
 }
 
 }  // namespace

@@ -191,10 +191,11 @@ class SpgemmPlan:
         addressable with int32, and the plan reuses the staged A runs:
 
           fp32:      >= 16 entries per A diagonal, or >= 32 entries with
-                     >= 4 per A diagonal and >= 1.5 per C diagonal;
+                     >= 4 per A diagonal and >= 1.5 per C diagonal, or
+                     n >= 2^22;
           complex64: n >= 2^18 with >= 16 C diagonals (every wave of a
                      workgroup busy), or >= 32 entries with >= 4 per A
-                     diagonal.
+                     diagonal, or n >= 2^22.
 
         The thresholds separate what was measured against the gather on
         MI355X: fp32 stencil products gain 26-30 % (9-point square at
@@ -208,18 +209,22 @@ class SpgemmPlan:
         operand runs at its items' edges), and below that where each A
         diagonal feeds >= 4 entries.  (Ratios measured one buffer set at a
         time; under the benchmark's rotating sets complex config 4 gains
-        4 %: 128 vs 133 us.)"""
+        4 %: 128 vs 133 us.)  From n = 2^22 the kernel's longer row blocks
+        (16 or 8 rows per lane for few, short C diagonals) win on every
+        measured product, config 2's square included (rotating sets: fp32
+        92 vs 102 us, complex 183 vs 226)."""
         na = self.A.offsets.numel()
         inf = self.info
         if inf.c_ndiag == 0 or self.n < 4096:
             return False
         reuse = inf.n_pairs >= 32 and inf.n_pairs >= 4 * na
+        big = self.n >= 1 << 22
         if dtype == torch.float32:
-            ok = na <= _lib.ASTAT_MAX_A and (inf.n_pairs >= 16 * na
+            ok = na <= _lib.ASTAT_MAX_A and (inf.n_pairs >= 16 * na or big
                                              or (reuse and 2 * inf.n_pairs >= 3 * inf.c_ndiag))
         elif dtype == torch.complex64:
             ok = na <= _lib.ASTAT_MAX_A_C64 and ((self.n >= 1 << 18 and inf.c_ndiag >= 16)
-                                                 or reuse)
+                                                 or reuse or big)
         else:
             ok = False
         if not ok:

@@ -305,10 +305,11 @@ public:
         const int64_t np = info_.n_pairs, nc = info_.c_ndiag, na = a_ndiag;
         const bool sized = nc > 0 && int64_t(n) >= 4096;
         const bool reuse = np >= 32 && np >= 4 * na;
+        const bool big = int64_t(n) >= (1 << 22);
         astat_auto_ = !uses_band() && sized && na <= DIAGPU_ASTAT_MAX_A &&
-                      (np >= 16 * na || (reuse && 2 * np >= 3 * nc));
+                      (np >= 16 * na || big || (reuse && 2 * np >= 3 * nc));
         astat_auto_c64_ = sized && na <= DIAGPU_ASTAT_MAX_A_C64 &&
-                          ((int64_t(n) >= (1 << 18) && nc >= 16) || reuse);
+                          ((int64_t(n) >= (1 << 18) && nc >= 16) || reuse || big);
         if (astat_auto_ || astat_auto_c64_) {
             try {
                 prepare_astat(stream);
@@ -330,11 +331,11 @@ public:
     // DIAGPU_ASTAT_MAX_A diagonals, n >= 4096, and the plan has >= 16
     // entries per A diagonal, or >= 32 entries with >= 4 per A diagonal and
     // >= 1.5 per C diagonal (config 4, 63 entries over 47 C diagonals, is a
-    // near-streaming product that the gather runs as fast).
+    // near-streaming product that the gather runs as fast), or n >= 2^22.
     bool uses_astat() const { return astat_auto_; }
     // The same for complex64 values: A has at most DIAGPU_ASTAT_MAX_A_C64
     // diagonals, n >= 4096, and n >= 2^18 with >= 16 C diagonals, or >= 32
-    // entries with >= 4 per A diagonal.
+    // entries with >= 4 per A diagonal, or n >= 2^22.
     bool uses_astat_c64() const { return astat_auto_c64_; }
 
     // C_vals (device, info().c_nnz values) = A * B; asynchronous on `stream`

@@ -375,6 +375,7 @@ def _offsets(rng, cnt, lo, hi):
     (1, "one"),             # a 1 x 1 matrix: one block, 16 lead rows before row 0
     (3, "three"),           # every diagonal of a 3 x 3 matrix
     (1 << 17, "tail"),      # 512 blocks, the last with 5 rows per lane (513 would take 2 rounds)
+    (1 << 20, "short"),     # 5 C diagonals: 8 rows per lane, 2048 blocks, the last 9
 ])
 def test_complex_astat_same_bits_as_gather(dev, oracle, n, case):
     """The complex A-stationary kernel returns the complex gather's C bit for
@@ -397,6 +398,8 @@ def test_complex_astat_same_bits_as_gather(dev, oracle, n, case):
         oa, ob = [-2, -1, 0, 1, 2], [-2, 0, 1]
     elif case == "tail":
         oa, ob = _offsets(rng, 30, -3000, 3000), _offsets(rng, 10, -600, 600)
+    elif case == "short":
+        oa = ob = [-512, 0, 512]
     else:
         oa, ob = _offsets(rng, _lib.ASTAT_MAX_A_C64, -2000, 2000), _offsets(rng, 9, -100, 100)
     A = _complexify(workloads.hm_random(n, oa, seed=31, device=dev), 3)
@@ -433,8 +436,8 @@ def test_complex_astat_real_values_equal_real_kernel(dev):
 def test_complex_astat_choice_and_capacity(dev):
     """auto takes the complex A-stationary kernel where A fits (at most
     DIAGPU_ASTAT_MAX_A_C64 diagonals), n >= 4096, and n >= 2^18 with >= 16
-    C diagonals or the plan has >= 32 entries with >= 4 per A diagonal; the
-    gather otherwise.  More A diagonals are refused with DIAGPU_ERR_CAPACITY
+    C diagonals, or the plan has >= 32 entries with >= 4 per A diagonal, or
+    n >= 2^22; the gather otherwise.  More A diagonals are refused with DIAGPU_ERR_CAPACITY
     before any launch; the band kernel takes fp32 only."""
     from diagpu_amd import _lib
     from diagpu_amd.spgemm import SpgemmPlan
@@ -456,6 +459,8 @@ def test_complex_astat_choice_and_capacity(dev):
     five = workloads.hm_random(1 << 18, [-512, -1, 0, 1, 512], seed=9, device=dev)
     p5 = SpgemmPlan(_complexify(five, 1), _complexify(five, 2))    # 13 C diagonals, 25 entries
     assert p5.kernel_for(torch.complex64) == "gather"
+    P2 = _complexify(workloads.recon_to_hm(workloads.spmv_config(2, seed=1, device=dev)), 1)
+    assert SpgemmPlan(P2, P2).kernel_for(torch.complex64) == "astat"   # the same at n = 2^22
     wide = _complexify(workloads.hm_random(4096, _offsets(rng, _lib.ASTAT_MAX_A_C64 + 1, -300, 300),
                                            seed=6, device=dev), 2)
     pw = SpgemmPlan(wide, wide)

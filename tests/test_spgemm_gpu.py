@@ -411,6 +411,8 @@ def _random_offsets(rng, cnt, lo, hi, with_zero=True):
     (1, "one"),             # a 1 x 1 matrix: one block, 32 lead rows before row 0
     (3, "three"),           # every diagonal of a 3 x 3 matrix
     (1 << 17, "tail"),      # 512 blocks, the last with 5 rows per lane (513 would take 2 rounds)
+    (1 << 20, "short"),     # 25 short C diagonals: 16 rows per lane, 1024 blocks, the last 17
+    (1 << 20, "many"),      # 7 x 40 diagonals, > 64 C diagonals: 8 rows per lane, the last 9
 ])
 def test_astat_kernel_same_bits_as_gather(dev, oracle, n, case):
     """The A-stationary kernel returns the gather kernel's C bit for bit
@@ -434,6 +436,11 @@ def test_astat_kernel_same_bits_as_gather(dev, oracle, n, case):
     elif case == "tail":
         offs_a = _random_offsets(rng, 40, -3000, 3000)
         offs_b = _random_offsets(rng, 12, -600, 600)
+    elif case == "short":
+        offs_a = offs_b = [-1024, -32, -1, 0, 1, 32, 1024]
+    elif case == "many":
+        offs_a = [-1024, -32, -1, 0, 1, 32, 1024]
+        offs_b = _random_offsets(rng, 40, -5000, 5000)
     else:
         offs_a = _random_offsets(rng, _lib.ASTAT_MAX_A, -2000, 2000, with_zero=False)
         offs_b = _random_offsets(rng, 9, -100, 100)
@@ -464,7 +471,8 @@ def test_astat_kernel_choice_and_capacity(dev):
     band over +-512 (64 entries per A diagonal), for gemm_diag's band below
     512 row blocks (21 per A diagonal) and for the 9-point stencil's square,
     the band kernel above 512 row blocks, the gather for config 4 (63
-    entries over 47 C diagonals) and the 5-point square (25 entries); more than
+    entries over 47 C diagonals) and the 5-point square (25 entries) below
+    n = 2^22, the A-stationary kernel for config 2's square; more than
     DIAGPU_ASTAT_MAX_A A diagonals are refused with DIAGPU_ERR_CAPACITY."""
     rng = np.random.default_rng(3)
     n = 1 << 18
@@ -493,6 +501,8 @@ def test_astat_kernel_choice_and_capacity(dev):
                        p9.multiply(S9.values, S9.values, kernel="gather").view(torch.int32))
     S5 = workloads.hm_random(1 << 16, [-256, -1, 0, 1, 256], 8, dev)
     assert SpgemmPlan(S5, S5).kernel_for() == "gather"          # 25 entries
+    P2 = workloads.recon_to_hm(workloads.spmv_config(2, seed=1, device=dev))
+    assert SpgemmPlan(P2, P2).kernel_for() == "astat"           # the same, at n = 2^22
     wide = workloads.hm_random(4096, _random_offsets(rng, _lib.ASTAT_MAX_A + 1, -300, 300), 6, dev)
     pw = SpgemmPlan(wide, wide)
     assert pw.kernel_for() != "astat"
