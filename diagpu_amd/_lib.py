@@ -145,7 +145,7 @@ PROTOTYPES: dict[str, tuple] = {
 
 # diagpu.h: DIAGPU_ASTAT_MAX_A, DIAGPU_ASTAT_MAX_A_C64, DIAGPU_SYMBOLIC_SCRATCH_BYTES
 ASTAT_MAX_A = 142
-ASTAT_MAX_A_C64 = 75
+ASTAT_MAX_A_C64 = 142
 SYMBOLIC_SCRATCH_BYTES = 40 << 20
 
 _lib: C.CDLL | None = None

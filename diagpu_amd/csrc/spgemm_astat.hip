@@ -59,8 +59,14 @@ template <typename T, int R = 4> struct Astat {
     static constexpr int kMax = (160 * 1024) / (kStage * (int)sizeof(T));
     static constexpr int kMax2 = (80 * 1024) / (kStage * (int)sizeof(T));
 };
-static_assert(Astat<float>::kMax == DIAGPU_ASTAT_MAX_A, "fp32 A diagonals in 160 KiB of LDS");
-static_assert(Astat<cf32>::kMax == DIAGPU_ASTAT_MAX_A_C64, "complex A diagonals in 160 KiB of LDS");
+// The A-diagonal capacity: fp32 at 4 rows per lane; complex at 2, the
+// blocks that take more than 4 rows' worth of complex A diagonals.
+template <typename T> constexpr int astat_cap()
+{
+    return sizeof(T) == 4 ? Astat<T, 4>::kMax : Astat<T, 2>::kMax;
+}
+static_assert(astat_cap<float>() == DIAGPU_ASTAT_MAX_A, "fp32 A diagonals in 160 KiB of LDS");
+static_assert(astat_cap<cf32>() == DIAGPU_ASTAT_MAX_A_C64, "complex A diagonals in 160 KiB of LDS");
 
 // records[g] = {a, lo, hi, b} for plan entry g; flag[0] set if an entry's A
 // start is no A diagonal's start, flag[1] if its B indices do not fit int32.
@@ -373,7 +379,7 @@ int launch_astat(const char* fn, int32_t n, const int32_t* A_off, const int64_t*
                  const int64_t* pair_ptr, const int32_t* records, int64_t n_pairs, T* C_vals,
                  void* stream)
 {
-    constexpr int kMax = Astat<T>::kMax;
+    constexpr int kMax = astat_cap<T>();
     if (n < 1 || n > (1 << 30) || nA < 1 || c_ndiag < 0 || c_ndiag > 2 * (int64_t)n - 1 ||
         n_pairs < 0 || n_pairs > INT_MAX)
         return fail(DIAGPU_ERR_ARG, "%s: bad sizes (n=%d nA=%d c_ndiag=%lld n_pairs=%lld)", fn,
@@ -398,11 +404,19 @@ int launch_astat(const char* fn, int32_t n, const int32_t* A_off, const int64_t*
     // 18 / 21) and where the longer window costs a workgroup per CU (the
     // 64-diagonal band at n = 2^18: 379 / 405 / -).  Complex values, R = 8
     // (80 VGPRs: one workgroup per CU): config 2's square 223 -> 194,
-    // config 4 78 -> 83.
+    // config 4 78 -> 83.  Complex A with more diagonals than 4 rows per lane
+    // hold takes 2 (config 5 with complex values: 6.15 ms against 7.06 on
+    // the gather); fp32 stays at 4 and at most DIAGPU_ASTAT_MAX_A diagonals
+    // (2 rows per lane over 142 fp32 A diagonals lost to the gather: 200 x 64
+    // at n = 2^18 3.17 against 2.64 ms).
     auto rounds_ok = [&](int rows, int64_t slots) {
         return ceil_div<int64_t>(n, 64 * rows) >= 4 * slots;
     };
-    if constexpr (kForceR == 16 && sizeof(T) == 4) {
+    if constexpr (sizeof(T) == 8)
+        if (nA > Astat<T, 4>::kMax) return DIAGPU_ASTAT_LAUNCH(2);
+    if constexpr (kForceR == 2) {
+        if (nA <= Astat<T, 2>::kMax) return DIAGPU_ASTAT_LAUNCH(2);
+    } else if constexpr (kForceR == 16 && sizeof(T) == 4) {
         if (nA <= Astat<T, 16>::kMax) return DIAGPU_ASTAT_LAUNCH(16);
     } else if constexpr (kForceR == 8) {
         if (nA <= Astat<T, 8>::kMax) return DIAGPU_ASTAT_LAUNCH(8);

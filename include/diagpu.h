@@ -349,9 +349,10 @@ DIAGPU_API int diagpu_spgemm_numeric_band_mfma_f32(
  * workgroups hold 288 rows of every A diagonal in LDS, 160 KiB at most (up to
  * 71 diagonals, 80 KiB, two workgroups share a CU; above, one). */
 #define DIAGPU_ASTAT_MAX_A 142
-/* The same for diagpu_spgemm_numeric_astat_c64: 272 complex rows per A
- * diagonal (two workgroups per CU up to 37 diagonals). */
-#define DIAGPU_ASTAT_MAX_A_C64 75
+/* The same for diagpu_spgemm_numeric_astat_c64: up to 75 A diagonals its
+ * workgroups hold 272 complex rows of each (two workgroups per CU up to 37),
+ * above that 144. */
+#define DIAGPU_ASTAT_MAX_A_C64 142
 
 /* For the A-stationary kernel, per plan (once): records[4g .. 4g+3] =
  * {a, lo, hi, b} for plan entry g: a the index of its A diagonal (looked up
@@ -381,9 +382,10 @@ DIAGPU_API int diagpu_spgemm_numeric_astat_f32(
 
 /* The same with complex64 values: the numeric phase of
  * diagpu_spgemm_numeric_c64 (same C, bit for bit), same records; each
- * workgroup holds the block's 256 rows plus the 16 before it; nA at most
- * DIAGPU_ASTAT_MAX_A_C64 (else DIAGPU_ERR_CAPACITY).  No reference
- * counterpart (the reference is real only). */
+ * workgroup holds a block of 256 rows (128 above 75 A diagonals) plus the
+ * 16 before it; nA at most DIAGPU_ASTAT_MAX_A_C64 (else
+ * DIAGPU_ERR_CAPACITY).  No reference counterpart (the reference is real
+ * only). */
 DIAGPU_API int diagpu_spgemm_numeric_astat_c64(
     int32_t n, const int32_t* A_off, const int64_t* A_starts, int32_t nA,
     const diagpu_complex64* A_vals, const diagpu_complex64* B_vals, const int32_t* C_off,

@@ -193,8 +193,9 @@ def test_complex_and_krylov_argument_errors():
 
 def test_astat_max_a_matches_header():
     """The Python constants mirror DIAGPU_ASTAT_MAX_A and _C64, and the
-    staged rows of that many A diagonals (288 fp32, 272 complex64) fit a
-    workgroup's 160 KiB of LDS, one more does not."""
+    staged rows of that many A diagonals (288 fp32; 144 complex64, the
+    128-row blocks taken above 75 complex A diagonals) fit a workgroup's
+    160 KiB of LDS, one more does not."""
     import re
     hdr = (Path(__file__).resolve().parents[1] / "include" / "diagpu.h").read_text()
     m = re.search(r"#define DIAGPU_ASTAT_MAX_A (\d+)", hdr)
@@ -202,7 +203,7 @@ def test_astat_max_a_matches_header():
     assert 288 * _lib.ASTAT_MAX_A * 4 <= 160 * 1024 < 288 * (_lib.ASTAT_MAX_A + 1) * 4
     m = re.search(r"#define DIAGPU_ASTAT_MAX_A_C64 (\d+)", hdr)
     assert m and int(m.group(1)) == _lib.ASTAT_MAX_A_C64
-    assert 272 * _lib.ASTAT_MAX_A_C64 * 8 <= 160 * 1024 < 272 * (_lib.ASTAT_MAX_A_C64 + 1) * 8
+    assert 144 * _lib.ASTAT_MAX_A_C64 * 8 <= 160 * 1024 < 144 * (_lib.ASTAT_MAX_A_C64 + 1) * 8
 
 
 def test_symbolic_noalloc_rejects_beyond_scratch():

@@ -376,6 +376,7 @@ def _offsets(rng, cnt, lo, hi):
     (3, "three"),           # every diagonal of a 3 x 3 matrix
     (1 << 17, "tail"),      # 512 blocks, the last with 5 rows per lane (513 would take 2 rounds)
     (1 << 20, "short"),     # 5 C diagonals: 8 rows per lane, 2048 blocks, the last 9
+    (1 << 17, "wideA"),     # 100 A diagonals: 2 rows per lane, 1024 blocks, the last 3
 ])
 def test_complex_astat_same_bits_as_gather(dev, oracle, n, case):
     """The complex A-stationary kernel returns the complex gather's C bit for
@@ -400,6 +401,8 @@ def test_complex_astat_same_bits_as_gather(dev, oracle, n, case):
         oa, ob = _offsets(rng, 30, -3000, 3000), _offsets(rng, 10, -600, 600)
     elif case == "short":
         oa = ob = [-512, 0, 512]
+    elif case == "wideA":
+        oa, ob = _offsets(rng, 100, -3000, 3000), _offsets(rng, 8, -300, 300)
     else:
         oa, ob = _offsets(rng, _lib.ASTAT_MAX_A_C64, -2000, 2000), _offsets(rng, 9, -100, 100)
     A = _complexify(workloads.hm_random(n, oa, seed=31, device=dev), 3)
@@ -465,7 +468,6 @@ def test_complex_astat_choice_and_capacity(dev):
                                            seed=6, device=dev), 2)
     pw = SpgemmPlan(wide, wide)
     assert pw.kernel_for(torch.complex64) == "gather"
-    assert pw.kernel_for(torch.float32) == "astat"               # the fp32 kernel holds 142
     with pytest.raises(_lib.DiagpuError) as e:
         pw.multiply(wide.values, wide.values, kernel="astat")
     assert e.value.status == _lib.ERR_CAPACITY
