@@ -22,14 +22,18 @@
 // s = (C start + min(dc, 0)) mod kLead, kLead = the elements of a 128-byte
 // line: the block's C values then start on a line, so no line is written in
 // two parts by two workgroups (a read-modify-write in HBM).  The kLead rows
-// staged before the block cover that shift.  The last of the ceil(n / kRB)
-// blocks also takes the rows [i0 + kRB - s, n) left after the shift: its
-// staged window holds them, since n <= i0 + kRB.
+// staged before the block cover that shift.  The rows the shift leaves after
+// the last block (at most kLead - 1 per diagonal) are covered in one of two
+// layouts chosen per launch: ceil((n + kLead) / kRB) blocks, the last
+// covering them, or ceil(n / kRB) blocks, the last taking the rows
+// [i0 + kRB - s, n) as one more row per lane (its staged window holds them,
+// since n <= i0 + kRB).
 //
 // A workgroup has kWaves waves; wave w evaluates C diagonals w, w + kWaves,
-// ... over the block's kRB rows, 4 rows per lane (lane l: rows l, l + 64,
-// l + 128, l + 192 of the shifted window; a 5th, l + 256, in the last
-// block).  The plan entries come as records
+// ... over the block's kRB = 64 R rows, R rows per lane (lane l: rows l,
+// l + 64, ..., l + 64 (R - 1) of the shifted window; R + 1 in the longer
+// last block), R = 2, 4, 8 or 16 chosen per launch from the plan's shape
+// and occupancy (launch_astat).  The plan entries come as records
 // {a, lo, hi, b} (diagpu_spgemm_astat_prepare): a the A diagonal's index,
 // [lo, hi) the C positions where both operands hold an element, b the B
 // index of C position 0.
@@ -129,8 +133,8 @@ __device__ __forceinline__ void store_elem_nt(T* p, T v)
 
 // Prefetch: each diagonal's metadata loaded while the one before it runs
 // (for waves that walk many diagonals).  tail5: the last block also takes
-// the rows the line-aligned shift leaves after it (else one more block of
-// at most kLead - 1 rows per diagonal covers them).
+// the rows the line-aligned shift leaves after it, R + 1 rows per lane (else
+// one more block of at most kLead - 1 rows per diagonal covers them).
 template <typename T, bool Prefetch, int R>
 __global__ __launch_bounds__(64 * kWaves) void k_astat(
     int32_t n, const int32_t* __restrict__ A_off, const int64_t* __restrict__ A_starts, int32_t nA,
@@ -150,7 +154,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
     // GPU), each staging the block's A rows.
     const int unit = (int)(blockIdx.x % kNumXcd) * per_xcd + (int)(blockIdx.x / kNumXcd);
     if (unit >= blocks * groups) return;
-    // with tail5 the last block (5 rows per lane) goes first: dispatched
+    // with tail5 the last block (R + 1 rows per lane) goes first: dispatched
     // with the first wave of workgroups, its longer work overlaps the others'
     const int blk = tail5 ? (unit / groups + blocks - 1) % blocks : unit / groups;
     const int grp = unit % groups;
