@@ -327,11 +327,11 @@ DIAGPU_API int diagpu_spgemm_numeric_band_f32(
  * each element's term sum), not bit for bit: the sums run in MFMA order.
  * Operands must be finite (a dense tile multiplies absent terms by zero).
  * info from diagpu_spgemm_band_prepare with mfma_eligible set (A's offset
- * range at most 32 wide, A's plus B's at most 48, LDS at most 80 KiB per
- * workgroup), else DIAGPU_ERR_CAPACITY.  C offsets must be the plan's (sums
- * of A's and B's).  Never picked by the plan's automatic choice: on
- * gemm_diag's -10..10 band it issues 2.9 times the useful flops and is
- * slower than the band kernel.  No reference counterpart: the reference's
+ * range at most 32 wide, A's plus B's at most 48), else
+ * DIAGPU_ERR_CAPACITY.  C offsets must be the plan's (sums of A's and B's).
+ * Never picked by the plan's automatic choice: on gemm_diag's -10..10 band it
+ * issues 2.9 times the useful flops and takes about 1.25 times the band
+ * kernel's time (on every band from +-4 to +-16 x +-8 as well).  No reference counterpart: the reference's
  * tensor-core kernel is the TF32 SpMV, and gemm_diag/gemm_diag.cu:119-329
  * runs this product on scalar FMAs; this is that product as a dense tile
  * contraction. */

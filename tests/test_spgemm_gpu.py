@@ -690,6 +690,8 @@ def test_band_lds_estimate_matches_prepare(dev):
     (300, [0], [0]),                                           # diagonal times diagonal
     (1, [0], [0]),                                             # a 1 x 1 matrix
     (3, [-2, -1, 0, 1, 2], [-2, 0, 1]),                        # every diagonal of 3 x 3
+    (65537, list(range(-16, 17)), list(range(-8, 8))),         # widest A range, C span 47
+    (20000, [-9, -4, 0, 3, 11], [-12, -2, 0, 1, 14]),          # holes, C span 46, ragged
 ])
 def test_band_mfma_kernel(dev, oracle, n, offs_a, offs_b):
     """The MFMA band kernel: every C value within 1e-5 of its fp64 term sum
