@@ -131,6 +131,19 @@ __device__ __forceinline__ void store_elem_nt(T* p, T v)
     __builtin_nontemporal_store(r, reinterpret_cast<Raw*>(p));
 }
 
+// B element c (0 <= c < n) of the run starting at base.  fp32: a buffer
+// load with the run's start as the descriptor base (scalar) and c's byte
+// offset (below 2^32 for n <= 2^30), which spares the per-lane 64-bit
+// address.  Complex: a global load (this toolchain compiles the 64-bit raw
+// buffer load builtin to a single-dword load).
+__device__ __forceinline__ float load_b(const float* base, int c)
+{
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, -1, 0x00020000);
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (uint32_t)c << 2, 0, 0));
+}
+__device__ __forceinline__ cf32 load_b(const cf32* base, int c) { return load_elem<cf32, false>(base + c); }
+
 // Prefetch: each diagonal's metadata loaded while the one before it runs
 // (for waves that walk many diagonals).  tail5: the last block also takes
 // the rows the line-aligned shift leaves after it, R + 1 rows per lane (else
@@ -226,13 +239,17 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
             T acc[RR];
 #pragma unroll
             for (int j = 0; j < RR; ++j) acc[j] = zero_of<T>();
-            // one term: B by a clamped (always valid) load, A from LDS (row
-            // R of a lane past the window, p >= len there, reads row 0), the
-            // multiply-add kept where both operands hold the element
-            auto term = [&](const int4& e, int hi, int j, T& b, T& a, bool& ok) {
+            // one term: B at the position clamped into the entry's range
+            // [e.y, e.z) (an always valid load: 0 <= c < n), A from LDS (row R
+            // of a lane past the window, p >= len there, reads row 0), the
+            // multiply-add kept where the clamp leaves the position as it is
+            // and the range is not empty: where both operands hold the element
+            // (positions p >= len take terms too, but are never stored)
+            auto term = [&](const int4& e, int j, T& b, T& a, bool& ok) {
                 const int p = pb + 64 * j;
-                ok = p >= e.y && p < hi;
-                b = load_elem<T, false>(Bv + (int64_t)e.w + min(max(p, e.y), e.z - 1));
+                const int c = min(max(p, e.y), e.z - 1);
+                ok = c == p && e.y < e.z;
+                b = load_b(Bv + (int64_t)e.w, c);
                 a = A_t[e.x * kStage + (j < R || lane < s ? ab + 64 * j : ab)];
             };
             // The values of a batch are pinned once all its loads are issued,
@@ -250,9 +267,8 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
                     const int4 e = records[g + u];
-                    const int hi = min(e.z, len);
 #pragma unroll
-                    for (int j = 0; j < RR; ++j) term(e, hi, j, bv[u][j], av[u][j], ok[u][j]);
+                    for (int j = 0; j < RR; ++j) term(e, j, bv[u][j], av[u][j], ok[u][j]);
                 }
 #pragma unroll
                 for (int u = 0; u < 2; ++u)
@@ -266,11 +282,10 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
             }
             for (; g < g1; ++g) {
                 const int4 e = records[g];
-                const int hi = min(e.z, len);
                 T bv[RR], av[RR];
                 bool ok[RR];
 #pragma unroll
-                for (int j = 0; j < RR; ++j) term(e, hi, j, bv[j], av[j], ok[j]);
+                for (int j = 0; j < RR; ++j) term(e, j, bv[j], av[j], ok[j]);
 #pragma unroll
                 for (int j = 0; j < RR; ++j) { pin(bv[j]); pin(av[j]); }
 #pragma unroll

@@ -368,8 +368,9 @@ DIAGPU_API int diagpu_spgemm_astat_prepare(int32_t n, const int64_t* A_starts, i
                                            int32_t* records, void* stream);
 
 /* The numeric phase of diagpu_spgemm_numeric_f32 (same C, bit for bit) with
- * each workgroup holding one 256-row block of every A diagonal (plus the 32
- * rows before it) in LDS and reading only B from memory: for products whose
+ * each workgroup holding one block of 64 R rows of every A diagonal (plus the
+ * 32 rows before it; R = 4, 8 or 16 rows per lane, chosen per launch) in LDS
+ * and reading only B from memory: for products whose
  * A diagonals each feed many plan entries but whose B window is too wide for
  * the band kernel (e.g. the square of a 64-diagonal band over +-512).
  * records from diagpu_spgemm_astat_prepare for this plan; nA at most
@@ -382,8 +383,9 @@ DIAGPU_API int diagpu_spgemm_numeric_astat_f32(
 
 /* The same with complex64 values: the numeric phase of
  * diagpu_spgemm_numeric_c64 (same C, bit for bit), same records; each
- * workgroup holds a block of 256 rows (128 above 75 A diagonals) plus the
- * 16 before it; nA at most DIAGPU_ASTAT_MAX_A_C64 (else
+ * workgroup holds a block of 256 rows (512 for a few short C diagonals, 128
+ * above 75 A diagonals) plus the 16 before it; nA at most
+ * DIAGPU_ASTAT_MAX_A_C64 (else
  * DIAGPU_ERR_CAPACITY).  No reference counterpart (the reference is real
  * only). */
 DIAGPU_API int diagpu_spgemm_numeric_astat_c64(
