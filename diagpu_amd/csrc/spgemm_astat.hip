@@ -345,25 +345,41 @@ int launch_rows(const char* fn, int32_t n, const int32_t* A_off, const int64_t* 
     // workgroups split each block's C diagonals over several workgroups (at
     // most one per wave's worth of diagonals).
     const int64_t slots = astat_slots<T, R>(nA);
+    // fp32 launches of 4 rows per lane and fewer than 16 rounds of
+    // workgroups also split each block, over G = 2 or 4 workgroups, towards
+    // 16 rounds (while every wave keeps at least kPrefetchDiagsPerWave C
+    // diagonals).  Measured on random 64..142 x 16..128 products over
+    // +-512..+-8192 at n = 2^18..2^20 (forced, one buffer set): 4 -> 16
+    // rounds 4-8% faster (config 5: 2.49 -> 2.34 ms under the bench's
+    // rotation), 8 -> 16 rounds 3%, at 16 rounds no split gained more than
+    // noise but one (128 x 16 at 2^20, 6%).  Lost with it: complex values
+    // (config 5 complex, 8 rounds: 6.13 -> 6.28 ms at G = 2) and the 8 rows
+    // per lane of the Taylor chain's products (numeric 1.96 -> 2.05 ms).
+    int64_t G = 1;
+    if constexpr (sizeof(T) == 4 && R == 4) {
+        const int64_t r0 = ceil_div<int64_t>(ceil_div<int64_t>((int64_t)n + kLead, kRB), slots);
+        while (G < 4 && r0 * G < 16 && c_ndiag >= 2 * G * kPrefetchDiagsPerWave * kWaves) G *= 2;
+    }
     auto split = [&](int64_t blocks) {
-        if (blocks >= slots) return (int64_t)1;
-        return std::max<int64_t>(1, std::min<int64_t>(ceil_div<int64_t>(slots, blocks),
+        if (blocks >= slots) return G;
+        return std::max<int64_t>(G, std::min<int64_t>(ceil_div<int64_t>(slots, blocks),
                                                       ceil_div<int64_t>(c_ndiag, kWaves)));
     };
     // ceil((n + kLead) / kRB) blocks of R rows per lane, the last covering
     // the rows the line-aligned shift leaves (at most kLead - 1 per
     // diagonal); or ceil(n / kRB), the last block taking those rows as one
-    // more per lane, where that saves one of at most 8 rounds of workgroups
-    // on the GPU (config 5: 1025 blocks on 256 CUs take 5 rounds, 1024 take
-    // 4).  A workgroup's time is set by its waves' chains of loads per
-    // diagonal, not by its rows, so the short block can cost a full round;
-    // over more rounds the saving shrinks below the longer block's own cost
-    // (the 7-point stencil's square, 4097 blocks in 9 rounds: 1 us slower).
+    // more per lane, where that saves one of at most 8 G rounds of
+    // workgroups on the GPU (config 5 unsplit: 1025 blocks on 256 CUs take 5
+    // rounds, 1024 take 4).  A workgroup's time is set by its waves' chains
+    // of loads per diagonal, not by its rows, so the short block can cost a
+    // full round; over more rounds the saving shrinks below the longer
+    // block's own cost (the 7-point stencil's square, 4097 blocks in 9
+    // rounds: 1 us slower).
     int64_t blocks = ceil_div<int64_t>((int64_t)n + kLead, kRB), groups = split(blocks);
     int32_t tail5 = 0;
     const int64_t b5 = ceil_div<int64_t>(n, kRB), g5 = split(b5);
     const int64_t rounds = ceil_div<int64_t>(blocks * groups, slots);
-    if (b5 < blocks && ceil_div<int64_t>(b5 * g5, slots) < rounds && rounds <= 8) {
+    if (b5 < blocks && ceil_div<int64_t>(b5 * g5, slots) < rounds && rounds <= 8 * G) {
         blocks = b5;
         groups = g5;
         tail5 = 1;
