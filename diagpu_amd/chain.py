@@ -165,6 +165,12 @@ def _timed(stats_list, fn, *args, **kw):
     return out
 
 
+def _c_values(nnz: int, like: torch.Tensor) -> torch.Tensor:
+    """Uninitialised C values (at least one element allocated, nnz viewed)."""
+    v = torch.empty(max(1, nnz), dtype=like.dtype, device=like.device)
+    return v if nnz else v[:0]
+
+
 def multiply(A: HM, B: HM, stats: ChainStats | None = None) -> HM:
     """C = A * B with its plan built on the device for this product (torch's
     current stream; one sync for the symbolic counts)."""
@@ -176,17 +182,18 @@ def multiply(A: HM, B: HM, stats: ChainStats | None = None) -> HM:
     plan = SpgemmPlan(A, B)
     inf = plan.info
     # C's structure arrays are views of the plan's buffer (kept alive by
-    # them); its host offsets follow from the operands' where both are known
-    c_host = (_sumset(A.n, A.host_offsets, B.host_offsets)
-              if A.host_offsets is not None and B.host_offsets is not None else None)
+    # them)
     C = HM(A.n, plan.c_offsets(), plan.c_lengths(), plan.c_starts(),
-           torch.empty(max(1, inf.c_nnz), dtype=A.values.dtype, device=A.values.device)[: inf.c_nnz],
-           c_host)
+           _c_values(inf.c_nnz, A.values))
     if stats is not None:
         torch.cuda.synchronize()
     t1 = time.perf_counter()
     if inf.c_ndiag:
         plan.numeric(A.values, B.values, C.values)
+    # C's host offsets follow from the operands' where both are known:
+    # computed while the product runs
+    if A.host_offsets is not None and B.host_offsets is not None:
+        C.host_offsets = _sumset(A.n, A.host_offsets, B.host_offsets)
     if stats is not None:
         torch.cuda.synchronize()
         stats.symbolic.append(t1 - t0)
@@ -311,10 +318,10 @@ def _taylor_steps(H: HM, t, order: int, S: HM) -> HM:
         plan.hand_over(main)
         inf = plan.info
         C = HM(A.n, plan.c_offsets(), plan.c_lengths(), plan.c_starts(),
-               torch.empty(max(1, inf.c_nnz), dtype=A.values.dtype, device=A.values.device)[: inf.c_nnz],
-               _sumset(A.n, _host_offsets(A), _host_offsets(B)))
+               _c_values(inf.c_nnz, A.values))
         if inf.c_ndiag:
             plan.numeric(A.values, B.values, C.values)
+        C.host_offsets = _sumset(A.n, _host_offsets(A), _host_offsets(B))   # while the product runs
         S = add_identity(C)
         if S.offsets is not C.offsets:
             side.wait_stream(main)              # a new structure, written on main

@@ -61,17 +61,38 @@ class SpgemmPlan:
             parts.append(("lookup", torch.int32, 2 * self.n - 1))
         esz = {torch.uint8: 1, torch.int32: 4, torch.int64: 8}
         sizes = [-(-cnt * esz[dt] // 256) * 256 for _, dt, cnt in parts]
-        buf = self._buf = torch.empty(sum(sizes), dtype=torch.uint8, device=dev)
-        o = 0
+        self._buf = torch.empty(sum(sizes), dtype=torch.uint8, device=dev)
+        # the parts' tensor views are made on first use (C_off, ...); the
+        # entry points take their addresses, base + byte offset
+        self._parts, self._views, o = {}, {}, 0
         for (name, dt, cnt), sz in zip(parts, sizes):
-            setattr(self, name, buf[o: o + cnt * esz[dt]].view(dt))
+            self._parts[name] = (o, dt, cnt, esz[dt])
             o += sz
-        if not want_lookup:
-            self.lookup = None
+        self._base = self._buf.data_ptr()
         self.info = _lib.SpgemmInfo()
         self._band = None
         self._astat = None
         self.symbolic()
+
+    def _view(self, name: str):
+        v = self._views.get(name)
+        if v is None:
+            if name not in self._parts:
+                return None                 # no lookup was asked for
+            o, dt, cnt, e = self._parts[name]
+            v = self._views[name] = self._buf[o: o + cnt * e].view(dt)
+        return v
+
+    def _addr(self, name: str):
+        return self._base + self._parts[name][0] if name in self._parts else None
+
+    C_off = property(lambda self: self._view("C_off"))
+    C_len = property(lambda self: self._view("C_len"))
+    C_starts = property(lambda self: self._view("C_starts"))
+    ptr = property(lambda self: self._view("ptr"))
+    pairs = property(lambda self: self._view("pairs"))
+    lookup = property(lambda self: self._view("lookup"))
+    workspace = property(lambda self: self._view("workspace"))
 
     def symbolic(self) -> None:
         A, B = self.A, self.B
@@ -82,10 +103,9 @@ class SpgemmPlan:
                   A.offsets.numel(),
                   B.offsets.data_ptr(), B.lengths.data_ptr(), B.starts.data_ptr(),
                   B.offsets.numel(),
-                  self.C_off.data_ptr(), self.C_len.data_ptr(), self.C_starts.data_ptr(),
-                  self.c_cap, self.ptr.data_ptr(), self.pairs.data_ptr(), self.p_cap,
-                  self.lookup.data_ptr() if self.lookup is not None else None,
-                  self.workspace.data_ptr(), self.workspace.numel(),
+                  self._addr("C_off"), self._addr("C_len"), self._addr("C_starts"),
+                  self.c_cap, self._addr("ptr"), self._addr("pairs"), self.p_cap,
+                  self._addr("lookup"), self._addr("workspace"), self._parts["workspace"][2],
                   C.byref(self.info), _stream_handle(self.stream))
 
     # structure views (device tensors) --------------------------------------
