@@ -129,6 +129,13 @@ def test_tc_cases_against_dense_and_scipy(oracle, name, N, offsets):
     y32 = oracle.spmv_recon_f32(N, N, r_off, r_val, x)
     assert np.all(np.abs(y32 - y64) <= 1e-6 * absum + 1e-30)
     assert np.array_equal(oracle.recon_to_dense(N, N, r_off, r_val), H)
+    # fp64 build_recon (orc_build_recon_f64): the same scatter on fp64 data
+    # with bits below fp32 resolution, against scipy's layout of the same H
+    v64 = vals.astype(np.float64) * (1 + 2.0 ** -40)
+    r_off64, r_val64 = oracle.build_recon(N, N, offs, starts, lens, v64)
+    assert r_val64.dtype == np.float64 and np.array_equal(r_off64, r_off)
+    S64 = sp.dia_matrix((r_val64.reshape(len(r_off), N), r_off), shape=(N, N)).toarray()
+    assert np.array_equal(S64, H.astype(np.float64) * (1 + 2.0 ** -40))
 
 
 def test_spmv_poisson_closed_form(oracle):
@@ -143,6 +150,97 @@ def test_spmv_poisson_closed_form(oracle):
     missing = (i == 0).astype(int) + (i == side - 1) + (j == 0) + (j == side - 1)
     assert np.array_equal(y, missing.astype(np.float64))
     assert torch.count_nonzero(R.values).item() == 5 * n - 4 * side
+
+
+def _recon_f64_case(rows, cols, offsets, seed):
+    """fp64 Recon values with full 53-bit mantissas (not fp32-representable),
+    NaN in every padding slot (column c of diagonal d with row c - d outside
+    [0, rows)), the dense matrix scipy's dia_matrix builds from the in-range
+    slots, and an fp64 x."""
+    import scipy.sparse as sp
+    rng = np.random.default_rng(seed)
+    K = len(offsets)
+    vals = rng.uniform(-1, 1, (K, cols)) + rng.uniform(-1, 1, (K, cols)) * 2.0 ** -30
+    c = np.arange(cols)
+    for k, d in enumerate(offsets):
+        vals[k, (c - d < 0) | (c - d >= rows)] = np.nan
+    D = sp.dia_matrix((np.nan_to_num(vals, nan=0.0), offsets), shape=(rows, cols)).toarray()
+    x = rng.standard_normal(cols) + rng.standard_normal(cols) * 2.0 ** -29
+    return vals.reshape(-1), D, x
+
+
+F64_CASES = [(n, n, offs) for _, n, offs in TC_CASES] + [
+    (31, 45, [-30, -1, 0, 5, 44]), (50, 20, [-49, -6, 0, 1, 19]), (64, 64, [-70, 0, 3, 80])]
+
+
+@pytest.mark.parametrize("rows,cols,offsets", F64_CASES)
+def test_spmv_f64_vs_dense_and_scipy(oracle, rows, cols, offsets):
+    """orc_spmv_recon_f64, the fp64 checker of the GPU's fp64 SpMV, against
+    the dense fp64 product of scipy's dia_matrix (the column-indexed Recon
+    convention of spmv/src/dia_reconstruct.cuh:9-27), summing exactly the
+    in-range terms of spmv/test/test_reconstruct.cpp:122-138 (NaN padding
+    must never be read); abs_sum against |D| |x|; x shorter than cols drops
+    the columns past its end."""
+    import scipy.sparse as sp
+    vals, D, x = _recon_f64_case(rows, cols, offsets, rows * 131 + cols)
+    y, absum = oracle.spmv_recon_ref64(rows, cols, offsets, vals, x)
+    assert y.dtype == np.float64 and np.all(np.isfinite(y))
+    want = D @ x
+    bound = np.abs(D) @ np.abs(x)
+    assert np.all(np.abs(y - want) <= 1e-14 * bound + 1e-300)
+    assert np.allclose(absum, bound, rtol=1e-13, atol=0)
+    S = sp.dia_matrix((np.nan_to_num(vals.reshape(len(offsets), cols)), offsets), shape=(rows, cols))
+    assert np.all(np.abs(y - S @ x) <= 1e-14 * bound + 1e-300)
+    # a value below fp32 resolution reaches y: fp64 arithmetic throughout
+    y32, _ = oracle.spmv_recon_ref64(rows, cols, offsets, vals.astype(np.float32), x.astype(np.float32))
+    if np.any(D != 0):
+        assert not np.array_equal(y, y32)
+    # x of length cols - 3: columns >= cols - 3 contribute nothing
+    m = max(cols - 3, 0)
+    y_short, _ = oracle.spmv_recon_ref64(rows, cols, offsets, vals, x[:m].copy())
+    assert np.all(np.abs(y_short - D[:, :m] @ x[:m]) <= 1e-14 * bound + 1e-300)
+
+
+def test_spmv_f64_poisson_closed_form(oracle):
+    """5-point stencil in fp64: x = 1 gives the count of missing grid
+    neighbours exactly; x = i (the row's grid column index) gives 4j - the
+    present horizontal neighbours' columns - 2j for the vertical ones."""
+    from diagpu_amd.workloads import recon_poisson5
+    side = 16
+    R = recon_poisson5(side, seed=0, device="cpu")
+    n = side * side
+    off = R.offsets.numpy()
+    v64 = R.values.numpy().astype(np.float64)
+    y, _ = oracle.spmv_recon_ref64(n, n, off, v64, np.ones(n))
+    i, j = np.divmod(np.arange(n), side)
+    missing = (i == 0).astype(int) + (i == side - 1) + (j == 0) + (j == side - 1)
+    assert np.array_equal(y, missing.astype(np.float64))
+    # x = grid column j: y = 4j - (j-1)[j>0] - (j+1)[j<side-1] - j[i>0] - j[i<side-1]
+    y2, _ = oracle.spmv_recon_ref64(n, n, off, v64, j.astype(np.float64))
+    want = (4 * j - np.where(j > 0, j - 1, 0) - np.where(j < side - 1, j + 1, 0)
+            - np.where(i > 0, j, 0) - np.where(i < side - 1, j, 0))
+    assert np.array_equal(y2, want.astype(np.float64))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("rows,cols,offsets", [(80, 80, [-9, -5, -2, -1, 0, 1, 2, 5, 9]),
+                                              (50, 20, [-49, -6, 0, 1, 19]),
+                                              (4099, 4099, [-2048, -1, 0, 1, 2048])])
+def test_spmv_omp_baseline_vs_dense(oracle, dtype, rows, cols, offsets):
+    """The OpenMP CPU baselines (orc_spmv_recon_omp_f32/_f64) compute every
+    row of y: compared with the dense product (accumulation in the element
+    type, so the bound scales with its epsilon)."""
+    vals, D, x = _recon_f64_case(rows, cols, offsets, rows + 7 * cols)
+    vals = np.nan_to_num(vals).astype(dtype)
+    x = x.astype(dtype)
+    D = D.astype(dtype).astype(np.float64)
+    y = np.full(rows, np.nan, dtype=dtype)
+    threads = oracle.spmv_recon_omp(rows, cols, np.array(offsets, np.int32), vals, x, y)
+    assert threads >= 1
+    want = D @ x.astype(np.float64)
+    bound = np.abs(D) @ np.abs(x.astype(np.float64))
+    eps = np.finfo(dtype).eps
+    assert np.all(np.abs(y.astype(np.float64) - want) <= 2 * len(offsets) * eps * bound + 1e-300)
 
 
 def test_spmv_main_diagonal_and_out_of_range(oracle):
