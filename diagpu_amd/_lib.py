@@ -136,7 +136,8 @@ PROTOTYPES: dict[str, tuple] = {
     "diagpu_spgemm_numeric_band_mfma_f32": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _i32,
                                                       _vp, _vp, _vp, _i64, C.POINTER(BandInfo),
                                                       _vp, _vp]),
-    "diagpu_spgemm_astat_prepare": (C.c_int, [_i32, _vp, _i32, _vp, _i64, _vp, _vp]),
+    "diagpu_spgemm_astat_prepare": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _i32, _vp, _vp,
+                                                _i64, _vp, _i64, _vp, _vp]),
     "diagpu_spgemm_numeric_astat_f32": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp,
                                                   _i64, _vp, _vp, _i64, _vp, _vp]),
     "diagpu_spgemm_numeric_astat_c64": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp,

@@ -50,17 +50,34 @@ def identity(n: int, device, dtype=torch.float32) -> HM:
 
 
 # Identities the chain reads (never writes), one per (n, device, dtype): a
-# Taylor step adds I without building it again.
+# Taylor step adds I without building it again.  Each entry keeps the event
+# recorded after its fill and the handles of the streams that have read it.
+# A stream reading it for the first time waits for that event, and the
+# entry's tensors are marked as used on that stream (record_stream), so
+# dropping the cache never hands their memory to new work while a read on
+# another stream is still queued.
 _UNITS: dict = {}
 
 
 def _unit(n: int, device, dtype) -> HM:
-    key = (n, str(torch.device(device)), dtype)
-    I = _UNITS.get(key)
-    if I is None:
+    """The cached identity, ready to be read on torch's current stream."""
+    dev = torch.device(device)
+    cur = torch.cuda.current_stream(dev)
+    key = (n, str(dev), dtype)
+    ent = _UNITS.get(key)
+    if ent is None:
         if len(_UNITS) >= 8:
             _UNITS.clear()
-        I = _UNITS[key] = identity(n, device, dtype)
+        I = identity(n, dev, dtype)
+        filled = torch.cuda.Event()
+        filled.record(cur)
+        ent = _UNITS[key] = (I, filled, {cur.cuda_stream})
+    I, filled, readers = ent
+    if cur.cuda_stream not in readers:
+        cur.wait_event(filled)
+        for t in (I.offsets, I.starts, I.values):
+            t.record_stream(cur)
+        readers.add(cur.cuda_stream)
     return I
 
 

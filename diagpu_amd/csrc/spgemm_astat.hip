@@ -72,42 +72,73 @@ template <typename T> constexpr int astat_cap()
 static_assert(astat_cap<float>() == DIAGPU_ASTAT_MAX_A, "fp32 A diagonals in 160 KiB of LDS");
 static_assert(astat_cap<cf32>() == DIAGPU_ASTAT_MAX_A_C64, "complex A diagonals in 160 KiB of LDS");
 
-// records[g] = {a, lo, hi, b} for plan entry g; flag[0] set if an entry's A
-// start is no A diagonal's start, flag[1] if its B indices do not fit int32.
-__global__ __launch_bounds__(256) void k_astat_prepare(const diagpu_gpair* __restrict__ pairs,
-                                                       int64_t n_pairs,
-                                                       const int64_t* __restrict__ A_starts,
-                                                       int32_t nA, int4* __restrict__ records,
-                                                       int32_t* __restrict__ flag)
+// records[g] = {a, lo, hi, b} for plan entry g; flag[0] set if an entry is
+// not in the symbolic plan's form (its A or B start is no diagonal's start,
+// da + db is not its C diagonal's offset, or its shifts or lengths differ
+// from min0(da) - min0(dc), da + min0(db) - min0(dc), n - |da|, n - |db|),
+// flag[1] if its B indices do not fit int32.  The kernel builds each A row
+// from A_off and C_off but takes each term's range from the record, so an
+// entry of another form would give a different C without an error.
+__device__ __forceinline__ int find_start(const int64_t* s, int32_t cnt, int64_t v)
+{
+    // binary search (diagonals stored in offset order: starts ascend), then a
+    // linear scan for operands stored in another order
+    int lo = 0, hi = cnt - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s[mid] <= v) lo = mid; else hi = mid - 1;
+    }
+    if (s[lo] == v) return lo;
+    for (int i = 0; i < cnt; ++i)
+        if (s[i] == v) return i;
+    return -1;
+}
+
+__global__ __launch_bounds__(256) void k_astat_prepare(
+    int32_t n, const int32_t* __restrict__ A_off, const int64_t* __restrict__ A_starts, int32_t nA,
+    const int32_t* __restrict__ B_off, const int64_t* __restrict__ B_starts, int32_t nB,
+    const int32_t* __restrict__ C_off, const int64_t* __restrict__ pair_ptr, int64_t c_ndiag,
+    const diagpu_gpair* __restrict__ pairs, int64_t n_pairs, int4* __restrict__ records,
+    int32_t* __restrict__ flag)
 {
     const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (g >= n_pairs) return;
     const diagpu_gpair p = pairs[g];
-    // binary search (diagonals stored in offset order: starts ascend), then a
-    // linear scan for operands stored in another order
-    int lo = 0, hi = nA - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (A_starts[mid] <= (int64_t)p.ab) lo = mid; else hi = mid - 1;
+    // the C diagonal k whose entries [pair_ptr[k], pair_ptr[k + 1]) hold g
+    int64_t klo = 0, khi = c_ndiag - 1;
+    while (klo < khi) {
+        const int64_t mid = (klo + khi + 1) >> 1;
+        if (pair_ptr[mid] <= g) klo = mid; else khi = mid - 1;
     }
-    if (A_starts[lo] != (int64_t)p.ab)
-        for (int i = 0; i < nA; ++i)
-            if (A_starts[i] == (int64_t)p.ab) lo = i;
+    const bool in_c = c_ndiag > 0 && pair_ptr[klo] <= g && g < pair_ptr[klo + 1];
+    const int a = find_start(A_starts, nA, (int64_t)p.ab);
+    const int bi = find_start(B_starts, nB, (int64_t)p.bb);
+    bool ok = in_c && a >= 0 && bi >= 0;
+    if (ok) {
+        const int64_t da = A_off[a], db = B_off[bi], dc = C_off[klo];
+        auto min0 = [](int64_t x) { return x < 0 ? x : (int64_t)0; };
+        auto absl = [](int64_t x) { return x < 0 ? -x : x; };
+        ok = da + db == dc && dc > -(int64_t)n && dc < n &&
+             (int64_t)p.ash == min0(da) - min0(dc) &&
+             (int64_t)p.bsh == da + min0(db) - min0(dc) && (int64_t)p.al == n - absl(da) &&
+             (int64_t)p.bl == n - absl(db);
+    }
     const int plo = max(0, max(-p.ash, -p.bsh));
     const int phi = min(p.al - p.ash, p.bl - p.bsh);
     const int64_t b = (int64_t)p.bb + p.bsh;
     int4 r = int4{0, 0, 0, 0};
-    if (A_starts[lo] != (int64_t)p.ab) {
+    if (!ok) {
         flag[0] = 1;   // every writer stores the same value
     } else if (plo >= phi) {
-        // No position holds both operands (a symbolic plan has no such entry,
-        // a caller's may): a record that never fires, whose clamped B load
-        // min(max(p, 1), 0) = 0 reads B[0].
-        r = int4{lo, 1, 1, 0};
+        // No position holds both operands (an entry of the symbolic form
+        // always has one; kept so that no record can read past B): a record
+        // that never fires, whose clamped B load min(max(p, 1), 0) = 0 reads
+        // B[0].
+        r = int4{a, 1, 1, 0};
     } else if (b < INT_MIN || b + phi > INT_MAX) {
         flag[1] = 1;
     } else {
-        r = int4{lo, plo, phi, (int)b};
+        r = int4{a, plo, phi, (int)b};
     }
     records[g] = r;
 }
@@ -477,16 +508,26 @@ int launch_astat(const char* fn, int32_t n, const int32_t* A_off, const int64_t*
 
 extern "C" {
 
-DIAGPU_API int diagpu_spgemm_astat_prepare(int32_t n, const int64_t* A_starts, int32_t nA,
+DIAGPU_API int diagpu_spgemm_astat_prepare(int32_t n, const int32_t* A_off,
+                                           const int64_t* A_starts, int32_t nA,
+                                           const int32_t* B_off, const int64_t* B_starts,
+                                           int32_t nB, const int32_t* C_off,
+                                           const int64_t* pair_ptr, int64_t c_ndiag,
                                            const diagpu_gpair* pairs, int64_t n_pairs,
                                            int32_t* records, void* stream)
 {
     using namespace diagpu;
     const char* fn = "diagpu_spgemm_astat_prepare";
-    if (n < 1 || nA < 1 || n_pairs < 0 || n_pairs > INT_MAX)
-        return fail(DIAGPU_ERR_ARG, "%s: need n, nA >= 1 and 0 <= n_pairs <= 2^31 - 1", fn);
-    if (!A_starts || !records || (n_pairs > 0 && !pairs))
+    if (n < 1 || nA < 1 || nB < 1 || n_pairs < 0 || n_pairs > INT_MAX || c_ndiag < 0 ||
+        c_ndiag > 2 * (int64_t)n - 1)
+        return fail(DIAGPU_ERR_ARG,
+                    "%s: need n, nA, nB >= 1, 0 <= c_ndiag <= 2n - 1 and "
+                    "0 <= n_pairs <= 2^31 - 1", fn);
+    if (!A_off || !A_starts || !B_off || !B_starts || !records ||
+        (n_pairs > 0 && (!pairs || !C_off || !pair_ptr)))
         return fail(DIAGPU_ERR_ARG, "%s: a pointer is NULL", fn);
+    if (n_pairs > 0 && c_ndiag == 0)
+        return fail(DIAGPU_ERR_ARG, "%s: plan entries without C diagonals", fn);
     hipStream_t s = as_stream(stream);
     int32_t* flag = records + 4 * n_pairs;   // the caller's 4 scratch ints
     int32_t host[2] = {0, 0};
@@ -494,13 +535,17 @@ DIAGPU_API int diagpu_spgemm_astat_prepare(int32_t n, const int64_t* A_starts, i
     int st = check_launch(fn);
     if (!st && n_pairs > 0) {
         hipLaunchKernelGGL(k_astat_prepare, dim3((unsigned)ceil_div<int64_t>(n_pairs, 256)),
-                           dim3(256), 0, s, pairs, n_pairs, A_starts, nA,
-                           reinterpret_cast<int4*>(records), flag);
+                           dim3(256), 0, s, n, A_off, A_starts, nA, B_off, B_starts, nB, C_off,
+                           pair_ptr, c_ndiag, pairs, n_pairs, reinterpret_cast<int4*>(records),
+                           flag);
         st = check_launch(fn);
     }
     if (!st) st = check_hip(hipMemcpyWithStream(host, flag, sizeof(host), hipMemcpyDeviceToHost, s), fn);
     if (st) return st;
-    if (host[0]) return fail(DIAGPU_ERR_ARG, "%s: a plan entry's A start is not an A diagonal's start", fn);
+    if (host[0])
+        return fail(DIAGPU_ERR_ARG,
+                    "%s: a plan entry is not in the symbolic plan's form (starts, offsets, "
+                    "shifts or lengths)", fn);
     if (host[1]) return fail(DIAGPU_ERR_CAPACITY, "%s: B indices beyond 2^31 - 1", fn);
     return DIAGPU_OK;
 }

@@ -890,6 +890,28 @@ int scratch_ptr(const char* fn, void** out)
     return DIAGPU_OK;
 }
 
+// One lock per device over that device's scratch array: a no-alloc call holds
+// it from before its first launch until its stream has drained, so calls that
+// overlap in one process (other host threads, other streams) run one after
+// the other instead of racing for the array.
+std::mutex& scratch_lock(int dev)
+{
+    static std::mutex mu[64];
+    return mu[dev];
+}
+
+// Waits for `s` when armed: on an error return after a launch, the queued
+// kernels may still use the scratch array, so the lock is released only after
+// they finish.  Declared after the lock, so it runs before the unlock.
+struct DrainOnExit {
+    hipStream_t s = nullptr;
+    bool armed = false;
+    ~DrainOnExit()
+    {
+        if (armed) (void)hipStreamSynchronize(s);
+    }
+};
+
 // k_sym_fast takes kFastLdsBytes of dynamic LDS; more than 64 KiB must be
 // allowed explicitly (once per device).
 int fast_lds_allowed(const char* fn)
@@ -937,13 +959,20 @@ int run_symbolic(
         return fail(DIAGPU_ERR_ARG, "%s: C arrays are NULL", fn);
     if (pair_capacity > 0 && !pairs) return fail(DIAGPU_ERR_ARG, "%s: pairs is NULL", fn);
     const Layout L = layout_for(n, a_ndiag, b_ndiag);
+    std::unique_lock<std::mutex> scratch_guard;
     if (use_scratch) {
         if (L.total > kScratchBytes)
             return fail(DIAGPU_ERR_CAPACITY,
                         "%s: n=%d with %d x %d diagonals needs %zu bytes of scratch, more than "
                         "the %zu the library holds (use diagpu_spgemm_symbolic with a workspace)",
                         fn, n, a_ndiag, b_ndiag, L.total, kScratchBytes);
-        const int rc = scratch_ptr(fn, &workspace);
+        int dev = 0;
+        int rc = check_hip(hipGetDevice(&dev), fn);
+        if (rc) return rc;
+        if (dev < 0 || dev >= 64)
+            return fail(DIAGPU_ERR_ARG, "%s: device %d out of range", fn, dev);
+        scratch_guard = std::unique_lock<std::mutex>(scratch_lock(dev));
+        rc = scratch_ptr(fn, &workspace);
         if (rc) return rc;
         workspace_bytes = kScratchBytes;
     }
@@ -968,6 +997,8 @@ int run_symbolic(
     } back;
     SymState& h = back.h;
     int rc = DIAGPU_OK;
+    DrainOnExit drain;
+    drain.s = s;
 
     // The one-launch path where the operand product is small enough for each
     // workgroup to enumerate (it reports kFlagFallback when the spans do not
@@ -982,6 +1013,7 @@ int run_symbolic(
         int64_t G = ceil_div<int64_t>(ub, 32);
         const int64_t gmax = cu_count() < kMaxFastGroups ? cu_count() : kMaxFastGroups;
         G = G < 1 ? 1 : (G > gmax ? gmax : G);
+        drain.armed = use_scratch;
         hipLaunchKernelGGL(k_sym_fast, dim3((unsigned)G), dim3(kFastBlock), kFastLdsBytes, s, n,
                            A_off, A_len, A_starts, a_ndiag, B_off, B_len, B_starts, b_ndiag,
                            C_off, C_len, C_starts, c_capacity, pair_ptr, pairs, pair_capacity,
@@ -994,6 +1026,7 @@ int run_symbolic(
         rc = check_hip(hipMemcpyWithStream(&back, st, sizeof(SymState) + sizeof(int32_t) * G,
                                            hipMemcpyDeviceToHost, s), fn);
         if (rc) return rc;
+        drain.armed = false;
         if (!(h.flags & kFlagFallback)) {
             int32_t mx = 0;
             for (int64_t g = 0; g < G && !h.flags; ++g) mx = back.m[g] > mx ? back.m[g] : mx;
@@ -1005,6 +1038,7 @@ int run_symbolic(
         const int64_t c_cap = c_capacity < L.cmax ? c_capacity : L.cmax;
         const int64_t nkb = ceil_div<int64_t>(c_cap + 1, kBlock);
 
+        drain.armed = use_scratch;
         hipLaunchKernelGGL(k_init, dim3(grid_for(L.nlk, 4096)), dim3(kBlock), 0, s, alk, L.nlk, bbits,
                            cbits, L.nwords, st);
         hipLaunchKernelGGL(k_operands, dim3(grid_for(a_ndiag > b_ndiag ? a_ndiag : b_ndiag)),
@@ -1032,6 +1066,7 @@ int run_symbolic(
         if (rc) return rc;
         rc = check_hip(hipMemcpyWithStream(&h, st, sizeof(h), hipMemcpyDeviceToHost, s), fn);
         if (rc) return rc;
+        drain.armed = false;
     }
     info->c_ndiag = h.c_ndiag;
     info->c_nnz = h.c_nnz;

@@ -198,9 +198,12 @@ class SpgemmPlan:
             A = self.A
             rec = torch.empty(4 * self.info.n_pairs + 4, dtype=torch.int32,
                               device=self.C_off.device)
-            _lib.call("diagpu_spgemm_astat_prepare", self.n, A.starts.data_ptr(),
-                      A.offsets.numel(), self.pairs.data_ptr(), self.info.n_pairs,
-                      rec.data_ptr(), _stream_handle(self.stream))
+            B = self.B
+            _lib.call("diagpu_spgemm_astat_prepare", self.n, A.offsets.data_ptr(),
+                      A.starts.data_ptr(), A.offsets.numel(), B.offsets.data_ptr(),
+                      B.starts.data_ptr(), B.offsets.numel(), self.C_off.data_ptr(),
+                      self.ptr.data_ptr(), self.info.c_ndiag, self.pairs.data_ptr(),
+                      self.info.n_pairs, rec.data_ptr(), _stream_handle(self.stream))
             self._astat = rec
         return self._astat
 

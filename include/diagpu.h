@@ -221,17 +221,19 @@ DIAGPU_API int diagpu_spgemm_symbolic(
     diagpu_spgemm_info* info, void* stream);
 
 /* diagpu_spgemm_symbolic without the workspace argument: for callers that
- * cannot allocate device memory (code under HIP graph capture, tight serving
- * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
- * The workspace is a file-scope device array of DIAGPU_SYMBOLIC_SCRATCH_BYTES
- * that each GPU holds until the process ends; a problem whose workspace
+ * cannot allocate device memory (tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  The workspace is a
+ * file-scope device array of DIAGPU_SYMBOLIC_SCRATCH_BYTES that each GPU
+ * holds until the process ends; a problem whose workspace
  * (diagpu_spgemm_symbolic_workspace) is larger is rejected with
  * DIAGPU_ERR_CAPACITY before any GPU work (n up to about 4.7 million fits
  * for any diagonal counts).  Same arguments, outputs and errors as
- * diagpu_spgemm_symbolic otherwise; allocates nothing.  Every call on one GPU
- * shares that GPU's array, so calls that overlap on one GPU (other host
- * threads, other streams) race; calls in sequence do not, because each call
- * synchronises its stream before returning and re-initialises what it reads. */
+ * diagpu_spgemm_symbolic otherwise; allocates nothing.  Like that call it
+ * reads the counts back to the host with a synchronous copy on `stream`, so
+ * it cannot be recorded into a HIP graph.  Every call on one GPU shares that
+ * GPU's array: calls that overlap in one process (other host threads, other
+ * streams) are serialised by a per-device lock held until the call's stream
+ * has drained; each call re-initialises what it reads. */
 #define DIAGPU_SYMBOLIC_SCRATCH_BYTES (40u << 20)
 DIAGPU_API int diagpu_spgemm_symbolic_noalloc(
     int32_t n,
@@ -359,11 +361,19 @@ DIAGPU_API int diagpu_spgemm_numeric_band_mfma_f32(
  * from the entry's A start), [lo, hi) = [max(0, -ash, -bsh), min(al - ash,
  * bl - bsh)) the C positions where both operands hold an element, and
  * b = bb + bsh the B index of C position 0.  records holds 4 n_pairs + 4
- * int32 (the last 4 are scratch).  One stream synchronisation (to report
- * errors): DIAGPU_ERR_ARG if an entry's A start is no A diagonal's start,
+ * int32 (the last 4 are scratch).  A_off/A_starts, B_off/B_starts, C_off
+ * and pair_ptr (c_ndiag + 1 entries) are the plan's device arrays.  One
+ * stream synchronisation (to report errors): DIAGPU_ERR_ARG if an entry is
+ * not in the symbolic plan's form (its A or B start is no diagonal's start,
+ * da + db is not its C diagonal's offset, or ash, bsh, al, bl differ from
+ * min0(da) - min0(dc), da + min0(db) - min0(dc), n - |da|, n - |db|),
  * DIAGPU_ERR_CAPACITY if a B index exceeds 2^31 - 1.  No reference
  * counterpart: the A-stationary form of the numeric phase below. */
-DIAGPU_API int diagpu_spgemm_astat_prepare(int32_t n, const int64_t* A_starts, int32_t nA,
+DIAGPU_API int diagpu_spgemm_astat_prepare(int32_t n, const int32_t* A_off,
+                                           const int64_t* A_starts, int32_t nA,
+                                           const int32_t* B_off, const int64_t* B_starts,
+                                           int32_t nB, const int32_t* C_off,
+                                           const int64_t* pair_ptr, int64_t c_ndiag,
                                            const diagpu_gpair* pairs, int64_t n_pairs,
                                            int32_t* records, void* stream);
 

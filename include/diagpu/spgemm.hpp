@@ -431,7 +431,9 @@ private:
     void prepare_astat(hipStream_t stream) const
     {
         records_.resize(size_t(4 * info_.n_pairs + 4));
-        check(diagpu_spgemm_astat_prepare(n_, A_starts_.data(), nA_, pairs_.data(), info_.n_pairs,
+        check(diagpu_spgemm_astat_prepare(n_, A_off_.data(), A_starts_.data(), nA_, B_off_.data(),
+                                          B_starts_.data(), nB_, C_off_.data(), ptr_.data(),
+                                          info_.c_ndiag, pairs_.data(), info_.n_pairs,
                                           records_.data(), stream));
         astat_prepared_ = true;
     }

@@ -173,10 +173,17 @@ def test_complex_and_krylov_argument_errors():
     band.eligible = 0
     assert call(3, band) == _lib.ERR_CAPACITY
     # A-stationary kernel: argument checks before any HIP call or launch
-    assert _status("diagpu_spgemm_astat_prepare", 0, fake, 1, fake, 1, fake, None) == _lib.ERR_ARG
-    assert _status("diagpu_spgemm_astat_prepare", 10, fake, 0, fake, 1, fake, None) == _lib.ERR_ARG
-    assert _status("diagpu_spgemm_astat_prepare", 10, None, 1, fake, 1, fake, None) == _lib.ERR_ARG
-    assert _status("diagpu_spgemm_astat_prepare", 10, fake, 1, fake, -1, fake, None) == _lib.ERR_ARG
+    prep = lambda n, aoff, nA, nB, cptr, nC, npairs: _status(
+        "diagpu_spgemm_astat_prepare", n, aoff, fake, nA, fake, fake, nB, fake, cptr, nC, fake,
+        npairs, fake, None)
+    assert prep(0, fake, 1, 1, fake, 1, 1) == _lib.ERR_ARG        # n < 1
+    assert prep(10, fake, 0, 1, fake, 1, 1) == _lib.ERR_ARG       # no A diagonal
+    assert prep(10, fake, 1, 0, fake, 1, 1) == _lib.ERR_ARG       # no B diagonal
+    assert prep(10, None, 1, 1, fake, 1, 1) == _lib.ERR_ARG       # A offsets NULL
+    assert prep(10, fake, 1, 1, None, 1, 1) == _lib.ERR_ARG       # pair_ptr NULL
+    assert prep(10, fake, 1, 1, fake, 1, -1) == _lib.ERR_ARG      # negative entry count
+    assert prep(10, fake, 1, 1, fake, 20, 1) == _lib.ERR_ARG      # c_ndiag > 2n - 1
+    assert prep(10, fake, 1, 1, fake, 0, 1) == _lib.ERR_ARG       # entries without C
     astat = lambda nA, nC: _status("diagpu_spgemm_numeric_astat_f32", 100, fake, fake, nA, fake,
                                    fake, fake, fake, fake, nC, fake, fake, 1, fake, None)
     assert astat(0, 5) == _lib.ERR_ARG

@@ -134,6 +134,36 @@ def test_add_identity_in_place_and_union(dev):
     assert np.array_equal(dense_of(V), dense_of(U) + 2.0 * np.eye(n))
 
 
+def test_identity_cache_across_streams(dev):
+    """The cached identity is filled on the stream of its first caller; a
+    caller on another stream must wait for that fill.  The first stream is
+    held busy (a bounded spin) so its fill runs late: the second stream's
+    union must still see ones on the main diagonal."""
+    n = 700_001
+    chain._UNITS.clear()
+    s1, s2 = torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)
+    U1 = hm_random(n, [-3, 2], 21, dev)
+    U2 = hm_random(n, [-1, 5], 22, dev)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s1):
+        torch.cuda._sleep(20_000_000)
+    V1 = chain.add_identity(U1, 2.0, stream=s1)
+    V2 = chain.add_identity(U2, 3.0, stream=s2)
+    torch.cuda.synchronize()
+    for V, U, sg, offs in ((V1, U1, 2.0, [-3, 0, 2]), (V2, U2, 3.0, [-1, 0, 5])):
+        assert V.offsets.cpu().tolist() == offs
+        st = V.starts.cpu().tolist()
+        main = V.values[st[1]: st[1] + n]
+        assert torch.all(main == sg).item()
+        for k, j in ((0, 0), (2, 1)):      # the other diagonals are U's, unchanged
+            ln = n - abs(offs[k])
+            src = U.values[U.starts[j].item(): U.starts[j].item() + ln]
+            assert torch.equal(V.values[st[k]: st[k] + ln], src)
+    I, _, readers = next(iter(chain._UNITS.values()))
+    assert {s1.cuda_stream, s2.cuda_stream} <= readers
+    chain._UNITS.clear()
+
+
 def test_taylor_order_zero_is_identity(dev):
     H = hm_random(64, [-1, 1], 9, dev)
     S = chain.taylor_expm(H, 1.0, 0)

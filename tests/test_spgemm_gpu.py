@@ -536,15 +536,13 @@ def test_lds_kernels_with_operands_in_any_order(dev):
 def test_plan_entries_without_positions(dev):
     """A caller's plan may hold entries where no position has both operands
     (a symbolic plan never does: |da|, |db|, |dc| < n leaves at least one
-    row).  The gather and the A-stationary kernel take each entry's range
-    from its lengths: here entries of the first B diagonal (B start 0, where
-    the clamped B load of an empty range would fall before the array) get
-    al = 0 on the device, the A-stationary records mark them {a, 1, 1, 0}
-    (a record that never fires and loads B[0]), both kernels return the same
-    bits, and those bits differ from the full plan's product on exactly the
-    C diagonals of the emptied entries.  The band kernel derives each
-    term's validity from the operands' offsets, not from the entry, so its
-    prepare step refuses the edited plan (DIAGPU_ERR_ARG)."""
+    row).  The gather takes each entry's range from its lengths: here
+    entries of the first B diagonal (B start 0, where the clamped B load of
+    an empty range would fall before the array) get al = 0 on the device,
+    and the gather's C differs from the full plan's product on exactly the C
+    diagonals of the emptied entries.  The band and A-stationary kernels
+    derive each term from the operands' offsets, so their prepare steps
+    refuse the edited plan (DIAGPU_ERR_ARG)."""
     n = 3000
     A = workloads.hm_random(n, list(range(-20, 21, 4)), 41, dev)
     B = workloads.hm_random(n, [-2999, -700, 0, 5, 2998], 42, dev)
@@ -554,16 +552,12 @@ def test_plan_entries_without_positions(dev):
     assert hit.size > 0
     words = plan.pairs[: plan.info.n_pairs * 32].view(torch.int32).view(-1, 8)
     words[torch.as_tensor(hit, device=dev), 6] = 0             # al = 0: empty range
-    plan._astat = None                                           # records from the edited plan
-    rec = plan.astat_records()[: 4 * plan.info.n_pairs].cpu().numpy().reshape(-1, 4)
-    assert (rec[hit, 1:] == [1, 1, 0]).all()
     Cg = plan.multiply(A.values, B.values, kernel="gather")
-    Ca = plan.multiply(A.values, B.values, kernel="astat")
-    assert torch.equal(Cg.view(torch.int32), Ca.view(torch.int32))
-    plan._band = None
-    with pytest.raises(_lib.DiagpuError) as e:
-        plan.band_info()
-    assert e.value.status == _lib.ERR_ARG and "symbolic" in str(e.value)
+    for k, fn in (("band", plan.band_info), ("astat", plan.astat_records)):
+        plan._band, plan._astat = None, None
+        with pytest.raises(_lib.DiagpuError) as e:
+            fn()
+        assert e.value.status == _lib.ERR_ARG and "symbolic" in str(e.value), k
     full = SpgemmPlan(A, B)
     Cf = full.multiply(A.values, B.values, kernel="gather")
     ptr = full.pair_ptr().cpu().numpy()
@@ -573,6 +567,44 @@ def test_plan_entries_without_positions(dev):
     diff = (Cg != Cf).cpu().numpy()
     for k in range(full.info.c_ndiag):
         assert diff[c_st[k]: c_st[k] + c_len[k]].any() == touched[k], k
+
+
+@pytest.mark.parametrize("field,delta", [("ash", 1), ("bsh", -1), ("al", -1), ("bl", 1),
+                                         ("bb", "next"), ("ptr", None)])
+def test_astat_prepare_refuses_edited_plans(dev, field, delta):
+    """diagpu_spgemm_astat_prepare checks every entry against the symbolic
+    form (A and B starts, da + db = dc, the shifts min0(da) - min0(dc) and
+    da + min0(db) - min0(dc), the lengths n - |d|): one edited field of one
+    entry, or a pair_ptr that moves an entry to the next C diagonal, gives
+    DIAGPU_ERR_ARG; the unedited plan is accepted and multiplies to the
+    gather's bits."""
+    n = 5000
+    A = workloads.hm_random(n, [-9, -4, 0, 3, 11], 51, dev)
+    B = workloads.hm_random(n, [-30, -1, 0, 2, 7, 40], 52, dev)
+    plan = SpgemmPlan(A, B)
+    Cg = plan.multiply(A.values, B.values, kernel="gather")
+    Ca = plan.multiply(A.values, B.values, kernel="astat")
+    assert torch.equal(Cg.view(torch.int32), Ca.view(torch.int32))
+    g = plan.info.n_pairs // 2
+    if field == "ptr":
+        ptr = plan.pair_ptr().cpu().numpy()
+        k = int(np.nonzero(np.diff(ptr)[:-1] >= 2)[0][0])   # a C diagonal with 2+ entries
+        g = int(ptr[k]) + 1
+        plan.ptr[k + 1] = g          # its entries from g on now count as the next one's
+    else:
+        words = plan.pairs[: plan.info.n_pairs * 32].view(torch.int32).view(-1, 8)
+        col = {"ash": 4, "bsh": 5, "al": 6, "bl": 7}.get(field)
+        if col is not None:
+            words[g, col] += delta
+        else:                        # bb: the start of another B diagonal
+            q = plan.pairs[: plan.info.n_pairs * 32].view(torch.int64).view(-1, 4)
+            bst = B.starts.cpu().tolist()
+            cur = q[g, 1].item()
+            q[g, 1] = bst[(bst.index(cur) + 1) % len(bst)]
+    plan._astat = None
+    with pytest.raises(_lib.DiagpuError) as e:
+        plan.astat_records()
+    assert e.value.status == _lib.ERR_ARG and "symbolic" in str(e.value)
 
 
 def _drop_diagonals(plan, empty):
