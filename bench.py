@@ -48,13 +48,39 @@ def parse_args(argv=None):
                     help="profiling aid: run just one workload (spmv2, spmv2d, spmv2c, "
                          "spmv2rc, spmv1, spmv3, spgemm1..spgemm3 (the squares of the SpMV "
                          "configs' matrices), spgemm4, spgemm5, spgemm4c, spgemm5c, taylor, krylov, "
-                         "propagator, propagator2d, gemmdiag, gemmdiag20, copy, fill20) "
+                         "propagator, propagator2d, gemmdiag, gemmdiag20, spmvhash (the "
+                         "reference SpMV bench's hash band), spgemmbanded (the reference "
+                         "SpGEMM bench's make_banded operands), copy, fill20) "
                          "and print its line")
     return ap.parse_args(argv)
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+_SPIN_CYCLES_PER_US = None
+
+
+def gpu_spin(stream, us: float = 150.0) -> None:
+    """Hold `stream` busy for about `us` microseconds with torch's bounded
+    spin kernel (untimed, before a timed region's first event), so that the
+    launches the host queues next are waiting when that event runs: the
+    host latency of the first launch then stays out of the timed region,
+    which holds exactly the timed steps."""
+    import torch
+    global _SPIN_CYCLES_PER_US
+    if _SPIN_CYCLES_PER_US is None:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            torch.cuda._sleep(100_000)
+            e0.record(stream)
+            torch.cuda._sleep(1_000_000)
+            e1.record(stream)
+        e1.synchronize()
+        _SPIN_CYCLES_PER_US = 1_000_000 / max(1.0, e0.elapsed_time(e1) * 1e3)
+    with torch.cuda.stream(stream):
+        torch.cuda._sleep(max(1, int(_SPIN_CYCLES_PER_US * us)))
 
 
 # --------------------------------------------------------------------------
@@ -68,10 +94,12 @@ def spmv_alg_bytes(R, elem: int, xelem: int | None = None) -> int:
     return elem * R.useful_terms() + xe * (R.cols + R.rows)
 
 
-def time_spmv(cfg: int, dtype, steps: int, warmup: int, seed: int, sets: int, xdtype=None):
+def time_spmv(cfg: int, dtype, steps: int, warmup: int, seed: int, sets: int, xdtype=None,
+              R=None):
     """One SpMV per step over rotating buffer sets (>= 2x the MALL).  dtype is
     the matrix dtype, xdtype the vector dtype (default: dtype; complex64
-    vectors with a float32 matrix use the real-matrix complex-state path)."""
+    vectors with a float32 matrix use the real-matrix complex-state path).
+    R: a prepared Recon matrix (default: benchmark config `cfg`)."""
     import torch
     from diagpu_amd import workloads
     from diagpu_amd.spmv import recon_view, _stream_handle, _SPMV
@@ -80,7 +108,8 @@ def time_spmv(cfg: int, dtype, steps: int, warmup: int, seed: int, sets: int, xd
 
     xdtype = xdtype or dtype
     base = torch.float64 if dtype == torch.float64 else torch.float32
-    R = workloads.spmv_config(cfg, seed=seed, device="cuda", dtype=base)
+    if R is None:
+        R = workloads.spmv_config(cfg, seed=seed, device="cuda", dtype=base)
     if dtype == torch.complex64:        # complex values: (1 + 0.5i) times the real ones
         R.values = (R.values * (1 + 0.5j)).to(torch.complex64).contiguous()
     if xdtype == torch.complex64:
@@ -111,6 +140,7 @@ def time_spmv(cfg: int, dtype, steps: int, warmup: int, seed: int, sets: int, xd
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
+    gpu_spin(stream)
     e0.record(stream)
     for i in range(steps):
         step(i)
@@ -123,6 +153,7 @@ def time_spmv(cfg: int, dtype, steps: int, warmup: int, seed: int, sets: int, xd
     return {
         "R": R, "ms": ms, "alg_bytes": alg, "flops": flops, "sets": nsets,
         "set_bytes": per_set, "gbs": alg / (ms * 1e6), "gflops": flops / (ms * 1e6),
+        "y": bufs[(steps - 1) % nsets][2] if steps else None,
     }
 
 
@@ -146,9 +177,14 @@ def host_cores() -> dict:
             "machine_logical_cpus": os.cpu_count()}
 
 
-def cpu_spmv_baseline(R, seconds: float):
+def cpu_spmv_baseline(R, seconds: float, y_gpu=None):
     """The oracle's OpenMP DIA loop over full SpMVs of the same matrix on the
-    host cores, repeated until `seconds` elapse (1 warm-up run first)."""
+    host cores, repeated until `seconds` elapse (1 warm-up run first).  With
+    y_gpu (the GPU's y for the same matrix and x), the CPU leg also checks
+    it, as the reference bench prints its difference from the CPU result
+    (spmv/bench/bench_cusparse.cu:220-230): every row against the oracle's
+    fp64 sum within tol * sum |terms| (1e-5 fp32, 1e-13 fp64), and the
+    largest difference from the CPU loop's own y."""
     import numpy as np
     from oracle import binding as orc
 
@@ -165,8 +201,32 @@ def cpu_spmv_baseline(R, seconds: float):
         if el >= seconds and reps >= 3:
             break
     ms = el * 1e3 / reps
-    return {"ms": ms, "threads": threads, "reps": reps,
-            "gbs": spmv_alg_bytes(R, vals.itemsize) / (ms * 1e6)}
+    out = {"ms": ms, "threads": threads, "reps": reps,
+           "gbs": spmv_alg_bytes(R, vals.itemsize) / (ms * 1e6)}
+    if y_gpu is not None:
+        g = y_gpu.cpu().numpy().astype(np.float64)
+        y64, ab = orc.spmv_recon_ref64(R.rows, R.cols, off, vals, x)
+        tol = 1e-13 if vals.dtype == np.float64 else 1e-5
+        err = np.abs(g - y64)
+        out["check"] = {
+            "rows": int(R.rows),
+            "max_err_over_term_sum": float(np.max(np.where(ab > 0, err / np.where(ab > 0, ab, 1), 0.0))),
+            "tol": tol, "ok": bool(np.all(err <= tol * ab + 1e-300)),
+            "max_abs_diff_vs_cpu": float(np.max(np.abs(g - y.astype(np.float64)))),
+        }
+    return out
+
+
+def spmv_cpu_record(R, res, seconds: float, what: str) -> dict:
+    """cpu_baseline object for an SpMV record (with the output check)."""
+    c = cpu_spmv_baseline(R, seconds, res.get("y"))
+    rec = {"value": round(c["gbs"], 2), "unit": "GB/s", "cores": c["threads"],
+           **host_cores(), "kind": "port",
+           "sample": f"{c['reps']} full SpMVs of {what} with the oracle's OpenMP DIA loop, "
+                     f"{c['ms']:.3f} ms each"}
+    if "check" in c:
+        rec["check"] = c["check"]
+    return rec
 
 
 def load_traffic(name: str):
@@ -233,12 +293,19 @@ def time_krylov(m: int = 30, t: float = 1.0, reps: int = 5):
 # SpGEMM (configs 4 and 5)
 # --------------------------------------------------------------------------
 
-def cpu_spgemm_baseline(plan, A, B, seconds: float):
+def cpu_spgemm_baseline(plan, A, B, seconds: float, C_gpu=None):
     """The oracle's OpenMP SpGEMM loop (schedule(dynamic) over C diagonals,
     each C diagonal's pairs resolved once, fp32 accumulation) on the host
     cores, over a bounded prefix of C diagonals (about `seconds` of work,
     growing the prefix until it takes at least a tenth of that); GFLOP/s and
-    GB/s from the sample's own useful flops and algorithmic bytes."""
+    GB/s from the sample's own useful flops and algorithmic bytes.
+
+    With C_gpu (the GPU's C for the same plan and operands) the CPU leg also
+    checks it, as the reference bench prints each kernel's difference from
+    the CPU result (spmspm/bench_spmspm.cu:779-796): up to 8 windows of C
+    diagonals spread over the sampled prefix (about 2^20 values each)
+    against the oracle's fp64 sum within 1e-5 * sum |terms|, and against
+    the CPU loop's own fp32 values."""
     import numpy as np
     from oracle import binding as orc
     Av = A.values.cpu().numpy()
@@ -274,19 +341,40 @@ def cpu_spgemm_baseline(plan, A, B, seconds: float):
     flops = float(fl_k[:k].sum())
     # bytes: the sample's C values once plus the A and B values its pairs read
     byt = 4 * (2 * float(ov[: ptr[k]].sum()) + out.size)
-    return {"value": round(flops / sec / 1e9, 2), "unit": "GFLOP/s", "GBs": round(byt / sec / 1e9, 2),
-            "cores": threads, **host_cores(), "kind": "port",
-            "sample": f"C diagonals 0..{k - 1} of {nC} ({100.0 * flops / max(1.0, float(fl_k.sum())):.1f}% "
-                      f"of the flops), {reps} runs of {sec * 1e3:.1f} ms, oracle OpenMP loop"}
+    rec = {"value": round(flops / sec / 1e9, 2), "unit": "GFLOP/s", "GBs": round(byt / sec / 1e9, 2),
+           "cores": threads, **host_cores(), "kind": "port",
+           "sample": f"C diagonals 0..{k - 1} of {nC} ({100.0 * flops / max(1.0, float(fl_k.sum())):.1f}% "
+                     f"of the flops), {reps} runs of {sec * 1e3:.1f} ms, oracle OpenMP loop"}
+    if C_gpu is not None and k > 0:
+        windows, e_prev = [], 0
+        for s0 in np.unique(np.linspace(0, k - 1, min(k, 8)).astype(np.int64)):
+            s0 = max(int(s0), e_prev)
+            if s0 >= k:
+                continue
+            e = s0 + 1
+            while e < k and c_st[e] + c_len[e] - c_st[s0] <= 1 << 20:
+                e += 1
+            windows.append((s0, e))
+            e_prev = e
+        worst, worst_cpu, nvals, ok = 0.0, 0.0, 0, True
+        for s0, e in windows:
+            lo, hi = int(c_st[s0]), int(c_st[e - 1] + c_len[e - 1])
+            ref, ab = orc.spgemm_pairs_f64(Av, Bv, c_len, c_st, ptr, pairs, s0, e)
+            g = C_gpu[lo:hi].cpu().numpy().astype(np.float64)
+            err = np.abs(g - ref)
+            ok &= bool(np.all(err <= 1e-5 * ab + 1e-30))
+            worst = max(worst, float(np.max(np.where(ab > 0, err / np.where(ab > 0, ab, 1), 0.0))))
+            cpu = out[lo - int(c_st[0]): hi - int(c_st[0])].astype(np.float64)
+            worst_cpu = max(worst_cpu, float(np.max(np.abs(g - cpu))))
+            nvals += hi - lo
+        rec["check"] = {"windows": [[int(a), int(b)] for a, b in windows], "values": int(nvals),
+                        "max_err_over_term_sum": worst, "tol": 1e-5, "ok": ok,
+                        "max_abs_diff_vs_cpu": worst_cpu}
+    return rec
 
 
-def compare_kernels(plan, sets, reps: int, alg: int, flops: int, complex_values: bool = False) -> dict:
-    """Every numeric kernel that takes this plan (fp32 or complex64 values),
-    forced, on the same rotated operand sets (the side-by-side run of
-    spmspm/bench_spmspm.cu:518-653): time per product, GFLOP/s, fraction of
-    HBM peak, and whether C is bit for bit the gather's (checked where one
-    more C fits in 4 GB)."""
-    import torch
+def kernel_legs(plan, complex_values: bool = False) -> list[str]:
+    """Every numeric kernel that takes this plan."""
     from diagpu_amd import _lib
     names = ["gather"]
     if not complex_values and plan.band_info()[1].eligible:
@@ -299,25 +387,57 @@ def compare_kernels(plan, sets, reps: int, alg: int, flops: int, complex_values:
             names.append("astat")
         except _lib.DiagpuError:
             pass
+    return names
+
+
+CHECK_BYTES = 24 << 30     # C sizes whose outputs are compared bit for bit on the GPU
+
+
+def compare_kernels(plan, sets, reps: int, alg: int, flops: int, complex_values: bool = False,
+                    rounds: int = 10) -> tuple[dict, dict]:
+    """The automatic choice and every numeric kernel that takes this plan
+    (fp32 or complex64 values), forced, on the same rotated operand sets
+    (the side-by-side run of spmspm/bench_spmspm.cu:518-653), timed in
+    interleaved rounds (auto, k1, k2, ..., auto, k1, ...; each round's
+    window of reps / rounds products opened behind a spin so that every leg
+    sees the same queue and clock state) and reported as the median over
+    rounds of the time per product, with GFLOP/s, the fraction of HBM peak,
+    and whether C is bit for bit the gather's (where C fits CHECK_BYTES).
+    Returns (auto record, {kernel: record})."""
+    import statistics
+    import torch
+    names = kernel_legs(plan, complex_values)
+    legs = ["auto"] + names
     stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     nsets = len(sets)
-    ref = None
-    esz = 8 if complex_values else 4
-    check = plan.info.c_nnz * esz <= (4 << 30)
-    out = {}
-    for k in names:
+    rounds = max(1, min(rounds, reps))
+    per = max(1, reps // rounds)
+    for k in legs:
         for i in range(2):
             plan.numeric(*sets[i % nsets], kernel=k)
+    torch.cuda.synchronize()
+    times = {k: [] for k in legs}
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * len(legs))]
+    for r in range(rounds):
+        gpu_spin(stream, 100.0)
+        for j, k in enumerate(legs):
+            ev[2 * j].record(stream)
+            for i in range(per):
+                plan.numeric(*sets[(r * per + i) % nsets], kernel=k)
+            ev[2 * j + 1].record(stream)
         torch.cuda.synchronize()
-        e0.record(stream)
-        for i in range(reps):
-            plan.numeric(*sets[i % nsets], kernel=k)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        kms = e0.elapsed_time(e1) / reps
+        for j, k in enumerate(legs):
+            times[k].append(ev[2 * j].elapsed_time(ev[2 * j + 1]) / per)
+    esz = 8 if complex_values else 4
+    check = plan.info.c_nnz * esz <= CHECK_BYTES
+    ref = None
+    out = {}
+    for k in ["gather"] + [x for x in legs if x != "gather"]:
+        kms = statistics.median(times[k])
         rec = {"numeric_ms": round(kms, 5), "GFLOPs": round(flops / (kms * 1e6), 1),
-               "frac_hbm": round(alg / (kms * 1e6) / HBM_PEAK_GBS, 4), "same_bits_as_gather": None}
+               "frac_hbm": round(alg / (kms * 1e6) / HBM_PEAK_GBS, 4),
+               "min_ms": round(min(times[k]), 5), "max_ms": round(max(times[k]), 5),
+               "rounds": rounds, "products_per_round": per, "same_bits_as_gather": None}
         if k == "band_mfma":
             rec["mfma_utilisation"] = round(plan.mfma_utilisation(), 4)
             rec["mfma_blocks_per_16_rows"] = plan.band_info()[1].mfma_blocks
@@ -332,15 +452,47 @@ def compare_kernels(plan, sets, reps: int, alg: int, flops: int, complex_values:
             if not rec["same_bits_as_gather"]:
                 rec["max_abs_diff_vs_gather"] = float((c - ref).abs().max())
         out[k] = rec
-    return out
+    del ref
+    auto = out.pop("auto")
+    return auto, out
+
+
+def mfma_record(plan) -> dict:
+    """Whether the fp32 MFMA band kernel (dense 16x16x4 tiles over the band)
+    takes this plan, its utilisation if so, and the reason if not."""
+    bi = plan.band_info()[1]
+    if bi.mfma_eligible:
+        return {"eligible": True, "utilisation": round(plan.mfma_utilisation(), 4),
+                "blocks_per_16_rows": bi.mfma_blocks}
+    na, nb = plan.A.offsets.numel(), plan.B.offsets.numel()
+    sa = bi.a_off_max - bi.a_off_min
+    sb = bi.b_off_max - bi.b_off_min
+    dens = (na / (sa + 1)) * (nb / (sb + 1))
+    return {"eligible": False,
+            "reason": (f"A's {na} offsets span {sa + 1} columns and B's {nb} span {sb + 1} "
+                       f"(the MFMA band kernel takes A spans up to 32 and A + B up to 48): "
+                       f"a dense tile contraction over this band would find "
+                       f"{100 * dens:.3g}% of its multiply-adds useful (about "
+                       f"{1 / max(dens, 1e-12):.0f} issued per useful one), and C has "
+                       f"{plan.info.n_pairs / max(1, plan.info.c_ndiag):.2f} plan entries per "
+                       f"diagonal, so there is no dense tile to give the matrix cores"),
+            "a_span": sa + 1, "b_span": sb + 1, "useful_fraction_dense": dens}
 
 
 def time_spgemm(cfg: int, seed: int, reps: int, complex_values: bool = False,
-                cpu_seconds: float = 0.0):
+                cpu_seconds: float = 0.0, operands=None, name: str | None = None,
+                rounds: int = 10):
+    """One SpGEMM configuration: the plan (symbolic phase timed on the
+    device), then compare_kernels over rotated operand sets, the CPU
+    baseline with its output check, and the MFMA record.  operands: (A, B)
+    (default: benchmark config `cfg`)."""
     import torch
     from diagpu_amd import workloads
     from diagpu_amd.spgemm import SpgemmPlan
-    A, B = workloads.spgemm_config(cfg, seed=seed, device="cuda")
+    if operands is None:
+        A, B = workloads.spgemm_config(cfg, seed=seed, device="cuda")
+    else:
+        A, B = operands
     if complex_values:   # same structure, values v + i * roll(v)
         A = workloads.HM(A.n, A.offsets, A.lengths, A.starts,
                          torch.complex(A.values, torch.roll(A.values, 1)).contiguous())
@@ -366,34 +518,51 @@ def time_spgemm(cfg: int, seed: int, reps: int, complex_values: bool = False,
     sets = [(A.values.clone(), B.values.clone(),
              torch.empty(plan.info.c_nnz, dtype=A.values.dtype, device="cuda"))
             for _ in range(nsets)]
-    for i in range(2):
-        plan.numeric(*sets[i % nsets])
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for i in range(reps):
-        plan.numeric(*sets[i % nsets])
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / reps
     alg = esz * (A.nnz + B.nnz + plan.info.c_nnz)
     flops = plan.info.useful_flops * (4 if complex_values else 1)   # complex MAC = 4 real
-    kernels = compare_kernels(plan, sets, max(3, reps // 2), alg, flops, complex_values)
-    return {
-        "workload": f"spgemm_cfg{cfg}" if cfg >= 4 else f"spgemm_HxH_cfg{cfg}",
+    auto, kernels = compare_kernels(plan, sets, reps, alg, flops, complex_values, rounds)
+    ms = auto["numeric_ms"]
+    kern = plan.kernel_for(torch.complex64 if complex_values else torch.float32)
+    rec = {
+        "workload": name or (f"spgemm_cfg{cfg}" if cfg >= 4 else f"spgemm_HxH_cfg{cfg}"),
         "dtype": "c64" if complex_values else "f32", "n": A.n,
         "A_diags": A.ndiag, "B_diags": B.ndiag, "C_diags": plan.info.c_ndiag,
         "pairs": plan.info.n_pairs, "max_pairs_per_C": plan.info.max_pairs,
         "C_nnz": plan.info.c_nnz, "numeric_ms": round(ms, 5),
-        "kernel": plan.kernel_for(torch.complex64 if complex_values else torch.float32),
+        "numeric_min_ms": auto["min_ms"], "numeric_max_ms": auto["max_ms"],
+        "kernel": kern,
         "symbolic_ms": round(sym_ms, 5), "symbolic_wall_ms_first": round(sym_wall_ms, 3),
         "GFLOPs": round(flops / (ms * 1e6), 1), "useful_flops": flops,
         "GBs": round(alg / (ms * 1e6), 1), "frac_hbm": round(alg / (ms * 1e6) / HBM_PEAK_GBS, 4),
         "alg_bytes": alg, "buffer_sets": nsets,
         "total_ms": round(ms + sym_ms, 5),
         "kernels": kernels,
-        "cpu_baseline": (cpu_spgemm_baseline(plan, A, B, cpu_seconds)
-                         if cpu_seconds > 0 and not complex_values else None),
     }
+    if not complex_values:
+        rec["mfma"] = mfma_record(plan)
+    if cpu_seconds > 0 and not complex_values:
+        plan.numeric(*sets[0])               # the automatic kernel's C, checked by the CPU leg
+        torch.cuda.synchronize()
+        rec["cpu_baseline"] = cpu_spgemm_baseline(
+            plan, workloads.HM(A.n, A.offsets, A.lengths, A.starts, sets[0][0]),
+            workloads.HM(B.n, B.offsets, B.lengths, B.starts, sets[0][1]), cpu_seconds,
+            C_gpu=sets[0][2])
+    else:
+        rec["cpu_baseline"] = None
+    return rec
+
+
+def time_spgemm_banded(reps: int, cpu_seconds: float):
+    """The reference SpGEMM bench's own operands (spmspm/bench_spmspm.cu:
+    455-471): A = make_banded(100000, 16, 1234), B = make_banded(100000, 16,
+    5678), 33 diagonals each, C on 65 diagonals; the reference times its
+    kernels on this product (:518-653)."""
+    from diagpu_amd import workloads
+    n, w = 100_000, 16
+    A = workloads.make_banded(n, w, 1234, device="cuda")
+    B = workloads.make_banded(n, w, 5678, device="cuda")
+    return time_spgemm(0, 0, reps, cpu_seconds=cpu_seconds, operands=(A, B),
+                       name=f"spgemm_make_banded_n{n}_w{w}")
 
 
 def time_taylor(order: int = 6, t: float = 0.05):
@@ -502,10 +671,11 @@ def time_propagator(grid: str = "3d", order: int = 6, dt: float = 0.02, m: int =
 def time_gemm_diag(n: int = 4096, hb: int = 10, reps: int = 100, cpu_seconds: float = 0.0):
     """gemm_diag on row-packed operands (gemm_diag/gemm_diag.cu:9-15) with the
     reference driver's default shape (n = 4096, offsets -hb..hb, values
-    U(0.5, 1.5), gemm_diag.cu:467-486): the plan once, then `reps` timed
-    numeric phases, then every kernel that takes the plan side by side,
-    including the fp32 MFMA band kernel with its utilisation (useful /
-    issued flops from its tile geometry).  The reference kernel has no
+    U(0.5, 1.5), gemm_diag.cu:467-486): the plan once, then the automatic
+    choice and every kernel that takes the plan in interleaved rounds of
+    `reps` products each (compare_kernels), including the fp32 MFMA band
+    kernel with its utilisation (useful / issued flops from its tile
+    geometry).  The reference kernel has no
     tensor-core instructions (products in shared memory, a sequential
     reduction and atomicAdd).  With cpu_seconds > 0 the oracle's OpenMP
     SpGEMM loop runs the same plan over the same row-packed operands on the
@@ -529,35 +699,32 @@ def time_gemm_diag(n: int = 4096, hb: int = 10, reps: int = 100, cpu_seconds: fl
     plan, C = gemm_diag(n, off, DA, off, DB)
     torch.cuda.synchronize()
     first_ms = (time.perf_counter() - t0) * 1e3
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    for _ in range(3):
-        plan.numeric(DA, DB, C)
-    e0.record(stream)
-    for _ in range(reps):
-        plan.numeric(DA, DB, C)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / reps
     nnz = sum(n - abs(d) for d in offs)
     alg = 4 * (2 * nnz + plan.info.c_nnz)
     flops = plan.info.useful_flops
-    kernels = compare_kernels(plan, [(DA, DB, C)], max(5, reps // 2), alg, flops)
+    auto, kernels = compare_kernels(plan, [(DA, DB, C)], reps, alg, flops)
+    ms = auto["numeric_ms"]
     kern = plan.kernel_for()
-    return {"workload": f"gemm_diag_n{n}_hb{hb}", "n": n, "A_diags": len(offs),
-            "B_diags": len(offs), "C_diags": plan.info.c_ndiag, "numeric_ms": round(ms, 5),
-            "kernel": kern, "first_call_ms": round(first_ms, 3),
-            "GFLOPs": round(flops / (ms * 1e6), 1),
-            "GBs": round(alg / (ms * 1e6), 1), "frac_hbm": round(alg / (ms * 1e6) / HBM_PEAK_GBS, 4),
-            "alg_bytes": alg,
-            # useful / issued flops of the kernel that ran; None when that kernel
-            # issues no MFMA (the MFMA band kernel's figure is under kernels)
-            "mfma_utilisation": (round(plan.mfma_utilisation(), 4) if kern == "band_mfma" else None),
-            "kernels": kernels,
-            # the plan's pair starts index the row-packed arrays directly
-            "cpu_baseline": (cpu_spgemm_baseline(plan, types.SimpleNamespace(values=DA),
-                                                 types.SimpleNamespace(values=DB), cpu_seconds)
-                             if cpu_seconds > 0 else None)}
+    rec = {"workload": f"gemm_diag_n{n}_hb{hb}", "n": n, "A_diags": len(offs),
+           "B_diags": len(offs), "C_diags": plan.info.c_ndiag, "numeric_ms": round(ms, 5),
+           "numeric_min_ms": auto["min_ms"], "numeric_max_ms": auto["max_ms"],
+           "kernel": kern, "first_call_ms": round(first_ms, 3),
+           "GFLOPs": round(flops / (ms * 1e6), 1),
+           "GBs": round(alg / (ms * 1e6), 1), "frac_hbm": round(alg / (ms * 1e6) / HBM_PEAK_GBS, 4),
+           "alg_bytes": alg,
+           # useful / issued flops of the kernel that ran; None when that kernel
+           # issues no MFMA (the MFMA band kernel's figure is under kernels)
+           "mfma_utilisation": (round(plan.mfma_utilisation(), 4) if kern == "band_mfma" else None),
+           "mfma": mfma_record(plan),
+           "kernels": kernels, "cpu_baseline": None}
+    if cpu_seconds > 0:
+        plan.numeric(DA, DB, C)
+        torch.cuda.synchronize()
+        # the plan's pair starts index the row-packed arrays directly
+        rec["cpu_baseline"] = cpu_spgemm_baseline(plan, types.SimpleNamespace(values=DA),
+                                                  types.SimpleNamespace(values=DB), cpu_seconds,
+                                                  C_gpu=C)
+    return rec
 
 
 def copy_calibration(steps: int):
@@ -612,7 +779,7 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
         return 2
-    from diagpu_amd import _lib
+    from diagpu_amd import _lib, workloads
     _lib.load()
 
     if args.only:
@@ -621,6 +788,14 @@ def main(argv=None) -> int:
             print(json.dumps(copy_calibration(args.steps)), flush=True)
         elif w == "fill20":
             print(json.dumps(fill_calibration(args.steps)), flush=True)
+        elif w == "spmvhash":
+            R = workloads.hash_band(device="cuda")
+            res = time_spmv(0, torch.float32, args.steps, args.warmup, args.seed, args.sets, R=R)
+            rec = spmv_record(0, torch.float32, res)
+            rec["workload"] = "spmv_hash_band_N1048576"
+            print(json.dumps(rec), flush=True)
+        elif w == "spgemmbanded":
+            print(json.dumps(time_spgemm_banded(args.steps, 0.0)), flush=True)
         elif w.startswith("spmv"):
             cfg = int(w[4])
             suffix = w[5:]
@@ -656,13 +831,12 @@ def main(argv=None) -> int:
     cpu = None
     if args.cpu_seconds > 0:
         log(f"CPU baseline ({args.cpu_seconds:.0f} s budget)")
-        c = cpu_spmv_baseline(R, args.cpu_seconds)
-        cpu = {"value": round(c["gbs"], 2), "unit": "GB/s", "cores": c["threads"],
-               **host_cores(), "kind": "port",
-               "sample": f"{c['reps']} full SpMVs of the config-2 matrix (n=4194304, fp32) "
-                         f"with the oracle's OpenMP DIA loop, {c['ms']:.2f} ms each, "
-                         f"{os.cpu_count()} logical CPUs visible"}
-        log(f"CPU baseline: {c['gbs']:.2f} GB/s on {c['threads']} threads")
+        cpu = spmv_cpu_record(R, head, args.cpu_seconds,
+                              "the config-2 matrix (n=4194304, fp32)")
+        cpu["sample"] += f", {os.cpu_count()} logical CPUs visible"
+        log(f"CPU baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} threads, "
+            f"GPU output check ok={cpu.get('check', {}).get('ok')}")
+    head.pop("y", None)
 
     extras = {}
     if args.extras:
@@ -672,13 +846,11 @@ def main(argv=None) -> int:
             try:
                 res = time_spmv(cfg, dt, 200, 20, args.seed, 0, xt)
                 rec = spmv_record(cfg, dt, res, xt)
-                if cfg in (1, 3) and dt == torch.float32 and args.cpu_seconds > 0:
-                    c = cpu_spmv_baseline(res["R"], min(2.0, args.cpu_seconds))
-                    rec["cpu_baseline"] = {
-                        "value": round(c["gbs"], 2), "unit": "GB/s", "cores": c["threads"],
-                        **host_cores(), "kind": "port",
-                        "sample": f"{c['reps']} full SpMVs of the config-{cfg} matrix with the "
-                                  f"oracle's OpenMP DIA loop, {c['ms']:.3f} ms each"}
+                if xt is None and dt != torch.complex64 and args.cpu_seconds > 0:
+                    rec["cpu_baseline"] = spmv_cpu_record(
+                        res["R"], res, min(2.0, args.cpu_seconds),
+                        f"the config-{cfg} matrix ({rec['dtype']}, accumulation in "
+                        f"{'fp64' if dt == torch.float64 else 'fp32'})")
                 extras[f"spmv_cfg{cfg}_{rec['dtype']}"] = rec
                 log(f"extra spmv cfg{cfg} {rec['dtype']}: {res['gbs']:.1f} GB/s")
                 del res
@@ -695,16 +867,39 @@ def main(argv=None) -> int:
             del res
         except Exception as e:
             extras["spmv_cfg2_f32_warm"] = {"error": repr(e)}
+        # the reference SpMV bench's own matrix (bench_cusparse.cu:84-144)
+        try:
+            Rh = workloads.hash_band(device="cuda")
+            res = time_spmv(0, torch.float32, 400, 40, args.seed, 0, R=Rh)
+            rec = spmv_record(0, torch.float32, res)
+            rec["workload"] = "spmv_hash_band_N1048576"
+            rec["offsets"] = workloads.HASH_BAND_OFFSETS
+            if args.cpu_seconds > 0:
+                rec["cpu_baseline"] = spmv_cpu_record(Rh, res, min(2.0, args.cpu_seconds),
+                                                      "the reference bench's 9-diagonal hash band")
+            extras["spmv_hash_band_N1048576"] = rec
+            log(f"extra spmv hash band: {res['gbs']:.1f} GB/s")
+            del res, Rh
+        except Exception as e:
+            extras["spmv_hash_band_N1048576"] = {"error": repr(e)}
         # configs 1-3 are SpMV matrices: their SpGEMM figure is H H
-        for cfg, reps in ((1, 100), (2, 50), (3, 5), (4, 50), (5, 10)):
+        for cfg, reps, rounds in ((1, 100, 10), (2, 50, 10), (3, 6, 3), (4, 50, 10), (5, 20, 10)):
             try:
-                rec = time_spgemm(cfg, args.seed, reps, cpu_seconds=min(3.0, args.cpu_seconds))
+                rec = time_spgemm(cfg, args.seed, reps, cpu_seconds=min(3.0, args.cpu_seconds),
+                                  rounds=rounds)
                 extras[rec["workload"]] = rec
                 log(f"extra spgemm cfg{cfg}: {rec['GFLOPs']} GFLOP/s, {rec['GBs']} GB/s")
                 torch.cuda.empty_cache()
             except Exception as e:
                 extras[f"spgemm_cfg{cfg}"] = {"error": repr(e)}
             torch.cuda.empty_cache()
+        try:
+            rec = time_spgemm_banded(50, min(3.0, args.cpu_seconds))
+            extras[rec["workload"]] = rec
+            log(f"extra {rec['workload']}: {rec['GFLOPs']} GFLOP/s, {rec['GBs']} GB/s")
+            torch.cuda.empty_cache()
+        except Exception as e:
+            extras["spgemm_make_banded"] = {"error": repr(e)}
         try:
             rec = time_krylov()
             extras["krylov_expm"] = rec

@@ -211,43 +211,36 @@ class SpgemmPlan:
         """The automatic choice after the band kernel: the A-stationary kernel
         where A's diagonals fit its LDS (at most DIAGPU_ASTAT_MAX_A, or
         DIAGPU_ASTAT_MAX_A_C64 for complex values), n >= 4096, B values are
-        addressable with int32, and the plan reuses the staged A runs:
+        addressable with int32, and
 
-          fp32:      >= 16 entries per A diagonal, or >= 32 entries with
-                     >= 4 per A diagonal and >= 1.5 per C diagonal, or
-                     n >= 2^22;
-          complex64: n >= 2^18 with >= 16 C diagonals (every wave of a
-                     workgroup busy), or >= 32 entries with >= 4 per A
-                     diagonal, or n >= 2^22.
+          fp32:      any plan, except one of fewer than 16 entries at
+                     2^19 <= n < 2^22;
+          complex64: n >= 2^16, or >= 3 entries per A diagonal.
 
-        The thresholds separate what was measured against the gather on
-        MI355X: fp32 stencil products gain 26-30 % (9-point square at
-        n = 2^22: 135 vs 183 us), while config 4 (63 entries over 47 C
-        diagonals: a near-streaming product that the gather runs at the
-        write-bound rate) ties and config 2's square (25 entries: too little
-        work per staged block) loses (80 vs 58 us); random plans with 2-3
-        entries per A diagonal went either way (time ratios 0.73-1.22) and
-        are left to the gather.  Complex values gained at every measured shape from
-        n = 2^18 up with >= 16 C diagonals (the complex gather re-reads the
-        operand runs at its items' edges), and below that where each A
-        diagonal feeds >= 4 entries.  (Ratios measured one buffer set at a
-        time; under the benchmark's rotating sets complex config 4 gains
-        4 %: 128 vs 133 us.)  From n = 2^22 the kernel's longer row blocks
-        (16 or 8 rows per lane for few, short C diagonals) win on every
-        measured product, config 2's square included (rotating sets: fp32
-        92 vs 102 us, complex 183 vs 226)."""
+        fp32 thresholds from the gather and this kernel timed side by side
+        in interleaved rounds over rotated operand sets (median of 10) on
+        MI355X, 50 shapes from n = 4096 to 2^22: stencil, band and random
+        products with 1 to 64 entries per A diagonal and 1 to 16 per C
+        diagonal.  This kernel was faster on 48: by 30-60 % below n = 2^19
+        (the gather's per-entry operand reads dominate small products),
+        2-20 % above it, config 4 by 3 % (43.3 vs 44.7 us).  The gather was
+        faster on the 9-entry square of the tridiagonal band at n = 2^20
+        (11.4 vs 12.7 us: too little work per staged block) and tied on a
+        36-entry random product at n = 2^20; from n = 2^22 this kernel's
+        longer row blocks win again (tridiagonal square 42.5 vs 51.4 us).
+        Complex values, timed the same way on 25 shapes from n = 4096 to
+        2^22: this kernel was faster on 24, by 5-50 % (the complex gather
+        re-reads the operand runs at its items' edges); the gather was
+        faster (5.9 vs 6.3 us) on a 4096-row product with 2 entries per A
+        diagonal."""
         na = self.A.offsets.numel()
         inf = self.info
         if inf.c_ndiag == 0 or self.n < 4096:
             return False
-        reuse = inf.n_pairs >= 32 and inf.n_pairs >= 4 * na
-        big = self.n >= 1 << 22
         if dtype == torch.float32:
-            ok = na <= _lib.ASTAT_MAX_A and (inf.n_pairs >= 16 * na or big
-                                             or (reuse and 2 * inf.n_pairs >= 3 * inf.c_ndiag))
+            ok = na <= _lib.ASTAT_MAX_A and not (inf.n_pairs < 16 and 1 << 19 <= self.n < 1 << 22)
         elif dtype == torch.complex64:
-            ok = na <= _lib.ASTAT_MAX_A_C64 and ((self.n >= 1 << 18 and inf.c_ndiag >= 16)
-                                                 or reuse or big)
+            ok = na <= _lib.ASTAT_MAX_A_C64 and (self.n >= 1 << 16 or inf.n_pairs >= 3 * na)
         else:
             ok = False
         if not ok:

@@ -97,6 +97,61 @@ def random_band_offsets(count: int, half_width: int, seed: int) -> list[int]:
     return sorted({0, *map(int, pick)})
 
 
+_M32 = 0xFFFFFFFF
+
+
+def _mul32(h: torch.Tensor, c: int) -> torch.Tensor:
+    """(h * c) mod 2^32 for int64 h in [0, 2^32), in two 16-bit halves of c
+    so that no int64 product overflows."""
+    lo = h * (c & 0xFFFF)
+    hi = (h * (c >> 16)) & 0xFFFF
+    return (lo + (hi << 16)) & _M32
+
+
+def _hash_unit(h: torch.Tensor) -> torch.Tensor:
+    """Low 16 bits of h onto [-1, 1) in steps of 2^-15, in fp32 (exact)."""
+    return (h & 0xFFFF).to(torch.float32) * (2.0 / 65536.0) - 1.0
+
+
+def hval(r: torch.Tensor, d: int) -> torch.Tensor:
+    """H[r, r + d] of the reference SpMV benchmark's band (integer hash of
+    row and offset, spmv/bench/bench_cusparse.cu:70-76) for int64 rows r."""
+    h = _mul32(r, 2654435761)
+    h = h ^ (((d + 1024) * 40503) & _M32)
+    h = h ^ (h >> 13)
+    h = _mul32(h, 0x5BD1E995)
+    h = h ^ (h >> 15)
+    return _hash_unit(h)
+
+
+def xval(i: torch.Tensor) -> torch.Tensor:
+    """x[i] of the same benchmark (bench_cusparse.cu:78-82) for int64 i."""
+    h = _mul32(i, 2246822519)
+    h = h ^ (h >> 13)
+    h = _mul32(h, 0x85EBCA6B)
+    h = h ^ (h >> 16)
+    return _hash_unit(h)
+
+
+HASH_BAND_OFFSETS = [-9, -5, -2, -1, 0, 1, 2, 5, 9]   # bench_cusparse.cu:84-87
+
+
+def hash_band(N: int = 1 << 20, offsets=HASH_BAND_OFFSETS, device="cuda") -> Recon:
+    """The reference SpMV benchmark's matrix and x (bench_cusparse.cu:84-98,
+    Recon fill :131-144): offsets descending, Recon[k][c] = hval(c - d_k,
+    d_k) where row c - d_k exists, zero elsewhere; x[i] = xval(i).  Built
+    on the device, value for value the reference's."""
+    offs = sorted({int(d) for d in offsets}, reverse=True)
+    c = torch.arange(N, device=device, dtype=torch.int64)
+    vals = torch.zeros(len(offs), N, device=device, dtype=torch.float32)
+    for k, d in enumerate(offs):
+        r = c - d
+        ok = (r >= 0) & (r < N)
+        vals[k] = torch.where(ok, hval(r.clamp(0, N - 1), d), vals[k])
+    return Recon(N, N, torch.tensor(offs, dtype=torch.int32, device=device),
+                 vals.reshape(-1).contiguous(), xval(c).contiguous())
+
+
 def spmv_config(cfg: int, seed: int = 0, device="cuda", dtype=torch.float32) -> Recon:
     """Benchmark SpMV configs 1-3: the tridiagonal n = 2^20 band, the
     2048 x 2048 Poisson stencil, and the random 64-diagonal band."""
@@ -197,6 +252,29 @@ def recon_to_hm(R: Recon) -> HM:
              for k in order]
     vals = torch.cat(parts).contiguous() if parts else R.values.new_empty(0)
     return hm_from_values(n, [offs[k] for k in order], vals, R.values.device)
+
+
+def mt19937_uniform(seed: int, count: int, a: float, b: float) -> np.ndarray:
+    """count draws of std::uniform_real_distribution<float>(a, b) over
+    std::mt19937(seed) as libstdc++ computes them: one 32-bit MT19937 output
+    per value (numpy's RandomState is MT19937 with the same init_genrand
+    seeding), generate_canonical<float, 24> = g / 2^32 in float (a result of
+    1.0 replaced by the float just below it), then g * (b - a) + a in float."""
+    raw = np.random.RandomState(seed).randint(0, 2 ** 32, size=count, dtype=np.uint32)
+    g = raw.astype(np.float32) / np.float32(2.0 ** 32)
+    g = np.where(g >= 1, np.nextafter(np.float32(1), np.float32(0)), g).astype(np.float32)
+    return (g * (np.float32(b) - np.float32(a)) + np.float32(a)).astype(np.float32)
+
+
+def make_banded(n: int, w: int, seed: int, device="cuda") -> HM:
+    """make_banded of the reference SpGEMM benchmark
+    (spmspm/bench_spmspm.cu:89-106): offsets -w..w (those with n - |d| > 0),
+    each diagonal's n - |d| values drawn in order from U(-1, 1) with
+    std::mt19937(seed), libstdc++'s mapping (mt19937_uniform)."""
+    offs = [d for d in range(-w, w + 1) if n - abs(d) > 0]
+    total = sum(n - abs(d) for d in offs)
+    vals = torch.from_numpy(mt19937_uniform(seed, total, -1.0, 1.0)).to(device)
+    return hm_from_values(n, offs, vals, device)
 
 
 def spgemm_config(cfg: int, seed: int = 0, device="cuda") -> tuple[HM, HM]:

@@ -299,17 +299,15 @@ public:
                      info_.n_pairs >= 3 * info_.c_ndiag && int64_t(n) >= 512 * 256;
         if (band_auto_) prepare_band(stream);
         // The A-stationary kernel's records where the automatic choice may
-        // take it: A fits its LDS and each A diagonal feeds >= 16 entries.
-        // The records serve both value types (the band kernel is fp32 only);
-        // the rules are SpgemmPlan.uses_astat's in diagpu_amd/spgemm.py.
+        // take it.  The records serve both value types (the band kernel is
+        // fp32 only); the rules are SpgemmPlan.uses_astat's in
+        // diagpu_amd/spgemm.py, with the measurements behind them.
         const int64_t np = info_.n_pairs, nc = info_.c_ndiag, na = a_ndiag;
         const bool sized = nc > 0 && int64_t(n) >= 4096;
-        const bool reuse = np >= 32 && np >= 4 * na;
-        const bool big = int64_t(n) >= (1 << 22);
-        astat_auto_ = !uses_band() && sized && na <= DIAGPU_ASTAT_MAX_A &&
-                      (np >= 16 * na || big || (reuse && 2 * np >= 3 * nc));
+        const bool thin_mid = np < 16 && int64_t(n) >= (1 << 19) && int64_t(n) < (1 << 22);
+        astat_auto_ = !uses_band() && sized && na <= DIAGPU_ASTAT_MAX_A && !thin_mid;
         astat_auto_c64_ = sized && na <= DIAGPU_ASTAT_MAX_A_C64 &&
-                          ((int64_t(n) >= (1 << 18) && nc >= 16) || reuse || big);
+                          (int64_t(n) >= (1 << 16) || np >= 3 * na);
         if (astat_auto_ || astat_auto_c64_) {
             try {
                 prepare_astat(stream);
@@ -328,14 +326,13 @@ public:
     bool uses_band() const { return band_auto_ && band_.eligible; }
     // True where NumericKernel::Auto runs the A-stationary kernel for fp32
     // values: the band kernel does not take the plan, A has at most
-    // DIAGPU_ASTAT_MAX_A diagonals, n >= 4096, and the plan has >= 16
-    // entries per A diagonal, or >= 32 entries with >= 4 per A diagonal and
-    // >= 1.5 per C diagonal (config 4, 63 entries over 47 C diagonals, is a
-    // near-streaming product that the gather runs as fast), or n >= 2^22.
+    // DIAGPU_ASTAT_MAX_A diagonals, n >= 4096, and the plan is not one of
+    // fewer than 16 entries at 2^19 <= n < 2^22 (there the gather has more
+    // work per launch to hide its operand reads: the tridiagonal square at
+    // n = 2^20 takes 11.4 us on the gather, 12.7 on this kernel).
     bool uses_astat() const { return astat_auto_; }
     // The same for complex64 values: A has at most DIAGPU_ASTAT_MAX_A_C64
-    // diagonals, n >= 4096, and n >= 2^18 with >= 16 C diagonals, or >= 32
-    // entries with >= 4 per A diagonal, or n >= 2^22.
+    // diagonals, n >= 4096, and n >= 2^16 or >= 3 entries per A diagonal.
     bool uses_astat_c64() const { return astat_auto_c64_; }
 
     // C_vals (device, info().c_nnz values) = A * B; asynchronous on `stream`

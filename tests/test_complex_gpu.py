@@ -438,9 +438,8 @@ def test_complex_astat_real_values_equal_real_kernel(dev):
 
 def test_complex_astat_choice_and_capacity(dev):
     """auto takes the complex A-stationary kernel where A fits (at most
-    DIAGPU_ASTAT_MAX_A_C64 diagonals), n >= 4096, and n >= 2^18 with >= 16
-    C diagonals, or the plan has >= 32 entries with >= 4 per A diagonal, or
-    n >= 2^22; the gather otherwise.  More A diagonals are refused with DIAGPU_ERR_CAPACITY
+    DIAGPU_ASTAT_MAX_A_C64 diagonals), n >= 4096, and n >= 2^16 or the plan
+    has >= 3 entries per A diagonal; the gather otherwise.  More A diagonals are refused with DIAGPU_ERR_CAPACITY
     before any launch; the band kernel takes fp32 only."""
     from diagpu_amd import _lib
     from diagpu_amd.spgemm import SpgemmPlan
@@ -454,14 +453,17 @@ def test_complex_astat_choice_and_capacity(dev):
     A4, B4 = workloads.spgemm_config(4, seed=4, device=dev)      # n = 2^20, 63 C diagonals
     p4 = SpgemmPlan(_complexify(A4, 1), _complexify(B4, 2))
     assert p4.kernel_for(torch.complex64) == "astat"
-    assert SpgemmPlan(A4, B4).kernel_for(torch.float32) == "gather"   # 63 entries, 47 C diagonals
-    lo_a = _offsets(rng, 64, -4096, 4096)                        # 2 entries per A diagonal
-    lo = SpgemmPlan(_complexify(workloads.hm_random(1 << 16, lo_a, seed=7, device=dev), 1),
-                    _complexify(workloads.hm_random(1 << 16, [-9, 4], seed=8, device=dev), 2))
+    assert SpgemmPlan(A4, B4).kernel_for(torch.float32) == "astat"    # 63 entries, 47 C diagonals
+    lo_a = _offsets(rng, 64, -2000, 2000)                        # 2 entries per A diagonal
+    lo = SpgemmPlan(_complexify(workloads.hm_random(8192, lo_a, seed=7, device=dev), 1),
+                    _complexify(workloads.hm_random(8192, [-9, 4], seed=8, device=dev), 2))
     assert lo.kernel_for(torch.complex64) == "gather"
+    lo16 = SpgemmPlan(_complexify(workloads.hm_random(1 << 16, lo_a, seed=7, device=dev), 1),
+                      _complexify(workloads.hm_random(1 << 16, [-9, 4], seed=8, device=dev), 2))
+    assert lo16.kernel_for(torch.complex64) == "astat"            # the same at n = 2^16
     five = workloads.hm_random(1 << 18, [-512, -1, 0, 1, 512], seed=9, device=dev)
     p5 = SpgemmPlan(_complexify(five, 1), _complexify(five, 2))    # 13 C diagonals, 25 entries
-    assert p5.kernel_for(torch.complex64) == "gather"
+    assert p5.kernel_for(torch.complex64) == "astat"
     P2 = _complexify(workloads.recon_to_hm(workloads.spmv_config(2, seed=1, device=dev)), 1)
     assert SpgemmPlan(P2, P2).kernel_for(torch.complex64) == "astat"   # the same at n = 2^22
     wide = _complexify(workloads.hm_random(4096, _offsets(rng, _lib.ASTAT_MAX_A_C64 + 1, -300, 300),

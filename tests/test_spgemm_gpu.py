@@ -468,12 +468,12 @@ def test_astat_kernel_same_bits_as_gather(dev, oracle, n, case):
 
 def test_astat_kernel_choice_and_capacity(dev):
     """auto picks the A-stationary kernel for the square of a 64-diagonal
-    band over +-512 (64 entries per A diagonal), for gemm_diag's band below
-    512 row blocks (21 per A diagonal) and for the 9-point stencil's square,
-    the band kernel above 512 row blocks, the gather for config 4 (63
-    entries over 47 C diagonals) and the 5-point square (25 entries) below
-    n = 2^22, the A-stationary kernel for config 2's square; more than
-    DIAGPU_ASTAT_MAX_A A diagonals are refused with DIAGPU_ERR_CAPACITY."""
+    band over +-512, for gemm_diag's band below 512 row blocks, for the
+    9-point and 5-point stencils' squares, config 4 and config 2's square,
+    the band kernel above 512 row blocks, the gather below n = 4096 and for
+    plans of fewer than 16 entries at 2^19 <= n < 2^22 (the tridiagonal
+    square at n = 2^20); more than DIAGPU_ASTAT_MAX_A A diagonals are
+    refused with DIAGPU_ERR_CAPACITY."""
     rng = np.random.default_rng(3)
     n = 1 << 18
     offs = _random_offsets(rng, 63, -512, 512)
@@ -490,9 +490,11 @@ def test_astat_kernel_choice_and_capacity(dev):
     g5 = workloads.hm_random(2048, range(-10, 11), 1, dev)       # below n = 4096: the gather
     assert SpgemmPlan(g5, g5).kernel_for() == "gather"
     A4, B4 = workloads.spgemm_config(4, seed=4, device=dev)
-    assert SpgemmPlan(A4, B4).kernel_for() == "gather"
-    # stencil products: >= 32 entries, >= 4 per A diagonal, >= 1.5 per C
-    # diagonal (the 9-point square: 81 entries over 25 C diagonals)
+    assert SpgemmPlan(A4, B4).kernel_for() == "astat"           # 63 entries over 47 C diagonals
+    T = workloads.hm_random(1 << 20, [-1, 0, 1], 7, dev)
+    assert SpgemmPlan(T, T).kernel_for() == "gather"            # 9 entries at n = 2^20
+    T22 = workloads.hm_random(1 << 22, [-1, 0, 1], 7, dev)
+    assert SpgemmPlan(T22, T22).kernel_for() == "astat"         # the same at n = 2^22
     nine = sorted({dy * 256 + dx for dx in (-1, 0, 1) for dy in (-1, 0, 1)})
     S9 = workloads.hm_random(1 << 16, nine, 8, dev)
     p9 = SpgemmPlan(S9, S9)
@@ -500,7 +502,7 @@ def test_astat_kernel_choice_and_capacity(dev):
     assert torch.equal(p9.multiply(S9.values, S9.values).view(torch.int32),
                        p9.multiply(S9.values, S9.values, kernel="gather").view(torch.int32))
     S5 = workloads.hm_random(1 << 16, [-256, -1, 0, 1, 256], 8, dev)
-    assert SpgemmPlan(S5, S5).kernel_for() == "gather"          # 25 entries
+    assert SpgemmPlan(S5, S5).kernel_for() == "astat"           # 25 entries
     P2 = workloads.recon_to_hm(workloads.spmv_config(2, seed=1, device=dev))
     assert SpgemmPlan(P2, P2).kernel_for() == "astat"           # the same, at n = 2^22
     wide = workloads.hm_random(4096, _random_offsets(rng, _lib.ASTAT_MAX_A + 1, -300, 300), 6, dev)
