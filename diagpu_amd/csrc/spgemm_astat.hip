@@ -75,10 +75,19 @@ static_assert(astat_cap<cf32>() == DIAGPU_ASTAT_MAX_A_C64, "complex A diagonals 
 // records[g] = {a, lo, hi, b} for plan entry g; flag[0] set if an entry is
 // not in the symbolic plan's form (its A or B start is no diagonal's start,
 // da + db is not its C diagonal's offset, or its shifts or lengths differ
-// from min0(da) - min0(dc), da + min0(db) - min0(dc), n - |da|, n - |db|),
-// flag[1] if its B indices do not fit int32.  The kernel builds each A row
-// from A_off and C_off but takes each term's range from the record, so an
-// entry of another form would give a different C without an error.
+// from min0(da) - min0(dc), da + min0(db) - min0(dc), n - |da|, n - |db|) or
+// pair_ptr is not a partition of the entries, flag[1] if its B indices do
+// not fit int32.  The kernel builds each A row from A_off and C_off but
+// takes each term's range from the record, so an entry of another form
+// would give a different C without an error.
+//
+// One thread per C diagonal k walks its entries [pair_ptr[k], pair_ptr[k +
+// 1]), so no entry searches pair_ptr; each entry's A and B diagonals are
+// found by their starts, in tables staged in LDS when both fit (kPrepTable
+// diagonals each), else in global memory.
+constexpr int kPrepBlock = 256;
+constexpr int kPrepTable = 1024;
+
 __device__ __forceinline__ int find_start(const int64_t* s, int32_t cnt, int64_t v)
 {
     // binary search (diagonals stored in offset order: starts ascend), then a
@@ -94,53 +103,69 @@ __device__ __forceinline__ int find_start(const int64_t* s, int32_t cnt, int64_t
     return -1;
 }
 
-__global__ __launch_bounds__(256) void k_astat_prepare(
+__global__ __launch_bounds__(kPrepBlock) void k_astat_prepare(
     int32_t n, const int32_t* __restrict__ A_off, const int64_t* __restrict__ A_starts, int32_t nA,
     const int32_t* __restrict__ B_off, const int64_t* __restrict__ B_starts, int32_t nB,
     const int32_t* __restrict__ C_off, const int64_t* __restrict__ pair_ptr, int64_t c_ndiag,
     const diagpu_gpair* __restrict__ pairs, int64_t n_pairs, int4* __restrict__ records,
     int32_t* __restrict__ flag)
 {
-    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (g >= n_pairs) return;
-    const diagpu_gpair p = pairs[g];
-    // the C diagonal k whose entries [pair_ptr[k], pair_ptr[k + 1]) hold g
-    int64_t klo = 0, khi = c_ndiag - 1;
-    while (klo < khi) {
-        const int64_t mid = (klo + khi + 1) >> 1;
-        if (pair_ptr[mid] <= g) klo = mid; else khi = mid - 1;
+    __shared__ int64_t sa[kPrepTable], sb[kPrepTable];
+    __shared__ int32_t oa[kPrepTable], ob[kPrepTable];
+    const bool staged = nA <= kPrepTable && nB <= kPrepTable;
+    if (staged) {
+        for (int i = (int)threadIdx.x; i < nA; i += kPrepBlock) {
+            sa[i] = A_starts[i];
+            oa[i] = A_off[i];
+        }
+        for (int i = (int)threadIdx.x; i < nB; i += kPrepBlock) {
+            sb[i] = B_starts[i];
+            ob[i] = B_off[i];
+        }
+        __syncthreads();
     }
-    const bool in_c = c_ndiag > 0 && pair_ptr[klo] <= g && g < pair_ptr[klo + 1];
-    const int a = find_start(A_starts, nA, (int64_t)p.ab);
-    const int bi = find_start(B_starts, nB, (int64_t)p.bb);
-    bool ok = in_c && a >= 0 && bi >= 0;
-    if (ok) {
-        const int64_t da = A_off[a], db = B_off[bi], dc = C_off[klo];
-        auto min0 = [](int64_t x) { return x < 0 ? x : (int64_t)0; };
-        auto absl = [](int64_t x) { return x < 0 ? -x : x; };
-        ok = da + db == dc && dc > -(int64_t)n && dc < n &&
-             (int64_t)p.ash == min0(da) - min0(dc) &&
-             (int64_t)p.bsh == da + min0(db) - min0(dc) && (int64_t)p.al == n - absl(da) &&
-             (int64_t)p.bl == n - absl(db);
-    }
-    const int plo = max(0, max(-p.ash, -p.bsh));
-    const int phi = min(p.al - p.ash, p.bl - p.bsh);
-    const int64_t b = (int64_t)p.bb + p.bsh;
-    int4 r = int4{0, 0, 0, 0};
-    if (!ok) {
+    const int64_t k = (int64_t)blockIdx.x * kPrepBlock + threadIdx.x;
+    if (k >= c_ndiag) return;
+    const int64_t g0 = pair_ptr[k], g1 = pair_ptr[k + 1];
+    if (g0 < 0 || g1 < g0 || g1 > n_pairs || (k == 0 && g0 != 0) ||
+        (k == c_ndiag - 1 && g1 != n_pairs)) {
         flag[0] = 1;   // every writer stores the same value
-    } else if (plo >= phi) {
-        // No position holds both operands (an entry of the symbolic form
-        // always has one; kept so that no record can read past B): a record
-        // that never fires, whose clamped B load min(max(p, 1), 0) = 0 reads
-        // B[0].
-        r = int4{a, 1, 1, 0};
-    } else if (b < INT_MIN || b + phi > INT_MAX) {
-        flag[1] = 1;
-    } else {
-        r = int4{a, plo, phi, (int)b};
+        return;
     }
-    records[g] = r;
+    const int64_t dc = C_off[k];
+    auto min0 = [](int64_t x) { return x < 0 ? x : (int64_t)0; };
+    auto absl = [](int64_t x) { return x < 0 ? -x : x; };
+    for (int64_t g = g0; g < g1; ++g) {
+        const diagpu_gpair p = pairs[g];
+        const int a = find_start(staged ? sa : A_starts, nA, (int64_t)p.ab);
+        const int bi = find_start(staged ? sb : B_starts, nB, (int64_t)p.bb);
+        bool ok = a >= 0 && bi >= 0;
+        if (ok) {
+            const int64_t da = staged ? oa[a] : A_off[a], db = staged ? ob[bi] : B_off[bi];
+            ok = da + db == dc && dc > -(int64_t)n && dc < n &&
+                 (int64_t)p.ash == min0(da) - min0(dc) &&
+                 (int64_t)p.bsh == da + min0(db) - min0(dc) && (int64_t)p.al == n - absl(da) &&
+                 (int64_t)p.bl == n - absl(db);
+        }
+        const int plo = max(0, max(-p.ash, -p.bsh));
+        const int phi = min(p.al - p.ash, p.bl - p.bsh);
+        const int64_t b = (int64_t)p.bb + p.bsh;
+        int4 r = int4{0, 0, 0, 0};
+        if (!ok) {
+            flag[0] = 1;
+        } else if (plo >= phi) {
+            // No position holds both operands (an entry of the symbolic form
+            // always has one; kept so that no record can read past B): a
+            // record that never fires, whose clamped B load
+            // min(max(p, 1), 0) = 0 reads B[0].
+            r = int4{a, 1, 1, 0};
+        } else if (b < INT_MIN || b + phi > INT_MAX) {
+            flag[1] = 1;
+        } else {
+            r = int4{a, plo, phi, (int)b};
+        }
+        records[g] = r;
+    }
 }
 
 __global__ __launch_bounds__(64) void k_astat_clear(int32_t* __restrict__ flag)
@@ -534,10 +559,11 @@ DIAGPU_API int diagpu_spgemm_astat_prepare(int32_t n, const int32_t* A_off,
     hipLaunchKernelGGL(k_astat_clear, dim3(1), dim3(64), 0, s, flag);
     int st = check_launch(fn);
     if (!st && n_pairs > 0) {
-        hipLaunchKernelGGL(k_astat_prepare, dim3((unsigned)ceil_div<int64_t>(n_pairs, 256)),
-                           dim3(256), 0, s, n, A_off, A_starts, nA, B_off, B_starts, nB, C_off,
-                           pair_ptr, c_ndiag, pairs, n_pairs, reinterpret_cast<int4*>(records),
-                           flag);
+        hipLaunchKernelGGL(k_astat_prepare,
+                           dim3((unsigned)ceil_div<int64_t>(c_ndiag, kPrepBlock)),
+                           dim3(kPrepBlock), 0, s, n, A_off, A_starts, nA, B_off, B_starts, nB,
+                           C_off, pair_ptr, c_ndiag, pairs, n_pairs,
+                           reinterpret_cast<int4*>(records), flag);
         st = check_launch(fn);
     }
     if (!st) st = check_hip(hipMemcpyWithStream(host, flag, sizeof(host), hipMemcpyDeviceToHost, s), fn);

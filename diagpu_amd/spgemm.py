@@ -72,6 +72,8 @@ class SpgemmPlan:
         self.info = _lib.SpgemmInfo()
         self._band = None
         self._astat = None
+        self._sym_fn = getattr(_lib.load(), "diagpu_spgemm_symbolic")
+        self._sym_args, self._sym_caps = None, None
         self.symbolic()
 
     def _view(self, name: str):
@@ -95,18 +97,29 @@ class SpgemmPlan:
     workspace = property(lambda self: self._view("workspace"))
 
     def symbolic(self) -> None:
-        A, B = self.A, self.B
+        """(Re)builds the C structure and pair plan from the operands'
+        offsets, lengths and starts (diagpu_spgemm_symbolic; one stream
+        sync)."""
         self._band = None
         self._astat = None
-        _lib.call("diagpu_spgemm_symbolic", self.n,
-                  A.offsets.data_ptr(), A.lengths.data_ptr(), A.starts.data_ptr(),
-                  A.offsets.numel(),
-                  B.offsets.data_ptr(), B.lengths.data_ptr(), B.starts.data_ptr(),
-                  B.offsets.numel(),
-                  self._addr("C_off"), self._addr("C_len"), self._addr("C_starts"),
-                  self.c_cap, self._addr("ptr"), self._addr("pairs"), self.p_cap,
-                  self._addr("lookup"), self._addr("workspace"), self._parts["workspace"][2],
-                  C.byref(self.info), _stream_handle(self.stream))
+        if self._sym_caps != (self.c_cap, self.p_cap):
+            # the call's arguments but the stream, fixed while the capacities
+            # are (operand tensors and buffer do not move): one ctypes call
+            # per symbolic() with nothing rebuilt
+            A, B = self.A, self.B
+            self._sym_args = (self.n,
+                              A.offsets.data_ptr(), A.lengths.data_ptr(), A.starts.data_ptr(),
+                              A.offsets.numel(),
+                              B.offsets.data_ptr(), B.lengths.data_ptr(), B.starts.data_ptr(),
+                              B.offsets.numel(),
+                              self._addr("C_off"), self._addr("C_len"), self._addr("C_starts"),
+                              self.c_cap, self._addr("ptr"), self._addr("pairs"), self.p_cap,
+                              self._addr("lookup"), self._addr("workspace"),
+                              self._parts["workspace"][2], C.byref(self.info))
+            self._sym_caps = (self.c_cap, self.p_cap)
+        st = self._sym_fn(*self._sym_args, _stream_handle(self.stream))
+        if st:
+            _lib.check(st)
 
     # structure views (device tensors) --------------------------------------
     def c_offsets(self) -> torch.Tensor:

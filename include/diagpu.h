@@ -366,7 +366,8 @@ DIAGPU_API int diagpu_spgemm_numeric_band_mfma_f32(
  * stream synchronisation (to report errors): DIAGPU_ERR_ARG if an entry is
  * not in the symbolic plan's form (its A or B start is no diagonal's start,
  * da + db is not its C diagonal's offset, or ash, bsh, al, bl differ from
- * min0(da) - min0(dc), da + min0(db) - min0(dc), n - |da|, n - |db|),
+ * min0(da) - min0(dc), da + min0(db) - min0(dc), n - |da|, n - |db|) or if
+ * pair_ptr is not a partition of the n_pairs entries,
  * DIAGPU_ERR_CAPACITY if a B index exceeds 2^31 - 1.  No reference
  * counterpart: the A-stationary form of the numeric phase below. */
 DIAGPU_API int diagpu_spgemm_astat_prepare(int32_t n, const int32_t* A_off,
