@@ -398,9 +398,10 @@ def compare_kernels(plan, sets, reps: int, alg: int, flops: int, complex_values:
     """The automatic choice and every numeric kernel that takes this plan
     (fp32 or complex64 values), forced, on the same rotated operand sets
     (the side-by-side run of spmspm/bench_spmspm.cu:518-653), timed in
-    interleaved rounds (auto, k1, k2, ..., auto, k1, ...; each round's
-    window of reps / rounds products opened behind a spin so that every leg
-    sees the same queue and clock state) and reported as the median over
+    interleaved rounds (auto, k1, k2, ...; the order rotated by one leg each
+    round, so every leg leads as many rounds; each round opened behind a
+    spin so the first leg's launch latency stays out of its window; reps /
+    rounds products per leg per round) and reported as the median over
     rounds of the time per product, with GFLOP/s, the fraction of HBM peak,
     and whether C is bit for bit the gather's (where C fits CHECK_BYTES).
     Returns (auto record, {kernel: record})."""
@@ -420,13 +421,14 @@ def compare_kernels(plan, sets, reps: int, alg: int, flops: int, complex_values:
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * len(legs))]
     for r in range(rounds):
         gpu_spin(stream, 100.0)
-        for j, k in enumerate(legs):
+        order = legs[r % len(legs):] + legs[: r % len(legs)]   # each leg leads some rounds
+        for j, k in enumerate(order):
             ev[2 * j].record(stream)
             for i in range(per):
                 plan.numeric(*sets[(r * per + i) % nsets], kernel=k)
             ev[2 * j + 1].record(stream)
         torch.cuda.synchronize()
-        for j, k in enumerate(legs):
+        for j, k in enumerate(order):
             times[k].append(ev[2 * j].elapsed_time(ev[2 * j + 1]) / per)
     esz = 8 if complex_values else 4
     check = plan.info.c_nnz * esz <= CHECK_BYTES
