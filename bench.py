@@ -50,7 +50,7 @@ def parse_args(argv=None):
                          "configs' matrices), spgemm4, spgemm5, spgemm4c, spgemm5c, taylor, krylov, "
                          "propagator, propagator2d, gemmdiag, gemmdiag20, spmvhash (the "
                          "reference SpMV bench's hash band), spgemmbanded (the reference "
-                         "SpGEMM bench's make_banded operands), copy, fill20) "
+                         "SpGEMM bench's make_banded operands), launch (the launch floor), copy, fill20) "
                          "and print its line")
     return ap.parse_args(argv)
 
@@ -743,6 +743,27 @@ def time_gemm_diag(n: int = 4096, hb: int = 10, reps: int = 100, cpu_seconds: fl
     return rec
 
 
+def launch_floor(reps: int = 400) -> dict:
+    """Time per launch of back-to-back near-empty kernels (torch's spin
+    kernel with 0 cycles) on one stream, by HIP events: the floor under any
+    single-launch product, for reading the launch-bound lines (config 1's
+    SpMV and square, gemm_diag at n = 4096)."""
+    import torch
+    stream = torch.cuda.current_stream()
+    for _ in range(20):
+        torch.cuda._sleep(0)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    gpu_spin(stream)
+    e0.record(stream)
+    for _ in range(reps):
+        torch.cuda._sleep(0)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return {"workload": "launch_floor", "kernel": "torch spin kernel, 0 cycles", "launches": reps,
+            "us_per_launch": round(e0.elapsed_time(e1) * 1e3 / reps, 3)}
+
+
 def copy_calibration(steps: int):
     """A plain device copy of known size, for scaling rocprof FETCH/WRITE counters."""
     import torch
@@ -804,6 +825,8 @@ def main(argv=None) -> int:
             print(json.dumps(copy_calibration(args.steps)), flush=True)
         elif w == "fill20":
             print(json.dumps(fill_calibration(args.steps)), flush=True)
+        elif w == "launch":
+            print(json.dumps(launch_floor()), flush=True)
         elif w == "spmvhash":
             R = workloads.hash_band(device="cuda")
             res = time_spmv(0, torch.float32, args.steps, args.warmup, args.seed, args.sets, R=R)
@@ -937,6 +960,10 @@ def main(argv=None) -> int:
                 log(f"extra {rec['workload']}: {rec['numeric_ms']} ms, {rec['GFLOPs']} GFLOP/s")
             except Exception as e:
                 extras[f"gemm_diag_n{n_gd}"] = {"error": repr(e)}
+        try:
+            extras["launch_floor"] = launch_floor()
+        except Exception as e:
+            extras["launch_floor"] = {"error": repr(e)}
         for grid in ("3d", "2d"):
             try:
                 rec = time_propagator(grid)
