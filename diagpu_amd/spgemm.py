@@ -73,7 +73,7 @@ class SpgemmPlan:
         self._band = None
         self._astat = None
         self._sym_fn = getattr(_lib.load(), "diagpu_spgemm_symbolic")
-        self._sym_args, self._sym_caps = None, None
+        self._sym_args, self._sym_caps, self._sym_ops = None, None, ()
         self.symbolic()
 
     def _view(self, name: str):
@@ -102,11 +102,15 @@ class SpgemmPlan:
         sync)."""
         self._band = None
         self._astat = None
-        if self._sym_caps != (self.c_cap, self.p_cap):
-            # the call's arguments but the stream, fixed while the capacities
-            # are (operand tensors and buffer do not move): one ctypes call
-            # per symbolic() with nothing rebuilt
-            A, B = self.A, self.B
+        A, B = self.A, self.B
+        ops = (A.offsets, A.lengths, A.starts, B.offsets, B.lengths, B.starts)
+        if (self._sym_caps != (self.c_cap, self.p_cap)
+                or any(t is not u for t, u in zip(ops, self._sym_ops))):
+            # the call's arguments but the stream, kept while the capacities
+            # and the operands' structure tensors stay the same objects (held
+            # here, so the pointers in the arguments stay valid): one ctypes
+            # call per symbolic() with nothing rebuilt
+            self._sym_ops = ops
             self._sym_args = (self.n,
                               A.offsets.data_ptr(), A.lengths.data_ptr(), A.starts.data_ptr(),
                               A.offsets.numel(),

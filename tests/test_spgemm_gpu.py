@@ -306,6 +306,29 @@ def test_capacity_and_empty(dev):
     assert p3.info.c_ndiag == 0
 
 
+def test_symbolic_after_operand_rebinding(dev):
+    """symbolic() keeps its call's arguments between calls; a plan whose
+    operand is rebound (new structure tensors, same diagonal count) builds
+    the new operand's plan, equal to a fresh plan's, and the old tensors'
+    memory is not read after they are dropped."""
+    n = 4000
+    A = workloads.hm_random(n, [-30, -2, 0, 9, 400], 71, dev)
+    B = workloads.hm_random(n, [-5, 0, 3, 77], 72, dev)
+    plan = SpgemmPlan(A, B)
+    first = plan.c_offsets().cpu().tolist()
+    A2 = workloads.hm_random(n, [-1000, -7, 0, 12, 2500], 73, dev)
+    plan.A = A2
+    del A
+    torch.cuda.empty_cache()
+    junk = torch.full((1 << 20,), -9, dtype=torch.int64, device=dev)   # reuses freed blocks
+    plan.symbolic()
+    ref = SpgemmPlan(A2, B)
+    assert plan.c_offsets().cpu().tolist() == ref.c_offsets().cpu().tolist() != first
+    assert torch.equal(plan.pair_ptr(), ref.pair_ptr())
+    assert np.array_equal(plan.pairs_numpy(), ref.pairs_numpy())
+    del junk
+
+
 @pytest.mark.parametrize("cfg", [1, 2, 3])
 def test_square_of_spmv_configs(dev, oracle, cfg):
     """H H for the SpMV configs' matrices (full size): plan exact; values to
