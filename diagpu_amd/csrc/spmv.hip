@@ -75,7 +75,7 @@ namespace diagpu {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kShortMax = 5;   // K <= kShortMax: straight-line kernel
+constexpr int kShortMax = 9;   // K <= kShortMax: straight-line kernel
 
 // Per (matrix element, vector element) pair: rows per lane and ring depths,
 // chosen so the kernels stay within 64 VGPRs (8 waves per SIMD).
@@ -394,10 +394,14 @@ SpmvKernel<TV, TX> pick_kernel(int K, int64_t lim)
     case 3: return spmv_short_kernel<TV, TX, 3, DOT>;
     case 4: return spmv_short_kernel<TV, TX, 4, DOT>;
     case 5: return spmv_short_kernel<TV, TX, 5, DOT>;
+    case 6: return spmv_short_kernel<TV, TX, 6, DOT>;
+    case 7: return spmv_short_kernel<TV, TX, 7, DOT>;
+    case 8: return spmv_short_kernel<TV, TX, 8, DOT>;
+    case 9: return spmv_short_kernel<TV, TX, 9, DOT>;
     default: return spmv_ring_kernel<TV, TX, DOT>;
     }
 }
-static_assert(kShortMax == 5, "pick_kernel covers K = 0..5");
+static_assert(kShortMax == 9, "pick_kernel covers K = 0..9");
 
 }  // namespace
 
