@@ -75,7 +75,7 @@ namespace diagpu {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kShortMax = 9;   // K <= kShortMax: straight-line kernel
+constexpr int kShortMax = 16;   // K <= kShortMax: straight-line kernel
 
 // Per (matrix element, vector element) pair: rows per lane and ring depths,
 // chosen so the kernels stay within 64 VGPRs (8 waves per SIMD).
@@ -398,10 +398,17 @@ SpmvKernel<TV, TX> pick_kernel(int K, int64_t lim)
     case 7: return spmv_short_kernel<TV, TX, 7, DOT>;
     case 8: return spmv_short_kernel<TV, TX, 8, DOT>;
     case 9: return spmv_short_kernel<TV, TX, 9, DOT>;
+    case 10: return spmv_short_kernel<TV, TX, 10, DOT>;
+    case 11: return spmv_short_kernel<TV, TX, 11, DOT>;
+    case 12: return spmv_short_kernel<TV, TX, 12, DOT>;
+    case 13: return spmv_short_kernel<TV, TX, 13, DOT>;
+    case 14: return spmv_short_kernel<TV, TX, 14, DOT>;
+    case 15: return spmv_short_kernel<TV, TX, 15, DOT>;
+    case 16: return spmv_short_kernel<TV, TX, 16, DOT>;
     default: return spmv_ring_kernel<TV, TX, DOT>;
     }
 }
-static_assert(kShortMax == 9, "pick_kernel covers K = 0..9");
+static_assert(kShortMax == 16, "pick_kernel covers K = 0..16");
 
 }  // namespace
 
