@@ -227,7 +227,7 @@ class SpgemmPlan:
     def uses_astat(self, dtype=torch.float32) -> bool:
         """The automatic choice after the band kernel: the A-stationary kernel
         where A's diagonals fit its LDS (at most DIAGPU_ASTAT_MAX_A, or
-        DIAGPU_ASTAT_MAX_A_C64 for complex values), n >= 4096, B values are
+        DIAGPU_ASTAT_MAX_A_C64 for complex values), 4096 <= n < 2^30, B values are
         addressable with int32, and
 
           fp32:      any plan, except one of fewer than 16 entries at
@@ -252,7 +252,7 @@ class SpgemmPlan:
         diagonal."""
         na = self.A.offsets.numel()
         inf = self.info
-        if inf.c_ndiag == 0 or self.n < 4096:
+        if inf.c_ndiag == 0 or self.n < 4096 or self.n >= 1 << 30:
             return False
         if dtype == torch.float32:
             ok = na <= _lib.ASTAT_MAX_A and not (inf.n_pairs < 16 and 1 << 19 <= self.n < 1 << 22)

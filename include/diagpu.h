@@ -384,7 +384,8 @@ DIAGPU_API int diagpu_spgemm_astat_prepare(int32_t n, const int32_t* A_off,
  * and reading only B from memory: for products whose
  * A diagonals each feed many plan entries but whose B window is too wide for
  * the band kernel (e.g. the square of a 64-diagonal band over +-512).
- * records from diagpu_spgemm_astat_prepare for this plan; nA at most
+ * records from diagpu_spgemm_astat_prepare for this plan; n < 2^30 (else
+ * DIAGPU_ERR_ARG; the other numeric kernels take n = 2^30); nA at most
  * DIAGPU_ASTAT_MAX_A (else DIAGPU_ERR_CAPACITY). */
 DIAGPU_API int diagpu_spgemm_numeric_astat_f32(
     int32_t n, const int32_t* A_off, const int64_t* A_starts, int32_t nA, const float* A_vals,
@@ -395,8 +396,8 @@ DIAGPU_API int diagpu_spgemm_numeric_astat_f32(
 /* The same with complex64 values: the numeric phase of
  * diagpu_spgemm_numeric_c64 (same C, bit for bit), same records; each
  * workgroup holds a block of 256 rows (512 for a few short C diagonals, 128
- * above 75 A diagonals) plus the 16 before it; nA at most
- * DIAGPU_ASTAT_MAX_A_C64 (else
+ * above 75 A diagonals) plus the 16 before it; n < 2^30 (else
+ * DIAGPU_ERR_ARG); nA at most DIAGPU_ASTAT_MAX_A_C64 (else
  * DIAGPU_ERR_CAPACITY).  No reference counterpart (the reference is real
  * only). */
 DIAGPU_API int diagpu_spgemm_numeric_astat_c64(

@@ -303,7 +303,7 @@ public:
         // fp32 only); the rules are SpgemmPlan.uses_astat's in
         // diagpu_amd/spgemm.py, with the measurements behind them.
         const int64_t np = info_.n_pairs, nc = info_.c_ndiag, na = a_ndiag;
-        const bool sized = nc > 0 && int64_t(n) >= 4096;
+        const bool sized = nc > 0 && int64_t(n) >= 4096 && int64_t(n) < (int64_t(1) << 30);
         const bool thin_mid = np < 16 && int64_t(n) >= (1 << 19) && int64_t(n) < (1 << 22);
         astat_auto_ = !uses_band() && sized && na <= DIAGPU_ASTAT_MAX_A && !thin_mid;
         astat_auto_c64_ = sized && na <= DIAGPU_ASTAT_MAX_A_C64 &&
@@ -326,13 +326,13 @@ public:
     bool uses_band() const { return band_auto_ && band_.eligible; }
     // True where NumericKernel::Auto runs the A-stationary kernel for fp32
     // values: the band kernel does not take the plan, A has at most
-    // DIAGPU_ASTAT_MAX_A diagonals, n >= 4096, and the plan is not one of
+    // DIAGPU_ASTAT_MAX_A diagonals, 4096 <= n < 2^30, and the plan is not one of
     // fewer than 16 entries at 2^19 <= n < 2^22 (there the gather has more
     // work per launch to hide its operand reads: the tridiagonal square at
     // n = 2^20 takes 11.4 us on the gather, 12.7 on this kernel).
     bool uses_astat() const { return astat_auto_; }
     // The same for complex64 values: A has at most DIAGPU_ASTAT_MAX_A_C64
-    // diagonals, n >= 4096, and n >= 2^16 or >= 3 entries per A diagonal.
+    // diagonals, 4096 <= n < 2^30, and n >= 2^16 or >= 3 entries per A diagonal.
     bool uses_astat_c64() const { return astat_auto_c64_; }
 
     // C_vals (device, info().c_nnz values) = A * B; asynchronous on `stream`
