@@ -168,9 +168,25 @@ __global__ __launch_bounds__(kPrepBlock) void k_astat_prepare(
     }
 }
 
-__global__ __launch_bounds__(64) void k_astat_clear(int32_t* __restrict__ flag)
+// flag[0..1] = 0 (the error flags above); flag[2..3] = the smallest and
+// largest of A's offsets, which the numeric kernel reads.
+__global__ __launch_bounds__(64) void k_astat_init(int32_t* __restrict__ flag,
+                                                   const int32_t* __restrict__ A_off, int32_t nA)
 {
-    if (threadIdx.x < 4) flag[threadIdx.x] = 0;
+    int lo = INT_MAX, hi = INT_MIN;
+    for (int d = (int)threadIdx.x; d < nA; d += 64) {
+        lo = min(lo, A_off[d]);
+        hi = max(hi, A_off[d]);
+    }
+    for (int m = 32; m >= 1; m >>= 1) {
+        lo = min(lo, __shfl_xor(lo, m));
+        hi = max(hi, __shfl_xor(hi, m));
+    }
+    if (threadIdx.x < 2) flag[threadIdx.x] = 0;
+    if (threadIdx.x == 0) {
+        flag[2] = lo;
+        flag[3] = hi;
+    }
 }
 
 // Keeps a value in registers at this point: the compiler cannot sink its
@@ -239,8 +255,12 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
     const T* __restrict__ Av, const T* __restrict__ Bv, const int32_t* __restrict__ C_off,
     const int32_t* __restrict__ C_len, const int64_t* __restrict__ C_starts, int32_t nC,
     const int64_t* __restrict__ pair_ptr, const int4* __restrict__ records,
-    T* __restrict__ Cv, int32_t blocks, int32_t groups, int32_t per_xcd, int32_t tail5)
+    const int32_t* __restrict__ aext, T* __restrict__ Cv, int32_t blocks, int32_t groups,
+    int32_t per_xcd, int32_t tail5)
 {
+    // A's smallest and largest offset (written by diagpu_spgemm_astat_prepare
+    // after the records)
+    const int amin = aext[0], amax = aext[1];
     constexpr int kRB = Astat<T, R>::kRB, kLead = Astat<T, R>::kLead;
     constexpr int kStage = Astat<T, R>::kStage, kWords = Astat<T, R>::kWords;
     extern __shared__ float A_l[];   // [nA][kStage] elements: rows i0 - kLead .. i0 + kRB - 1
@@ -324,6 +344,9 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
             T acc[RR];
 #pragma unroll
             for (int j = 0; j < RR; ++j) acc[j] = zero_of<T>();
+            // the staged A row of the lane's row j (row R of a lane past the
+            // window, p >= len there, reads row 0)
+            auto arow = [&](int j) { return j < R || lane < s ? ab + 64 * j : ab; };
             // one term: B at the position clamped into the entry's range
             // [e.y, e.z) (an always valid load: 0 <= c < n), A from LDS (row R
             // of a lane past the window, p >= len there, reads row 0), the
@@ -335,46 +358,79 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
                 const int c = min(max(p, e.y), e.z - 1);
                 ok = c == p && e.y < e.z;
                 b = load_b(Bv + (int64_t)e.w, c);
-                a = A_t[e.x * kStage + (j < R || lane < s ? ab + 64 * j : ab)];
+                a = A_t[e.x * kStage + arow(j)];
             };
-            // The values of a batch are pinned once all its loads are issued,
-            // so the compiler cannot turn a masked multiply-add into a branch
-            // around its own load (each such branch ends in a full vmcnt(0)
-            // drain: gfx9 counts loads in order).
-            // two entries' loads in flight, or one where two would hold more
-            // than 8 dwords per lane per entry (within 64 VGPRs: two 16-wave
-            // workgroups per CU)
-            constexpr int U = (RR * kWords <= 8) ? 2 : 1;
-            int g = g0;
-            for (; U == 2 && g + 2 <= g1; g += 2) {
-                T bv[2][RR], av[2][RR];
-                bool ok[2][RR];
+            // Every entry of this diagonal takes every term of the wave's
+            // rows [r0, r0 + 64 RR), r0 = i0 - s, where each row i has
+            // 0 <= i, i + da, i + dc < n for all of A's offsets da (the
+            // rows where an entry's A and B elements and C's exist): then
+            // the B loads need no clamp and the multiply-adds no select,
+            // about a fifth of the vector instructions of the general form,
+            // with the same multiply-adds in the same order.  Taken for fp32
+            // at up to 4 rows per lane (measured against the general form
+            // alone: make_banded(100000, 16) squared 34.7 -> 28.2 us, config
+            // 3's square 7.62 -> 7.43 ms, config 5 2.28 -> 2.23 ms; at 8 rows
+            // per lane the Taylor chain's products lost 2-3 %, complex values
+            // 1 %).
+            constexpr bool kEveryPath = sizeof(T) == 4 && R <= 4;
+            const int r0 = i0 - s, r1 = i0 - s + 64 * RR;
+            const bool inner = kEveryPath && r0 >= 0 && r0 + amin >= 0 && r0 + dc >= 0 &&
+                               r1 <= n && r1 + amax <= n && r1 + dc <= n;
+            // A batch of NU entries: their loads issued together, then the
+            // multiply-adds in plan order.  The values are pinned once all
+            // loads are issued, so the compiler cannot turn a masked
+            // multiply-add into a branch around its own load (each such
+            // branch ends in a full vmcnt(0) drain: gfx9 counts loads in
+            // order).
+            auto batch = [&](auto nu, auto every, int g) {
+                constexpr int NU = decltype(nu)::value;
+                constexpr bool kEvery = decltype(every)::value;
+                T bv[NU][RR], av[NU][RR];
+                bool ok[NU][RR];
 #pragma unroll
-                for (int u = 0; u < 2; ++u) {
+                for (int u = 0; u < NU; ++u) {
                     const int4 e = records[g + u];
 #pragma unroll
-                    for (int j = 0; j < RR; ++j) term(e, j, bv[u][j], av[u][j], ok[u][j]);
+                    for (int j = 0; j < RR; ++j) {
+                        if constexpr (kEvery) {
+                            bv[u][j] = load_b(Bv + (int64_t)e.w, pb + 64 * j);
+                            av[u][j] = A_t[e.x * kStage + arow(j)];
+                        } else {
+                            term(e, j, bv[u][j], av[u][j], ok[u][j]);
+                        }
+                    }
                 }
 #pragma unroll
-                for (int u = 0; u < 2; ++u)
+                for (int u = 0; u < NU; ++u)
 #pragma unroll
                     for (int j = 0; j < RR; ++j) { pin(bv[u][j]); pin(av[u][j]); }
 #pragma unroll
-                for (int u = 0; u < 2; ++u)
+                for (int u = 0; u < NU; ++u)
 #pragma unroll
-                    for (int j = 0; j < RR; ++j)
-                        acc[j] = sel(ok[u][j], mad(acc[j], av[u][j], bv[u][j]), acc[j]);
-            }
-            for (; g < g1; ++g) {
-                const int4 e = records[g];
-                T bv[RR], av[RR];
-                bool ok[RR];
-#pragma unroll
-                for (int j = 0; j < RR; ++j) term(e, j, bv[j], av[j], ok[j]);
-#pragma unroll
-                for (int j = 0; j < RR; ++j) { pin(bv[j]); pin(av[j]); }
-#pragma unroll
-                for (int j = 0; j < RR; ++j) acc[j] = sel(ok[j], mad(acc[j], av[j], bv[j]), acc[j]);
+                    for (int j = 0; j < RR; ++j) {
+                        if constexpr (kEvery)
+                            acc[j] = mad(acc[j], av[u][j], bv[u][j]);
+                        else
+                            acc[j] = sel(ok[u][j], mad(acc[j], av[u][j], bv[u][j]), acc[j]);
+                    }
+            };
+            // two entries' loads in flight, or one where two would hold more
+            // than 8 dwords per lane per entry (within 64 VGPRs: two 16-wave
+            // workgroups per CU)
+            auto walk = [&](auto every) {
+                int g = g0;
+                if constexpr (RR * kWords <= 8)
+                    for (; g + 2 <= g1; g += 2) batch(std::integral_constant<int, 2>{}, every, g);
+                for (; g < g1; ++g) batch(std::integral_constant<int, 1>{}, every, g);
+            };
+            if constexpr (kEveryPath) {
+                if (inner) {
+                    walk(std::true_type{});
+                } else {
+                    walk(std::false_type{});
+                }
+            } else {
+                walk(std::false_type{});
             }
             store_c(Cv + cst, pb, len, acc);
         }
@@ -416,7 +472,8 @@ template <typename T, int R>
 int launch_rows(const char* fn, int32_t n, const int32_t* A_off, const int64_t* A_starts,
                 int32_t nA, const T* A_vals, const T* B_vals, const int32_t* C_off,
                 const int32_t* C_len, const int64_t* C_starts, int64_t c_ndiag,
-                const int64_t* pair_ptr, const int32_t* records, T* C_vals, void* stream)
+                const int64_t* pair_ptr, const int32_t* records, int64_t n_pairs, T* C_vals,
+                void* stream)
 {
     constexpr int kRB = Astat<T, R>::kRB, kLead = Astat<T, R>::kLead, kStage = Astat<T, R>::kStage;
     constexpr int kMax = Astat<T, R>::kMax;
@@ -476,14 +533,17 @@ int launch_rows(const char* fn, int32_t n, const int32_t* A_off, const int64_t* 
     if (st) return st;
     const dim3 grid((unsigned)(per_xcd * kNumXcd)), block(64 * kWaves);
     const int4* rec = reinterpret_cast<const int4*>(records);
+    const int32_t* aext = records + 4 * n_pairs + 2;
     if (prefetch)
         hipLaunchKernelGGL((k_astat<T, true, R>), grid, block, lds, as_stream(stream), n, A_off,
                            A_starts, nA, A_vals, B_vals, C_off, C_len, C_starts, (int32_t)c_ndiag,
-                           pair_ptr, rec, C_vals, (int32_t)blocks, (int32_t)groups, per_xcd, tail5);
+                           pair_ptr, rec, aext, C_vals, (int32_t)blocks, (int32_t)groups, per_xcd,
+                           tail5);
     else
         hipLaunchKernelGGL((k_astat<T, false, R>), grid, block, lds, as_stream(stream), n, A_off,
                            A_starts, nA, A_vals, B_vals, C_off, C_len, C_starts, (int32_t)c_ndiag,
-                           pair_ptr, rec, C_vals, (int32_t)blocks, (int32_t)groups, per_xcd, tail5);
+                           pair_ptr, rec, aext, C_vals, (int32_t)blocks, (int32_t)groups, per_xcd,
+                           tail5);
     return check_launch(fn);
 }
 
@@ -508,7 +568,7 @@ int launch_astat(const char* fn, int32_t n, const int32_t* A_off, const int64_t*
         return fail(DIAGPU_ERR_ARG, "%s: a pointer is NULL", fn);
 #define DIAGPU_ASTAT_LAUNCH(RV)                                                                   \
     launch_rows<T, RV>(fn, n, A_off, A_starts, nA, A_vals, B_vals, C_off, C_len, C_starts, c_ndiag, \
-                       pair_ptr, records, C_vals, stream)
+                       pair_ptr, records, n_pairs, C_vals, stream)
     // Rows per lane.  A wave's time per C diagonal is a chain of dependent
     // loads; longer blocks put more rows into each chain and need fewer
     // rounds of workgroups, where n gives at least 4 rounds of them.
@@ -579,9 +639,9 @@ DIAGPU_API int diagpu_spgemm_astat_prepare(int32_t n, const int32_t* A_off,
     if (n_pairs > 0 && c_ndiag == 0)
         return fail(DIAGPU_ERR_ARG, "%s: plan entries without C diagonals", fn);
     hipStream_t s = as_stream(stream);
-    int32_t* flag = records + 4 * n_pairs;   // the caller's 4 scratch ints
+    int32_t* flag = records + 4 * n_pairs;   // the 4 ints after the records
     int32_t host[2] = {0, 0};
-    hipLaunchKernelGGL(k_astat_clear, dim3(1), dim3(64), 0, s, flag);
+    hipLaunchKernelGGL(k_astat_init, dim3(1), dim3(64), 0, s, flag, A_off, nA);
     int st = check_launch(fn);
     if (!st && n_pairs > 0) {
         hipLaunchKernelGGL(k_astat_prepare,

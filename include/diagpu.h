@@ -361,7 +361,8 @@ DIAGPU_API int diagpu_spgemm_numeric_band_mfma_f32(
  * from the entry's A start), [lo, hi) = [max(0, -ash, -bsh), min(al - ash,
  * bl - bsh)) the C positions where both operands hold an element, and
  * b = bb + bsh the B index of C position 0.  records holds 4 n_pairs + 4
- * int32 (the last 4 are scratch).  A_off/A_starts, B_off/B_starts, C_off
+ * int32: the last 4 are two error flags and the smallest and largest of A's
+ * offsets, which the numeric entry points read.  A_off/A_starts, B_off/B_starts, C_off
  * and pair_ptr (c_ndiag + 1 entries) are the plan's device arrays.  One
  * stream synchronisation (to report errors): DIAGPU_ERR_ARG if an entry is
  * not in the symbolic plan's form (its A or B start is no diagonal's start,
