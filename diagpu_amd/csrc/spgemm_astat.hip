@@ -249,7 +249,7 @@ __device__ __forceinline__ void store_c(T* cd, int pb, int len, const T (&acc)[R
 // (for waves that walk many diagonals).  tail5: the last block also takes
 // the rows the line-aligned shift leaves after it, R + 1 rows per lane (else
 // one more block of at most kLead - 1 rows per diagonal covers them).
-template <typename T, bool Prefetch, int R>
+template <typename T, bool Prefetch, int R, bool Quad = false>
 __global__ __launch_bounds__(64 * kWaves) void k_astat(
     int32_t n, const int32_t* __restrict__ A_off, const int64_t* __restrict__ A_starts, int32_t nA,
     const T* __restrict__ Av, const T* __restrict__ Bv, const int32_t* __restrict__ C_off,
@@ -416,9 +416,11 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
             };
             // two entries' loads in flight, or one where two would hold more
             // than 8 dwords per lane per entry (within 64 VGPRs: two 16-wave
-            // workgroups per CU)
+            // workgroups per CU); with Quad, four in the every-term form
             auto walk = [&](auto every) {
                 int g = g0;
+                if constexpr (Quad && decltype(every)::value && RR * kWords <= 4)
+                    for (; g + 4 <= g1; g += 4) batch(std::integral_constant<int, 4>{}, every, g);
                 if constexpr (RR * kWords <= 8)
                     for (; g + 2 <= g1; g += 2) batch(std::integral_constant<int, 2>{}, every, g);
                 for (; g < g1; ++g) batch(std::integral_constant<int, 1>{}, every, g);
@@ -526,25 +528,35 @@ int launch_rows(const char* fn, int32_t n, const int32_t* A_off, const int64_t* 
     // ~575 each) and costs where they walk one or two (the 7-point stencil's
     // square: 25 C diagonals over 16 waves, 31 -> 34 us)
     const bool prefetch = c_ndiag >= kPrefetchDiagsPerWave * groups * kWaves;
-    const void* kern = prefetch ? (const void*)k_astat<T, true, R> : (const void*)k_astat<T, false, R>;
-    // more than 64 KiB of dynamic LDS must be allowed explicitly
-    const int st = check_hip(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 kStage * kMax * (int)sizeof(T)), fn);
-    if (st) return st;
+    // Quad (fp32, 4 rows per lane): batches of four entries in the
+    // every-term form, for plans of >= 3 entries per C diagonal on average
+    // (make_banded(100000, 16) squared 27.9 -> 26.3 us, config 3's square
+    // 7.45 -> 7.33 ms; config 5, 1.8 entries per C diagonal, lost 1 %)
+    const bool quad = n_pairs >= 3 * c_ndiag;
     const dim3 grid((unsigned)(per_xcd * kNumXcd)), block(64 * kWaves);
     const int4* rec = reinterpret_cast<const int4*>(records);
     const int32_t* aext = records + 4 * n_pairs + 2;
-    if (prefetch)
-        hipLaunchKernelGGL((k_astat<T, true, R>), grid, block, lds, as_stream(stream), n, A_off,
+    auto go = [&](auto pf, auto qd) {
+        constexpr bool kPf = decltype(pf)::value, kQd = decltype(qd)::value;
+        // more than 64 KiB of dynamic LDS must be allowed explicitly
+        const int st = check_hip(
+            hipFuncSetAttribute((const void*)k_astat<T, kPf, R, kQd>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                kStage * kMax * (int)sizeof(T)),
+            fn);
+        if (st) return st;
+        hipLaunchKernelGGL((k_astat<T, kPf, R, kQd>), grid, block, lds, as_stream(stream), n, A_off,
                            A_starts, nA, A_vals, B_vals, C_off, C_len, C_starts, (int32_t)c_ndiag,
                            pair_ptr, rec, aext, C_vals, (int32_t)blocks, (int32_t)groups, per_xcd,
                            tail5);
-    else
-        hipLaunchKernelGGL((k_astat<T, false, R>), grid, block, lds, as_stream(stream), n, A_off,
-                           A_starts, nA, A_vals, B_vals, C_off, C_len, C_starts, (int32_t)c_ndiag,
-                           pair_ptr, rec, aext, C_vals, (int32_t)blocks, (int32_t)groups, per_xcd,
-                           tail5);
-    return check_launch(fn);
+        return check_launch(fn);
+    };
+    using yes = std::true_type;
+    using no = std::false_type;
+    if constexpr (sizeof(T) == 4 && R == 4) {
+        if (quad) return prefetch ? go(yes{}, yes{}) : go(no{}, yes{});
+    }
+    return prefetch ? go(yes{}, no{}) : go(no{}, no{});
 }
 
 template <typename T>
