@@ -137,10 +137,14 @@ def _axpby(alpha, X: HM, beta, Y: HM | None, stream) -> HM:
     for offs, nm in ((ox, "X"), (oy, "Y")):
         if any(b <= a for a, b in zip(offs, offs[1:])):
             raise ValueError(f"{nm} offsets must be ascending and distinct")
-    if Y is None or oy == ox:
-        # Z has X's diagonals: X's structure tensors, new values
+    if Y is None or oy == ox or set(oy) <= set(ox):
+        # Z has X's diagonals: X's structure tensors, new values (no host
+        # to device copies: I + t H for an H that holds the main diagonal)
         Z = HM(X.n, X.offsets, X.lengths, X.starts,
                torch.empty(X.values.numel(), dtype=dt, device=X.values.device), ox)
+    elif set(ox) <= set(oy):
+        Z = HM(Y.n, Y.offsets, Y.lengths, Y.starts,
+               torch.empty(Y.values.numel(), dtype=dt, device=Y.values.device), oy)
     else:
         Z = hm_structure(X.n, sorted(set(ox) | set(oy)), X.values.device, dt)
     for M, nm in ((X, "X"), (Y, "Y")):
