@@ -436,6 +436,7 @@ def _random_offsets(rng, cnt, lo, hi, with_zero=True):
     (1 << 17, "tail"),      # 512 blocks, the last with 5 rows per lane (513 would take 2 rounds)
     (1 << 20, "short"),     # 25 short C diagonals: 16 rows per lane, 1024 blocks, the last 17
     (1 << 20, "many"),      # 7 x 40 diagonals, > 64 C diagonals: 8 rows per lane, the last 9
+    (1 << 18, "quadpf"),    # 64 x 64 over +-256: metadata prefetch, 4-entry batches, 5-row tail
 ])
 def test_astat_kernel_same_bits_as_gather(dev, oracle, n, case):
     """The A-stationary kernel returns the gather kernel's C bit for bit
@@ -464,6 +465,9 @@ def test_astat_kernel_same_bits_as_gather(dev, oracle, n, case):
     elif case == "many":
         offs_a = [-1024, -32, -1, 0, 1, 32, 1024]
         offs_b = _random_offsets(rng, 40, -5000, 5000)
+    elif case == "quadpf":
+        offs_a = _random_offsets(rng, 63, -256, 256)
+        offs_b = _random_offsets(rng, 63, -256, 256)
     else:
         offs_a = _random_offsets(rng, _lib.ASTAT_MAX_A, -2000, 2000, with_zero=False)
         offs_b = _random_offsets(rng, 9, -100, 100)
@@ -471,7 +475,13 @@ def test_astat_kernel_same_bits_as_gather(dev, oracle, n, case):
     A = workloads.hm_random(n, offs_a, 21, dev)
     B = workloads.hm_random(n, offs_b, 22, dev)
     plan = SpgemmPlan(A, B)
-    rec = plan.astat_records()[: 4 * plan.info.n_pairs].cpu().numpy().reshape(-1, 4)
+    if case == "quadpf":      # >= 3 entries per C diagonal, > 64 per wave's share
+        assert plan.info.n_pairs >= 3 * plan.info.c_ndiag and plan.info.c_ndiag >= 64
+    full = plan.astat_records().cpu().numpy()
+    np_ = plan.info.n_pairs
+    # after the records: two clear error flags, then A's smallest and largest offset
+    assert full[4 * np_: 4 * np_ + 4].tolist() == [0, 0, min(offs_a), max(offs_a)]
+    rec = full[: 4 * np_].reshape(-1, 4)
     pairs = plan.pairs_numpy()
     a_st = A.starts.cpu().numpy()
     a_idx = np.searchsorted(a_st, pairs["ab"].astype(np.int64))
@@ -552,6 +562,8 @@ def test_lds_kernels_with_operands_in_any_order(dev):
     A = shuffled(list(range(-10, 11)), 31)
     B = shuffled(list(range(-8, 9)), 32)
     plan = SpgemmPlan(A, B)
+    # A's offset extremes after the records, whatever the storage order
+    assert plan.astat_records()[4 * plan.info.n_pairs:].cpu().tolist() == [0, 0, -10, 10]
     Cg = plan.multiply(A.values, B.values, kernel="gather")
     for k in ("band", "astat", "auto"):
         Ck = plan.multiply(A.values, B.values, kernel=k)
