@@ -437,6 +437,8 @@ def _random_offsets(rng, cnt, lo, hi, with_zero=True):
     (1 << 20, "short"),     # 25 short C diagonals: 16 rows per lane, 1024 blocks, the last 17
     (1 << 20, "many"),      # 7 x 40 diagonals, > 64 C diagonals: 8 rows per lane, the last 9
     (1 << 18, "quadpf"),    # 64 x 64 over +-256: metadata prefetch, 4-entry batches, 5-row tail
+    (4096, "gd"),           # gemm_diag's band: 10.8 entries per C diagonal, 17 blocks split
+                            # over 3 workgroups each, 4-entry batches
 ])
 def test_astat_kernel_same_bits_as_gather(dev, oracle, n, case):
     """The A-stationary kernel returns the gather kernel's C bit for bit
@@ -465,6 +467,8 @@ def test_astat_kernel_same_bits_as_gather(dev, oracle, n, case):
     elif case == "many":
         offs_a = [-1024, -32, -1, 0, 1, 32, 1024]
         offs_b = _random_offsets(rng, 40, -5000, 5000)
+    elif case == "gd":
+        offs_a = offs_b = list(range(-10, 11))
     elif case == "quadpf":
         offs_a = _random_offsets(rng, 63, -256, 256)
         offs_b = _random_offsets(rng, 63, -256, 256)
