@@ -36,7 +36,12 @@
 // and occupancy (launch_astat).  The plan entries come as records
 // {a, lo, hi, b} (diagpu_spgemm_astat_prepare): a the A diagonal's index,
 // [lo, hi) the C positions where both operands hold an element, b the B
-// index of C position 0.
+// index of C position 0.  Each term's B load is clamped into [lo, hi) and
+// its multiply-add kept by a select, except on a C diagonal whose rows in
+// the block lie inside the matrix for every A offset (tested once per
+// diagonal from A's smallest and largest offset, which the prepare step
+// stores after the records): there every entry takes every term, with no
+// clamp and no select (fp32, up to 4 rows per lane).
 #include <algorithm>
 #include <climits>
 #include <type_traits>
