@@ -508,9 +508,10 @@ def test_astat_kernel_choice_and_capacity(dev):
     band over +-512, for gemm_diag's band below 512 row blocks, for the
     9-point and 5-point stencils' squares, config 4 and config 2's square,
     the band kernel above 512 row blocks, the gather below n = 4096 and for
-    plans of fewer than 16 entries at 2^19 <= n < 2^22 (the tridiagonal
-    square at n = 2^20); more than DIAGPU_ASTAT_MAX_A A diagonals are
-    refused with DIAGPU_ERR_CAPACITY."""
+    plans of fewer than 16 entries and at least 1.5 per C diagonal at
+    2^19 <= n < 2^22 (the tridiagonal square at n = 2^20, but not a
+    random 3 x 3 product there); more than DIAGPU_ASTAT_MAX_A A diagonals
+    are refused with DIAGPU_ERR_CAPACITY."""
     rng = np.random.default_rng(3)
     n = 1 << 18
     offs = _random_offsets(rng, 63, -512, 512)
@@ -532,6 +533,12 @@ def test_astat_kernel_choice_and_capacity(dev):
     assert SpgemmPlan(T, T).kernel_for() == "gather"            # 9 entries at n = 2^20
     T22 = workloads.hm_random(1 << 22, [-1, 0, 1], 7, dev)
     assert SpgemmPlan(T22, T22).kernel_for() == "astat"         # the same at n = 2^22
+    R3a = workloads.hm_random(1 << 20, [-1500, 7, 1900], 7, dev)
+    R3b = workloads.hm_random(1 << 20, [-800, 0, 1200], 8, dev)
+    pr = SpgemmPlan(R3a, R3b)                                     # 9 entries, one per C diagonal
+    assert pr.info.n_pairs == 9 and pr.info.c_ndiag == 9 and pr.kernel_for() == "astat"
+    assert torch.equal(pr.multiply(R3a.values, R3b.values).view(torch.int32),
+                       pr.multiply(R3a.values, R3b.values, kernel="gather").view(torch.int32))
     nine = sorted({dy * 256 + dx for dx in (-1, 0, 1) for dy in (-1, 0, 1)})
     S9 = workloads.hm_random(1 << 16, nine, 8, dev)
     p9 = SpgemmPlan(S9, S9)
