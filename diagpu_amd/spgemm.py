@@ -184,12 +184,13 @@ class SpgemmPlan:
         """The automatic first choice: the LDS-staged band kernel for fp32
         plans whose staged operands fit, whose C diagonals average >= 3
         entries (each operand run then feeds several entries) and that have
-        at least 512 row blocks of 256 (below that the A-stationary kernel or
-        the gather is faster: measured on gemm_diag's band, A-stationary vs
-        band 15.3 vs 16.4 us at n = 65536, 23.5 vs 19.4 us at n = 131072)."""
+        at least 1024 row blocks of 256 (below that the A-stationary kernel
+        or the gather is faster: gemm_diag's band, interleaved rounds,
+        A-stationary vs band 14.5 vs 20.0 us at n = 2^17, 32.0 vs 27.9 us at
+        2^18; the 9-diagonal band's square 6.3 vs 8.2 and 11.7 vs 11.1 us)."""
         na, nb = self.A.offsets.numel(), self.B.offsets.numel()
         if (dtype != torch.float32 or self.info.c_ndiag == 0 or na > 65535 or nb > 32767
-                or self.info.n_pairs < 3 * self.info.c_ndiag or self.n < 512 * 256):
+                or self.info.n_pairs < 3 * self.info.c_ndiag or self.n < 1024 * 256):
             return False
         est = self.band_lds_estimate()
         if est is not None and est > BAND_LDS_BUDGET:

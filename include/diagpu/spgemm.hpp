@@ -296,7 +296,7 @@ public:
         // The band kernel's tables for plans the automatic choice may take
         // (one more stream synchronisation); others prepare on demand.
         band_auto_ = info_.c_ndiag > 0 && a_ndiag <= 65535 && b_ndiag <= 32767 &&
-                     info_.n_pairs >= 3 * info_.c_ndiag && int64_t(n) >= 512 * 256;
+                     info_.n_pairs >= 3 * info_.c_ndiag && int64_t(n) >= 1024 * 256;
         if (band_auto_) prepare_band(stream);
         // The A-stationary kernel's records where the automatic choice may
         // take it.  The records serve both value types (the band kernel is
@@ -322,7 +322,7 @@ public:
     // True where NumericKernel::Auto runs the band kernel for fp32 values:
     // the staged operands fit in LDS, the C diagonals average >= 3 plan
     // entries (each staged operand run then feeds several entries) and there
-    // are >= 512 row blocks of 256 (below that the A-stationary kernel or
+    // are >= 1024 row blocks of 256 (below that the A-stationary kernel or
     // the gather is faster).
     bool uses_band() const { return band_auto_ && band_.eligible; }
     // True where NumericKernel::Auto runs the A-stationary kernel for fp32

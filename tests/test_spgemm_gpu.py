@@ -393,13 +393,16 @@ def test_band_kernel_same_bits_as_gather(dev, oracle, n, offs_a, offs_b):
 
 
 def test_band_kernel_choice_and_capacity(dev):
-    """auto picks the band kernel for gemm_diag's contiguous bands from 512
+    """auto picks the band kernel for gemm_diag's contiguous bands from 1024
     row blocks on (the A-stationary kernel below that) and the gather for
     config 4 (1.3 entries per C diagonal); a plan whose staged operands
     exceed the LDS budget is refused with DIAGPU_ERR_CAPACITY."""
     n = 1 << 14
-    A = workloads.hm_random(1 << 17, range(-10, 11), 1, dev)     # 512 row blocks
+    A = workloads.hm_random(1 << 18, range(-10, 11), 1, dev)     # 1024 row blocks
     assert SpgemmPlan(A, A).uses_band()
+    A17 = workloads.hm_random(1 << 17, range(-10, 11), 1, dev)   # 512: the A-stationary kernel
+    p17 = SpgemmPlan(A17, A17)
+    assert not p17.uses_band() and p17.kernel_for() == "astat"
     small = workloads.hm_random(n, range(-10, 11), 1, dev)        # 64 row blocks
     ps = SpgemmPlan(small, small)
     assert not ps.uses_band() and ps.kernel_for() == "astat"
@@ -505,9 +508,9 @@ def test_astat_kernel_same_bits_as_gather(dev, oracle, n, case):
 
 def test_astat_kernel_choice_and_capacity(dev):
     """auto picks the A-stationary kernel for the square of a 64-diagonal
-    band over +-512, for gemm_diag's band below 512 row blocks, for the
+    band over +-512, for gemm_diag's band below 1024 row blocks, for the
     9-point and 5-point stencils' squares, config 4 and config 2's square,
-    the band kernel above 512 row blocks, the gather below n = 4096 and for
+    the band kernel from 1024 row blocks, the gather below n = 4096 and for
     plans of fewer than 16 entries and at least 1.5 per C diagonal at
     2^19 <= n < 2^22 (the tridiagonal square at n = 2^20, but not a
     random 3 x 3 product there); more than DIAGPU_ASTAT_MAX_A A diagonals
