@@ -353,8 +353,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
             // window, p >= len there, reads row 0)
             auto arow = [&](int j) { return j < R || lane < s ? ab + 64 * j : ab; };
             // one term: B at the position clamped into the entry's range
-            // [e.y, e.z) (an always valid load: 0 <= c < n), A from LDS (row R
-            // of a lane past the window, p >= len there, reads row 0), the
+            // [e.y, e.z) (an always valid load: 0 <= c < n), A from LDS, the
             // multiply-add kept where the clamp leaves the position as it is
             // and the range is not empty: where both operands hold the element
             // (positions p >= len take terms too, but are never stored)
