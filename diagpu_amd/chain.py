@@ -201,6 +201,7 @@ def multiply(A: HM, B: HM, stats: ChainStats | None = None) -> HM:
         torch.cuda.synchronize()
     t0 = time.perf_counter()
     plan = SpgemmPlan(A, B)
+    plan.prepare(A.values.dtype)      # the numeric kernel's set-up belongs to the plan
     inf = plan.info
     # C's structure arrays are views of the plan's buffer (kept alive by
     # them)
