@@ -81,10 +81,11 @@ static_assert(astat_cap<cf32>() == DIAGPU_ASTAT_MAX_A_C64, "complex A diagonals 
 // not in the symbolic plan's form (its A or B start is no diagonal's start,
 // da + db is not its C diagonal's offset, or its shifts or lengths differ
 // from min0(da) - min0(dc), da + min0(db) - min0(dc), n - |da|, n - |db|) or
-// pair_ptr is not a partition of the entries, flag[1] if its B indices do
-// not fit int32.  The kernel builds each A row from A_off and C_off but
-// takes each term's range from the record, so an entry of another form
-// would give a different C without an error.
+// pair_ptr is not a partition of the entries, flag[1] if its B indices
+// reach 2^30 (the numeric kernel forms their byte offsets in 32 bits).  The
+// kernel builds each A row from A_off and C_off but takes each term's range
+// from the record, so an entry of another form would give a different C
+// without an error.
 //
 // One thread per C diagonal k walks its entries [pair_ptr[k], pair_ptr[k +
 // 1]), so no entry searches pair_ptr; each entry's A and B diagonals are
@@ -164,8 +165,8 @@ __global__ __launch_bounds__(kPrepBlock) void k_astat_prepare(
             // record that never fires, whose clamped B load
             // min(max(p, 1), 0) = 0 reads B[0].
             r = int4{a, 1, 1, 0};
-        } else if (b < INT_MIN || b + phi > INT_MAX) {
-            flag[1] = 1;
+        } else if (b < INT_MIN || b + phi > ((int64_t)1 << 30)) {
+            flag[1] = 1;   // the kernel forms 4 (b + c) in 32 bits
         } else {
             r = int4{a, plo, phi, (int)b};
         }
@@ -208,18 +209,30 @@ __device__ __forceinline__ void store_elem_nt(T* p, T v)
     __builtin_nontemporal_store(r, reinterpret_cast<Raw*>(p));
 }
 
-// B element c (0 <= c < n) of the run starting at base.  fp32: a buffer
-// load with the run's start as the descriptor base (scalar) and c's byte
-// offset (below 2^32 for n < 2^30), which spares the per-lane 64-bit
-// address.  Complex: a global load (this toolchain compiles the 64-bit raw
-// buffer load builtin to a single-dword load).
-__device__ __forceinline__ float load_b(const float* base, int c)
+// *(base + o bytes) for a uniform base and offset: compiled to a scalar load
+// with the offset in an SGPR, so the address costs no 64-bit arithmetic.
+template <typename V>
+__device__ __forceinline__ V at_byte(const V* __restrict__ base, uint32_t o)
 {
-    const __amdgpu_buffer_rsrc_t r =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, -1, 0x00020000);
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (uint32_t)c << 2, 0, 0));
+    return *reinterpret_cast<const V*>(reinterpret_cast<const char*>(base) + o);
 }
-__device__ __forceinline__ cf32 load_b(const cf32* base, int c) { return load_elem<cf32, false>(base + c); }
+
+// B element b + c, b the B index of the entry's C position 0 and c the C
+// position (0 <= b + c < 2^30, the prepare step's bound on B indices).
+// fp32: a buffer load through one descriptor over all of B (rB), with the
+// byte offset 4 (b + c) formed in 32-bit arithmetic (exact, since it is
+// below 2^32): an entry costs one scalar shift, not a descriptor of its own.
+// Complex: a global load (this toolchain compiles the 64-bit raw buffer load
+// builtin to a single-dword load).
+__device__ __forceinline__ float load_b(const float*, __amdgpu_buffer_rsrc_t rB, int b, int c)
+{
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(rB, ((uint32_t)c << 2) + ((uint32_t)b << 2), 0, 0));
+}
+__device__ __forceinline__ cf32 load_b(const cf32* B, __amdgpu_buffer_rsrc_t, int b, int c)
+{
+    return load_elem<cf32, false>(B + (int64_t)b + c);
+}
 
 // Stores a wave's RR values of one C diagonal cd[0, len): lane l holds
 // positions pb + 64 j, those in [0, len) are written.  fp32: buffer stores
@@ -228,7 +241,18 @@ __device__ __forceinline__ cf32 load_b(const cf32* base, int c) { return load_el
 // past it (dropped by the hardware): no branch around the stores (config 5
 // 2.33 -> 2.25 ms against branched global stores).  Complex: branched global
 // stores.
-template <typename T, int RR>
+//
+// The test 0 <= p < len takes one of two equivalent forms, which compile to
+// different schedules of the whole diagonal loop: two signed compares
+// (TwoCmp, the kernels of four-entry batches) or one unsigned compare.
+// Measured in interleaved rounds on two boxes: config 3's square (four-entry
+// batches) 7.04-7.07 / 6.67-6.88 ms with two compares against 7.43-7.49 /
+// 7.24-7.27 with one; config 5, config 4, config 2's square and complex
+// config 4 0.5-2 % faster with one.  Counters on config 3's square: with two
+// compares the vector L1 hit rate is 78 % against 72 % and L2 read requests
+// 427 M against 536 M per launch; why the schedule moves the hit rate is not
+// established.
+template <typename T, int RR, bool TwoCmp = false>
 __device__ __forceinline__ void store_c(T* cd, int pb, int len, const T (&acc)[RR])
 {
     if constexpr (sizeof(T) == 4) {
@@ -237,7 +261,8 @@ __device__ __forceinline__ void store_c(T* cd, int pb, int len, const T (&acc)[R
 #pragma unroll
         for (int j = 0; j < RR; ++j) {
             const int p = pb + 64 * j;
-            const uint32_t off = (p >= 0 && p < len) ? (uint32_t)p << 2 : 0xFFFFFFFFu;
+            const bool in = TwoCmp ? (p >= 0 && p < len) : (uint32_t)p < (uint32_t)len;
+            const uint32_t off = in ? (uint32_t)p << 2 : 0xFFFFFFFFu;
             // cache policy 2: non-temporal, as store_elem_nt
             __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc[j]), r, off, 0, 2);
         }
@@ -266,6 +291,8 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
     // A's smallest and largest offset (written by diagpu_spgemm_astat_prepare
     // after the records)
     const int amin = aext[0], amax = aext[1];
+    const __amdgpu_buffer_rsrc_t rB =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(Bv), (short)0, -1, 0x00020000);
     constexpr int kRB = Astat<T, R>::kRB, kLead = Astat<T, R>::kLead;
     constexpr int kStage = Astat<T, R>::kStage, kWords = Astat<T, R>::kWords;
     extern __shared__ float A_l[];   // [nA][kStage] elements: rows i0 - kLead .. i0 + kRB - 1
@@ -318,8 +345,20 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
         const int stride = groups * kWaves;
         int kc = grp * kWaves + wave;
         if (kc >= nC) return;
-        int dcn = C_off[kc], lenn = C_len[kc];
-        int64_t cstn = C_starts[kc], g0n = pair_ptr[kc], g1n = pair_ptr[kc + 1];
+        // The metadata of diagonal k sits at byte offsets 4 k (C_off, C_len)
+        // and 8 k (C_starts, pair_ptr), below 2^32 for nC < 2^29.
+        int dcn = at_byte(C_off, (uint32_t)kc << 2), lenn = at_byte(C_len, (uint32_t)kc << 2);
+        int64_t cstn = at_byte(C_starts, (uint32_t)kc << 3), g0n = at_byte(pair_ptr, (uint32_t)kc << 3),
+                g1n = at_byte(pair_ptr + 1, (uint32_t)kc << 3);
+        // The block-wide part of the every-term test below: whatever a
+        // diagonal's shift s (0 <= s < kLead), its rows [i0 - s, i0 - s + 64
+        // RR) lie in [i0 - kLead + 1, i0 + 64 RR), inside the matrix for
+        // every A offset when blk_in holds; they then meet 0 <= i + dc < n
+        // for dc - dlo in [0, dspan] (dlo = kLead - 1 - i0, dspan = n - 64 RR
+        // - kLead + 1, which is >= 0 where blk_in holds).
+        const bool blk_in = i0 >= kLead - 1 - min(amin, 0) && n - i0 - 64 * RR >= max(amax, 0);
+        const int dlo = kLead - 1 - i0;
+        const uint32_t dspan = (uint32_t)(n - 64 * RR - kLead + 1);
         for (; kc < nC; kc += stride) {
             int dc, len, g0, g1;
             int64_t cst;
@@ -329,29 +368,37 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
                 cst = cstn;
                 g0 = (int)g0n;
                 g1 = (int)g1n;
-                const int kn = min(kc + stride, nC - 1);
-                dcn = C_off[kn];
-                lenn = C_len[kn];
-                cstn = C_starts[kn];
-                g0n = pair_ptr[kn];
-                g1n = pair_ptr[kn + 1];
+                const uint32_t kn = (uint32_t)min(kc + stride, nC - 1);
+                dcn = at_byte(C_off, kn << 2);
+                lenn = at_byte(C_len, kn << 2);
+                cstn = at_byte(C_starts, kn << 3);
+                g0n = at_byte(pair_ptr, kn << 3);
+                g1n = at_byte(pair_ptr + 1, kn << 3);
             } else {
-                dc = C_off[kc];
-                len = C_len[kc];
-                cst = C_starts[kc];
-                g0 = (int)pair_ptr[kc];
-                g1 = (int)pair_ptr[kc + 1];
+                dc = at_byte(C_off, (uint32_t)kc << 2);
+                len = at_byte(C_len, (uint32_t)kc << 2);
+                cst = at_byte(C_starts, (uint32_t)kc << 3);
+                g0 = (int)at_byte(pair_ptr, (uint32_t)kc << 3);
+                g1 = (int)at_byte(pair_ptr + 1, (uint32_t)kc << 3);
             }
             const int mc = dc < 0 ? dc : 0;
-            const int s = (int)((cst + mc) & (kLead - 1));   // C(i0 - s, ...) starts a line
+            // C(i0 - s, ...) starts a line (the low bits of the start suffice)
+            const int s = ((int)(uint32_t)cst + mc) & (kLead - 1);
             const int pb = i0 - s + lane + mc;          // C position of the lane's first row
             const int ab = kLead - s + lane;            // its staged A row
             T acc[RR];
 #pragma unroll
             for (int j = 0; j < RR; ++j) acc[j] = zero_of<T>();
-            // the staged A row of the lane's row j (row R of a lane past the
-            // window, p >= len there, reads row 0)
-            auto arow = [&](int j) { return j < R || lane < s ? ab + 64 * j : ab; };
+            // A element of entry a at the lane's row j: staged row ab + 64 j
+            // (row R of a lane past the window, p >= len there, reads row 0),
+            // addressed as the lane's byte offset plus the entry's (one add
+            // per entry, the rows' 256 j bytes an instruction offset)
+            const char* A_c = reinterpret_cast<const char*>(A_t);
+            const int abx = ab * (int)sizeof(T);
+            auto a_at = [&](int a, int j) -> T {
+                const int rb = j < R || lane < s ? abx + 64 * j * (int)sizeof(T) : abx;
+                return *reinterpret_cast<const T*>(A_c + (a * kStage * (int)sizeof(T) + rb));
+            };
             // one term: B at the position clamped into the entry's range
             // [e.y, e.z) (an always valid load: 0 <= c < n), A from LDS, the
             // multiply-add kept where the clamp leaves the position as it is
@@ -361,13 +408,15 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
                 const int p = pb + 64 * j;
                 const int c = min(max(p, e.y), e.z - 1);
                 ok = c == p && e.y < e.z;
-                b = load_b(Bv + (int64_t)e.w, c);
-                a = A_t[e.x * kStage + arow(j)];
+                b = load_b(Bv, rB, e.w, c);
+                a = a_at(e.x, j);
             };
             // Every entry of this diagonal takes every term of the wave's
             // rows [r0, r0 + 64 RR), r0 = i0 - s, where each row i has
             // 0 <= i, i + da, i + dc < n for all of A's offsets da (the
-            // rows where an entry's A and B elements and C's exist): then
+            // rows where an entry's A and B elements and C's exist; tested
+            // by blk_in and the bounds on dc above, which hold for any s
+            // and so miss at most the kLead - 1 rows at an edge): then
             // the B loads need no clamp and the multiply-adds no select,
             // about a fifth of the vector instructions of the general form,
             // with the same multiply-adds in the same order.  Taken for fp32
@@ -377,9 +426,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
             // per lane the Taylor chain's products lost 2-3 %, complex values
             // 1 %).
             constexpr bool kEveryPath = sizeof(T) == 4 && R <= 4;
-            const int r0 = i0 - s, r1 = i0 - s + 64 * RR;
-            const bool inner = kEveryPath && r0 >= 0 && r0 + amin >= 0 && r0 + dc >= 0 &&
-                               r1 <= n && r1 + amax <= n && r1 + dc <= n;
+            const bool inner = kEveryPath && blk_in && (uint32_t)(dc - dlo) <= dspan;
             // A batch of NU entries: their loads issued together, then the
             // multiply-adds in plan order.  The values are pinned once all
             // loads are issued, so the compiler cannot turn a masked
@@ -393,12 +440,15 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
                 bool ok[NU][RR];
 #pragma unroll
                 for (int u = 0; u < NU; ++u) {
-                    const int4 e = records[g + u];
+                    // byte offset 16 g (below 2^32 for n_pairs < 2^28) from
+                    // records + u: u's 16 bytes an immediate offset, so the
+                    // batch's loads merge into one
+                    const int4 e = at_byte(records + u, (uint32_t)g << 4);
 #pragma unroll
                     for (int j = 0; j < RR; ++j) {
                         if constexpr (kEvery) {
-                            bv[u][j] = load_b(Bv + (int64_t)e.w, pb + 64 * j);
-                            av[u][j] = A_t[e.x * kStage + arow(j)];
+                            bv[u][j] = load_b(Bv, rB, e.w, pb + 64 * j);
+                            av[u][j] = a_at(e.x, j);
                         } else {
                             term(e, j, bv[u][j], av[u][j], ok[u][j]);
                         }
@@ -438,7 +488,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
             } else {
                 walk(std::false_type{});
             }
-            store_c(Cv + cst, pb, len, acc);
+            store_c<T, RR, Quad>(Cv + cst, pb, len, acc);
         }
     };
     if (tail5 && blk == blocks - 1)
@@ -571,11 +621,13 @@ int launch_astat(const char* fn, int32_t n, const int32_t* A_off, const int64_t*
                  void* stream)
 {
     constexpr int kMax = astat_cap<T>();
+    // the kernel addresses metadata and records by 32-bit byte offsets
     if (n < 1 || n >= (1 << 30) || nA < 1 || c_ndiag < 0 || c_ndiag > 2 * (int64_t)n - 1 ||
-        n_pairs < 0 || n_pairs > INT_MAX)
+        c_ndiag >= (1 << 29) || n_pairs < 0 || n_pairs >= (1 << 28))
         return fail(DIAGPU_ERR_ARG,
-                    "%s: bad sizes (n=%d nA=%d c_ndiag=%lld n_pairs=%lld; n < 2^30 here)", fn, n,
-                    nA, (long long)c_ndiag, (long long)n_pairs);
+                    "%s: bad sizes (n=%d nA=%d c_ndiag=%lld n_pairs=%lld; n < 2^30, c_ndiag < "
+                    "2^29 and n_pairs < 2^28 here)", fn, n, nA, (long long)c_ndiag,
+                    (long long)n_pairs);
     if (nA > kMax)
         return fail(DIAGPU_ERR_CAPACITY, "%s: %d A diagonals, at most %d fit in LDS", fn, nA, kMax);
     if (c_ndiag == 0) return DIAGPU_OK;
@@ -673,7 +725,7 @@ DIAGPU_API int diagpu_spgemm_astat_prepare(int32_t n, const int32_t* A_off,
         return fail(DIAGPU_ERR_ARG,
                     "%s: a plan entry is not in the symbolic plan's form (starts, offsets, "
                     "shifts or lengths)", fn);
-    if (host[1]) return fail(DIAGPU_ERR_CAPACITY, "%s: B indices beyond 2^31 - 1", fn);
+    if (host[1]) return fail(DIAGPU_ERR_CAPACITY, "%s: B indices beyond 2^30 - 1", fn);
     return DIAGPU_OK;
 }
 

@@ -228,8 +228,9 @@ class SpgemmPlan:
     def uses_astat(self, dtype=torch.float32) -> bool:
         """The automatic choice after the band kernel: the A-stationary kernel
         where A's diagonals fit its LDS (at most DIAGPU_ASTAT_MAX_A, or
-        DIAGPU_ASTAT_MAX_A_C64 for complex values), 4096 <= n < 2^30, B values are
-        addressable with int32, and
+        DIAGPU_ASTAT_MAX_A_C64 for complex values), 4096 <= n < 2^30, fewer
+        than 2^29 C diagonals and 2^28 plan entries, B has fewer than 2^30
+        values (the prepare step's bound), and
 
           fp32:      any plan, except one of fewer than 16 entries and at
                      least 1.5 per C diagonal at 2^19 <= n < 2^22;
@@ -259,7 +260,8 @@ class SpgemmPlan:
         diagonal."""
         na = self.A.offsets.numel()
         inf = self.info
-        if inf.c_ndiag == 0 or self.n < 4096 or self.n >= 1 << 30:
+        if (inf.c_ndiag == 0 or self.n < 4096 or self.n >= 1 << 30 or inf.c_ndiag >= 1 << 29
+                or inf.n_pairs >= 1 << 28):
             return False
         if dtype == torch.float32:
             thin_mid = (inf.n_pairs < 16 and 2 * inf.n_pairs >= 3 * inf.c_ndiag
@@ -271,7 +273,7 @@ class SpgemmPlan:
             ok = False
         if not ok:
             return False
-        if self._astat is False:                  # refused before: B indices beyond int32
+        if self._astat is False:                  # refused before: B indices beyond 2^30
             return False
         try:
             self.astat_records()

@@ -369,7 +369,8 @@ DIAGPU_API int diagpu_spgemm_numeric_band_mfma_f32(
  * da + db is not its C diagonal's offset, or ash, bsh, al, bl differ from
  * min0(da) - min0(dc), da + min0(db) - min0(dc), n - |da|, n - |db|) or if
  * pair_ptr is not a partition of the n_pairs entries,
- * DIAGPU_ERR_CAPACITY if a B index exceeds 2^31 - 1.  No reference
+ * DIAGPU_ERR_CAPACITY if a B index exceeds 2^30 - 1 (the numeric kernels
+ * form B byte offsets in 32 bits).  No reference
  * counterpart: the A-stationary form of the numeric phase below. */
 DIAGPU_API int diagpu_spgemm_astat_prepare(int32_t n, const int32_t* A_off,
                                            const int64_t* A_starts, int32_t nA,
@@ -385,8 +386,10 @@ DIAGPU_API int diagpu_spgemm_astat_prepare(int32_t n, const int32_t* A_off,
  * and reading only B from memory: for products whose
  * A diagonals each feed many plan entries but whose B window is too wide for
  * the band kernel (e.g. the square of a 64-diagonal band over +-512).
- * records from diagpu_spgemm_astat_prepare for this plan; n < 2^30 (else
- * DIAGPU_ERR_ARG; the other numeric kernels take n = 2^30); nA at most
+ * records from diagpu_spgemm_astat_prepare for this plan; n < 2^30,
+ * c_ndiag < 2^29 and n_pairs < 2^28 (else DIAGPU_ERR_ARG: the kernel
+ * addresses its metadata by 32-bit byte offsets; the other numeric kernels
+ * take n = 2^30); nA at most
  * DIAGPU_ASTAT_MAX_A (else DIAGPU_ERR_CAPACITY). */
 DIAGPU_API int diagpu_spgemm_numeric_astat_f32(
     int32_t n, const int32_t* A_off, const int64_t* A_starts, int32_t nA, const float* A_vals,
@@ -397,8 +400,8 @@ DIAGPU_API int diagpu_spgemm_numeric_astat_f32(
 /* The same with complex64 values: the numeric phase of
  * diagpu_spgemm_numeric_c64 (same C, bit for bit), same records; each
  * workgroup holds a block of 256 rows (512 for a few short C diagonals, 128
- * above 75 A diagonals) plus the 16 before it; n < 2^30 (else
- * DIAGPU_ERR_ARG); nA at most DIAGPU_ASTAT_MAX_A_C64 (else
+ * above 75 A diagonals) plus the 16 before it; n < 2^30, c_ndiag < 2^29
+ * and n_pairs < 2^28 (else DIAGPU_ERR_ARG); nA at most DIAGPU_ASTAT_MAX_A_C64 (else
  * DIAGPU_ERR_CAPACITY).  No reference counterpart (the reference is real
  * only). */
 DIAGPU_API int diagpu_spgemm_numeric_astat_c64(

@@ -303,7 +303,8 @@ public:
         // fp32 only); the rules are SpgemmPlan.uses_astat's in
         // diagpu_amd/spgemm.py, with the measurements behind them.
         const int64_t np = info_.n_pairs, nc = info_.c_ndiag, na = a_ndiag;
-        const bool sized = nc > 0 && int64_t(n) >= 4096 && int64_t(n) < (int64_t(1) << 30);
+        const bool sized = nc > 0 && int64_t(n) >= 4096 && int64_t(n) < (int64_t(1) << 30) &&
+                           nc < (int64_t(1) << 29) && np < (int64_t(1) << 28);
         const bool thin_mid = np < 16 && 2 * np >= 3 * nc && int64_t(n) >= (1 << 19) &&
                               int64_t(n) < (1 << 22);
         astat_auto_ = !uses_band() && sized && na <= DIAGPU_ASTAT_MAX_A && !thin_mid;
@@ -313,7 +314,7 @@ public:
             try {
                 prepare_astat(stream);
             } catch (const Error& e) {
-                if (e.status != DIAGPU_ERR_CAPACITY) throw;   // B indices beyond int32
+                if (e.status != DIAGPU_ERR_CAPACITY) throw;   // B indices beyond 2^30
                 astat_auto_ = astat_auto_c64_ = false;
             }
         }
@@ -327,7 +328,8 @@ public:
     bool uses_band() const { return band_auto_ && band_.eligible; }
     // True where NumericKernel::Auto runs the A-stationary kernel for fp32
     // values: the band kernel does not take the plan, A has at most
-    // DIAGPU_ASTAT_MAX_A diagonals, 4096 <= n < 2^30, and the plan is not one of
+    // DIAGPU_ASTAT_MAX_A diagonals, 4096 <= n < 2^30 (with fewer than 2^29 C
+    // diagonals, 2^28 entries and 2^30 B values), and the plan is not one of
     // fewer than 16 entries and at least 1.5 per C diagonal at 2^19 <= n <
     // 2^22 (there the gather has more work per launch to hide its operand
     // reads: the tridiagonal square at n = 2^20 takes 11.6 us on the gather,
