@@ -184,19 +184,24 @@ def test_complex_and_krylov_argument_errors():
     assert prep(10, fake, 1, 1, fake, 1, -1) == _lib.ERR_ARG      # negative entry count
     assert prep(10, fake, 1, 1, fake, 20, 1) == _lib.ERR_ARG      # c_ndiag > 2n - 1
     assert prep(10, fake, 1, 1, fake, 0, 1) == _lib.ERR_ARG       # entries without C
-    astat = lambda nA, nC, n=100: _status("diagpu_spgemm_numeric_astat_f32", n, fake, fake, nA,
-                                          fake, fake, fake, fake, fake, nC, fake, fake, 1, fake,
-                                          None)
+    astat = lambda nA, nC, n=100, npairs=1: _status("diagpu_spgemm_numeric_astat_f32", n, fake,
+                                                    fake, nA, fake, fake, fake, fake, fake, nC,
+                                                    fake, fake, npairs, fake, None)
     assert astat(0, 5) == _lib.ERR_ARG
     assert astat(3, 5, 1 << 30) == _lib.ERR_ARG     # n < 2^30 (C stores' 32-bit byte range)
+    # the kernel reads metadata and records at 32-bit byte offsets
+    assert astat(3, 1 << 29, 1 << 29) == _lib.ERR_ARG          # c_ndiag < 2^29
+    assert astat(3, 5, 100, 1 << 28) == _lib.ERR_ARG           # n_pairs < 2^28
     assert astat(_lib.ASTAT_MAX_A + 1, 5) == _lib.ERR_CAPACITY
     assert astat(3, 200) == _lib.ERR_ARG           # c_ndiag > 2n - 1
     assert astat(3, 0) == _lib.OK                   # empty C: nothing to do
-    astat_c = lambda nA, nC, n=100: _status("diagpu_spgemm_numeric_astat_c64", n, fake, fake, nA,
-                                            fake, fake, fake, fake, fake, nC, fake, fake, 1,
-                                            fake, None)
+    astat_c = lambda nA, nC, n=100, npairs=1: _status("diagpu_spgemm_numeric_astat_c64", n, fake,
+                                                      fake, nA, fake, fake, fake, fake, fake, nC,
+                                                      fake, fake, npairs, fake, None)
     assert astat_c(0, 5) == _lib.ERR_ARG
     assert astat_c(3, 5, 1 << 30) == _lib.ERR_ARG
+    assert astat_c(3, 1 << 29, 1 << 29) == _lib.ERR_ARG
+    assert astat_c(3, 5, 100, 1 << 28) == _lib.ERR_ARG
     assert astat_c(_lib.ASTAT_MAX_A_C64 + 1, 5) == _lib.ERR_CAPACITY
     assert astat_c(3, 200) == _lib.ERR_ARG
     assert astat_c(3, 0) == _lib.OK

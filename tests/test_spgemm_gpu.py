@@ -658,6 +658,37 @@ def test_astat_prepare_refuses_edited_plans(dev, field, delta):
     assert e.value.status == _lib.ERR_ARG and "symbolic" in str(e.value)
 
 
+def test_astat_prepare_b_index_bound(dev):
+    """The numeric kernel forms B byte offsets 4 (b + c) in 32 bits, so the
+    prepare step accepts a plan while every entry's last B index b + hi stays
+    within 2^30 and refuses it with DIAGPU_ERR_CAPACITY one index beyond; the
+    automatic choice then falls back to the gather.  B's starts and every
+    entry's B start are moved together (the entries keep the symbolic form;
+    the prepare step reads no values)."""
+    n = 5000
+    A = workloads.hm_random(n, [-9, -4, 0, 3, 11], 61, dev)
+    B = workloads.hm_random(n, [-30, -1, 0, 2, 7, 40], 62, dev)
+    plan = SpgemmPlan(A, B)
+    rec = plan.astat_records()[: 4 * plan.info.n_pairs].view(-1, 4).cpu().numpy().astype(np.int64)
+    top = int((rec[:, 3] + rec[:, 2]).max())      # largest b + hi
+    q = plan.pairs[: plan.info.n_pairs * 32].view(torch.int64).view(-1, 4)
+    starts0, bb0 = B.starts.clone(), q[:, 1].clone()
+    for shift, ok in ((2**30 - top, True), (2**30 - top + 1, False)):
+        B.starts.copy_(starts0 + shift)
+        q[:, 1] = bb0 + shift
+        plan._astat = None
+        if ok:
+            got = plan.astat_records()[: 4 * plan.info.n_pairs].view(-1, 4).cpu().numpy()
+            assert np.array_equal(got[:, :3], rec[:, :3])
+            assert np.array_equal(got[:, 3].astype(np.int64), rec[:, 3] + shift)
+        else:
+            with pytest.raises(_lib.DiagpuError) as e:
+                plan.astat_records()
+            assert e.value.status == _lib.ERR_CAPACITY and "2^30" in str(e.value)
+            plan._astat = None
+            assert not plan.uses_astat()
+
+
 def _drop_diagonals(plan, empty):
     """Remove every plan entry of the C diagonals `empty` (their pair_ptr
     ranges become empty); returns the kept entries' mask."""
