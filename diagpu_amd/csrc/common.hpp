@@ -30,4 +30,15 @@ int cu_count();
 template <typename T>
 __host__ __device__ constexpr T ceil_div(T a, T b) { return (a + b - 1) / b; }
 
+// *(base + o bytes) for a uniform base and offset: compiled to a scalar load
+// with the offset in an SGPR (s_load ... sbase, soffset), so the address
+// costs no 64-bit arithmetic.  A constant part of the offset belongs in the
+// pointer (base + 1), where it becomes the instruction's immediate and
+// neighbouring loads can merge.
+template <typename V>
+__device__ __forceinline__ V at_byte(const V* __restrict__ base, uint32_t o)
+{
+    return *reinterpret_cast<const V*>(reinterpret_cast<const char*>(base) + o);
+}
+
 }  // namespace diagpu

@@ -209,14 +209,6 @@ __device__ __forceinline__ void store_elem_nt(T* p, T v)
     __builtin_nontemporal_store(r, reinterpret_cast<Raw*>(p));
 }
 
-// *(base + o bytes) for a uniform base and offset: compiled to a scalar load
-// with the offset in an SGPR, so the address costs no 64-bit arithmetic.
-template <typename V>
-__device__ __forceinline__ V at_byte(const V* __restrict__ base, uint32_t o)
-{
-    return *reinterpret_cast<const V*>(reinterpret_cast<const char*>(base) + o);
-}
-
 // B element b + c, b the B index of the entry's C position 0 and c the C
 // position (0 <= b + c < 2^30, the prepare step's bound on B indices).
 // fp32: a buffer load through one descriptor over all of B (rB), with the

@@ -215,8 +215,8 @@ __global__ __launch_bounds__(kThreads) void k_band(
 #pragma unroll
             for (int u = 0; u < kS; ++u) {
                 const int d = d0 + u < nA ? d0 + u : nA - 1;
-                o[u] = A_off[d];
-                st[u] = A_starts[d];
+                o[u] = at_byte(A_off, (uint32_t)d << 2);
+                st[u] = at_byte(A_starts, (uint32_t)d << 3);
             }
 #pragma unroll
             for (int u = 0; u < kS; ++u)
@@ -228,8 +228,8 @@ __global__ __launch_bounds__(kThreads) void k_band(
 #pragma unroll
             for (int u = 0; u < kS; ++u) {
                 const int d = d0 + u < nB ? d0 + u : nB - 1;
-                o[u] = B_off[d];
-                st[u] = B_starts[d];
+                o[u] = at_byte(B_off, (uint32_t)d << 2);
+                st[u] = at_byte(B_starts, (uint32_t)d << 3);
             }
             for (int sl = 0; sl < slots; ++sl) {
                 const int q = rr + kRB * sl;
@@ -262,8 +262,12 @@ __global__ __launch_bounds__(kThreads) void k_band(
         auto evaluate = [&](auto interior_tag) {
             constexpr bool kInt = decltype(interior_tag)::value;
             for (int kc = wave; kc < nC; kc += kWaves) {
-                const int dc = C_off[kc];
-                const int g0 = (int)pair_ptr[kc], g1 = (int)pair_ptr[kc + 1];
+                // byte offsets 4 kc and 8 kc: small, since the plan's entries
+                // (16 bytes each, at least one per C diagonal) fit the 64 KiB
+                // LDS budget
+                const int dc = at_byte(C_off, (uint32_t)kc << 2);
+                const int g0 = (int)at_byte(pair_ptr, (uint32_t)kc << 3),
+                          g1 = (int)at_byte(pair_ptr + 1, (uint32_t)kc << 3);
                 float acc[kR];
 #pragma unroll
                 for (int j = 0; j < kR; ++j) acc[j] = 0.f;
@@ -308,7 +312,7 @@ __global__ __launch_bounds__(kThreads) void k_band(
                     }
                     step(e, a, b);
                 }
-                float* __restrict__ cp = Cv + C_starts[kc] + (dc < 0 ? dc : 0);
+                float* __restrict__ cp = Cv + at_byte(C_starts, (uint32_t)kc << 3) + (dc < 0 ? dc : 0);
 #pragma unroll
                 for (int j = 0; j < kR; ++j) {
                     const int ii = row0 + 64 * j;
