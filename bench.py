@@ -402,42 +402,68 @@ def compare_kernels(plan, sets, reps: int, alg: int, flops: int, complex_values:
     (fp32 or complex64 values), forced, on the same rotated operand sets
     (the side-by-side run of spmspm/bench_spmspm.cu:518-653), timed in
     interleaved rounds (auto, k1, k2, ...; the order rotated by one leg each
-    round, so every leg leads as many rounds; each round opened behind a
-    spin so the first leg's launch latency stays out of its window; reps /
+    round, so every leg leads as many rounds, and reversed every other
+    round, so every leg follows two different legs; each round opened behind
+    a spin so the first leg's launch latency stays out of its window; reps /
     rounds products per leg per round) and reported as the median over
     rounds of the time per product, with GFLOP/s, the fraction of HBM peak,
     and whether C is bit for bit the gather's (where C fits CHECK_BYTES).
+    The MFMA band kernel, opt-in and never the automatic choice, is timed
+    in rounds of its own after the others: the launch that followed it ran
+    up to 45 % slower (the A-stationary kernel on gemm_diag's band at n =
+    2^20: 115 against 79 us for the launch after it), which would charge its
+    neighbour in the interleaved order.
     Returns (auto record, {kernel: record})."""
     import statistics
     import torch
     names = kernel_legs(plan, complex_values)
-    legs = ["auto"] + names
+    legs = ["auto"] + [k for k in names if k != "band_mfma"]
+    alone = [k for k in names if k == "band_mfma"]
     stream = torch.cuda.current_stream()
     nsets = len(sets)
     rounds = max(1, min(rounds, reps))
     per = max(1, reps // rounds)
-    for k in legs:
+    for k in legs + alone:
         for i in range(2):
             plan.numeric(*sets[i % nsets], kernel=k)
     torch.cuda.synchronize()
-    times = {k: [] for k in legs}
+    times = {k: [] for k in legs + alone}
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * len(legs))]
-    for r in range(rounds):
-        gpu_spin(stream, 100.0)
-        order = legs[r % len(legs):] + legs[: r % len(legs)]   # each leg leads some rounds
-        for j, k in enumerate(order):
-            ev[2 * j].record(stream)
-            for i in range(per):
-                plan.numeric(*sets[(r * per + i) % nsets], kernel=k)
-            ev[2 * j + 1].record(stream)
-        torch.cuda.synchronize()
-        for j, k in enumerate(order):
-            times[k].append(ev[2 * j].elapsed_time(ev[2 * j + 1]) / per)
+
+    # one counter over every launch, whatever its leg: consecutive launches
+    # read different sets, so no leg reads a set the leg before it has just
+    # brought into the MALL (with a per-leg index, each leg's second product
+    # read the set its predecessor read last)
+    launch = [0]
+
+    def run_rounds(group, order_of):
+        for r in range(rounds):
+            gpu_spin(stream, 100.0)
+            order = order_of(r)
+            for j, k in enumerate(order):
+                ev[2 * j].record(stream)
+                for i in range(per):
+                    plan.numeric(*sets[launch[0] % nsets], kernel=k)
+                    launch[0] += 1
+                ev[2 * j + 1].record(stream)
+            torch.cuda.synchronize()
+            for j, k in enumerate(order):
+                times[k].append(ev[2 * j].elapsed_time(ev[2 * j + 1]) / per)
+
+    def interleaved(r):
+        # rounds 2s and 2s + 1: the order rotated by s legs, forward then
+        # reversed (each leg leads about as many rounds either way)
+        s = (r // 2) % len(legs)
+        order = legs[s:] + legs[:s]
+        return order[::-1] if r % 2 else order
+    run_rounds(legs, interleaved)
+    for k in alone:
+        run_rounds([k], lambda r, k=k: [k])
     esz = 8 if complex_values else 4
     check = plan.info.c_nnz * esz <= CHECK_BYTES
     ref = None
     out = {}
-    for k in ["gather"] + [x for x in legs if x != "gather"]:
+    for k in ["gather"] + [x for x in legs + alone if x != "gather"]:
         kms = statistics.median(times[k])
         rec = {"numeric_ms": round(kms, 5), "GFLOPs": round(flops / (kms * 1e6), 1),
                "frac_hbm": round(alg / (kms * 1e6) / HBM_PEAK_GBS, 4),
@@ -684,14 +710,20 @@ def time_propagator(grid: str = "3d", order: int = 6, dt: float = 0.02, m: int =
                                  if kry_ms > apply_ms else None)}
 
 
-def time_gemm_diag(n: int = 4096, hb: int = 10, reps: int = 100, cpu_seconds: float = 0.0):
+def time_gemm_diag(n: int = 4096, hb: int = 10, reps: int = 100, cpu_seconds: float = 0.0,
+                   rotate: bool = False):
     """gemm_diag on row-packed operands (gemm_diag/gemm_diag.cu:9-15) with the
     reference driver's default shape (n = 4096, offsets -hb..hb, values
     U(0.5, 1.5), gemm_diag.cu:467-486): the plan once, then the automatic
     choice and every kernel that takes the plan in interleaved rounds of
     `reps` products each (compare_kernels), including the fp32 MFMA band
     kernel with its utilisation (useful / issued flops from its tile
-    geometry).  The reference kernel has no
+    geometry).  One operand set, as the reference driver times its
+    products, or with `rotate` the bench's rotated sets of at least twice
+    the MALL (each product on operands no recent product touched): at n =
+    2^20 one set (348 MB) stays partly in the 256 MB MALL, which favoured
+    the A-stationary kernel (79 against 94 us for the band kernel; rotated,
+    118 against 97 on compact operands of the same band).  The reference kernel has no
     tensor-core instructions (products in shared memory, a sequential
     reduction and atomicAdd).  With cpu_seconds > 0 the oracle's OpenMP
     SpGEMM loop runs the same plan over the same row-packed operands on the
@@ -718,7 +750,12 @@ def time_gemm_diag(n: int = 4096, hb: int = 10, reps: int = 100, cpu_seconds: fl
     nnz = sum(n - abs(d) for d in offs)
     alg = 4 * (2 * nnz + plan.info.c_nnz)
     flops = plan.info.useful_flops
-    auto, kernels = compare_kernels(plan, [(DA, DB, C)], reps, alg, flops)
+    sets = [(DA, DB, C)]
+    if rotate:
+        set_bytes = 4 * (DA.numel() + DB.numel() + C.numel())
+        nsets = 1 if set_bytes >= 2 * MALL_BYTES else max(3, -(-2 * MALL_BYTES // set_bytes))
+        sets += [(DA.clone(), DB.clone(), torch.empty_like(C)) for _ in range(nsets - 1)]
+    auto, kernels = compare_kernels(plan, sets, reps, alg, flops)
     ms = auto["numeric_ms"]
     kern = plan.kernel_for()
     rec = {"workload": f"gemm_diag_n{n}_hb{hb}", "n": n, "A_diags": len(offs),
@@ -857,7 +894,7 @@ def main(argv=None) -> int:
         elif w == "gemmdiag":
             print(json.dumps(time_gemm_diag()), flush=True)
         elif w == "gemmdiag20":
-            print(json.dumps(time_gemm_diag(1 << 20, 10, 20)), flush=True)
+            print(json.dumps(time_gemm_diag(1 << 20, 10, 20, rotate=True)), flush=True)
         else:
             raise SystemExit(f"unknown --only {w}")
         return 0
@@ -955,7 +992,8 @@ def main(argv=None) -> int:
             extras["taylor_chain"] = {"error": repr(e)}
         for n_gd, reps_gd in ((4096, 100), (1 << 20, 20)):
             try:
-                rec = time_gemm_diag(n_gd, 10, reps_gd, cpu_seconds=min(2.0, args.cpu_seconds))
+                rec = time_gemm_diag(n_gd, 10, reps_gd, cpu_seconds=min(2.0, args.cpu_seconds),
+                                     rotate=n_gd > 4096)
                 extras[rec["workload"]] = rec
                 log(f"extra {rec['workload']}: {rec['numeric_ms']} ms, {rec['GFLOPs']} GFLOP/s")
             except Exception as e:

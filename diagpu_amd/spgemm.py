@@ -233,7 +233,7 @@ class SpgemmPlan:
         values (the prepare step's bound), and
 
           fp32:      any plan, except one of fewer than 16 entries and at
-                     least 1.5 per C diagonal at 2^19 <= n < 2^22;
+                     least 1.5 per C diagonal at 2^19 <= n < 2^20;
           complex64: n >= 2^16, or >= 3 entries per A diagonal.
 
         fp32 thresholds from the gather and this kernel timed side by side
@@ -247,12 +247,13 @@ class SpgemmPlan:
         (11.4 vs 12.7 us: too little work per staged block) and tied on a
         36-entry random product at n = 2^20; from n = 2^22 this kernel's
         longer row blocks win again (tridiagonal square 42.5 vs 51.4 us).
-        Thin plans (fewer than 16 entries) at 2^19 <= n < 2^22, timed again
-        after the clamp-free entry loop (20 shapes x 2 runs): the gather still
-        wins the tridiagonal square (1.8 entries per C diagonal; 11.6 vs 13.3
-        us at 2^20), this kernel the plans of one entry per C diagonal
-        (random 3 x 3, 3 x 5, a diagonal times 12) by 5-17 % from n = 2^20,
-        losing up to 15 % at 2^19.
+        Thin plans (fewer than 16 entries) at 2^19 <= n <= 3 2^20, timed
+        again after the scalar-cost changes with every product on operands
+        no recent product touched (25 shapes x 2 runs): from n = 2^20 this
+        kernel wins all of them, the tridiagonal square by 3-8 % (15.0 vs
+        16.3 us at 2^20), plans of one entry per C diagonal by 5-21 %; at
+        2^19 the gather wins the tridiagonal square (10.2 vs 13.4 us), random
+        3 x 3 and 5-point x tridiagonal by 4-6 %.
         Complex values, timed the same way on 25 shapes from n = 4096 to
         2^22: this kernel was faster on 24, by 5-50 % (the complex gather
         re-reads the operand runs at its items' edges); the gather was
@@ -265,7 +266,7 @@ class SpgemmPlan:
             return False
         if dtype == torch.float32:
             thin_mid = (inf.n_pairs < 16 and 2 * inf.n_pairs >= 3 * inf.c_ndiag
-                        and 1 << 19 <= self.n < 1 << 22)
+                        and 1 << 19 <= self.n < 1 << 20)
             ok = na <= _lib.ASTAT_MAX_A and not thin_mid
         elif dtype == torch.complex64:
             ok = na <= _lib.ASTAT_MAX_A_C64 and (self.n >= 1 << 16 or inf.n_pairs >= 3 * na)

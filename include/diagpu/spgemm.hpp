@@ -306,7 +306,7 @@ public:
         const bool sized = nc > 0 && int64_t(n) >= 4096 && int64_t(n) < (int64_t(1) << 30) &&
                            nc < (int64_t(1) << 29) && np < (int64_t(1) << 28);
         const bool thin_mid = np < 16 && 2 * np >= 3 * nc && int64_t(n) >= (1 << 19) &&
-                              int64_t(n) < (1 << 22);
+                              int64_t(n) < (1 << 20);
         astat_auto_ = !uses_band() && sized && na <= DIAGPU_ASTAT_MAX_A && !thin_mid;
         astat_auto_c64_ = sized && na <= DIAGPU_ASTAT_MAX_A_C64 &&
                           (int64_t(n) >= (1 << 16) || np >= 3 * na);
@@ -331,9 +331,9 @@ public:
     // DIAGPU_ASTAT_MAX_A diagonals, 4096 <= n < 2^30 (with fewer than 2^29 C
     // diagonals, 2^28 entries and 2^30 B values), and the plan is not one of
     // fewer than 16 entries and at least 1.5 per C diagonal at 2^19 <= n <
-    // 2^22 (there the gather has more work per launch to hide its operand
-    // reads: the tridiagonal square at n = 2^20 takes 11.6 us on the gather,
-    // 13.3 on this kernel).
+    // 2^20 (there the gather has more work per launch to hide its operand
+    // reads: the tridiagonal square at n = 2^19 takes 10.2 us on the gather,
+    // 13.4 on this kernel).
     bool uses_astat() const { return astat_auto_; }
     // The same for complex64 values: A has at most DIAGPU_ASTAT_MAX_A_C64
     // diagonals, 4096 <= n < 2^30, and n >= 2^16 or >= 3 entries per A diagonal.

@@ -512,9 +512,9 @@ def test_astat_kernel_choice_and_capacity(dev):
     9-point and 5-point stencils' squares, config 4 and config 2's square,
     the band kernel from 1024 row blocks, the gather below n = 4096 and for
     plans of fewer than 16 entries and at least 1.5 per C diagonal at
-    2^19 <= n < 2^22 (the tridiagonal square at n = 2^20, but not a
-    random 3 x 3 product there); more than DIAGPU_ASTAT_MAX_A A diagonals
-    are refused with DIAGPU_ERR_CAPACITY."""
+    2^19 <= n < 2^20 (the tridiagonal square at n = 2^19, not at 2^20, and
+    not a random 3 x 3 product at 2^20); more than DIAGPU_ASTAT_MAX_A A
+    diagonals are refused with DIAGPU_ERR_CAPACITY."""
     rng = np.random.default_rng(3)
     n = 1 << 18
     offs = _random_offsets(rng, 63, -512, 512)
@@ -532,10 +532,13 @@ def test_astat_kernel_choice_and_capacity(dev):
     assert SpgemmPlan(g5, g5).kernel_for() == "gather"
     A4, B4 = workloads.spgemm_config(4, seed=4, device=dev)
     assert SpgemmPlan(A4, B4).kernel_for() == "astat"           # 63 entries over 47 C diagonals
-    T = workloads.hm_random(1 << 20, [-1, 0, 1], 7, dev)
-    assert SpgemmPlan(T, T).kernel_for() == "gather"            # 9 entries at n = 2^20
-    T22 = workloads.hm_random(1 << 22, [-1, 0, 1], 7, dev)
-    assert SpgemmPlan(T22, T22).kernel_for() == "astat"         # the same at n = 2^22
+    T = workloads.hm_random(1 << 19, [-1, 0, 1], 7, dev)
+    assert SpgemmPlan(T, T).kernel_for() == "gather"            # 9 entries at n = 2^19
+    T20 = workloads.hm_random(1 << 20, [-1, 0, 1], 7, dev)
+    pt = SpgemmPlan(T20, T20)
+    assert pt.kernel_for() == "astat"                            # the same at n = 2^20
+    assert torch.equal(pt.multiply(T20.values, T20.values).view(torch.int32),
+                       pt.multiply(T20.values, T20.values, kernel="gather").view(torch.int32))
     R3a = workloads.hm_random(1 << 20, [-1500, 7, 1900], 7, dev)
     R3b = workloads.hm_random(1 << 20, [-800, 0, 1200], 8, dev)
     pr = SpgemmPlan(R3a, R3b)                                     # 9 entries, one per C diagonal
