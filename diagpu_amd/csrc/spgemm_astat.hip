@@ -41,7 +41,7 @@
 // the block lie inside the matrix for every A offset (tested once per
 // diagonal from A's smallest and largest offset, which the prepare step
 // stores after the records): there every entry takes every term, with no
-// clamp and no select (fp32, up to 4 rows per lane).
+// clamp and no select.
 #include <algorithm>
 #include <climits>
 #include <type_traits>
@@ -411,14 +411,16 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
             // and so miss at most the kLead - 1 rows at an edge): then
             // the B loads need no clamp and the multiply-adds no select,
             // about a fifth of the vector instructions of the general form,
-            // with the same multiply-adds in the same order.  Taken for fp32
-            // at up to 4 rows per lane (measured against the general form
-            // alone: make_banded(100000, 16) squared 34.7 -> 28.2 us, config
-            // 3's square 7.62 -> 7.43 ms, config 5 2.28 -> 2.23 ms; at 8 rows
-            // per lane the Taylor chain's products lost 2-3 %, complex values
-            // 1 %).
-            constexpr bool kEveryPath = sizeof(T) == 4 && R <= 4;
-            const bool inner = kEveryPath && blk_in && (uint32_t)(dc - dlo) <= dspan;
+            // with the same multiply-adds in the same order.  Measured
+            // against the general form alone: make_banded(100000, 16) squared
+            // 34.7 -> 28.2 us, config 3's square 7.62 -> 7.43 ms, config 5
+            // 2.28 -> 2.23 ms (fp32, 4 rows per lane); at 16 rows per lane
+            // config 1's square 15.4 -> 14.8 us and config 4 42.5 -> 42.05
+            // us, at 8 the Taylor chain's products 1.83 -> 1.81 ms, complex
+            // config 5 5.95 -> 5.85 ms.  (Before the scalar loads at byte
+            // offsets the path lost 2-3 % at 8 rows per lane and 1 % for
+            // complex values.)
+            const bool inner = blk_in && (uint32_t)(dc - dlo) <= dspan;
             // A batch of NU entries: their loads issued together, then the
             // multiply-adds in plan order.  The values are pinned once all
             // loads are issued, so the compiler cannot turn a masked
@@ -471,15 +473,10 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
                     for (; g + 2 <= g1; g += 2) batch(std::integral_constant<int, 2>{}, every, g);
                 for (; g < g1; ++g) batch(std::integral_constant<int, 1>{}, every, g);
             };
-            if constexpr (kEveryPath) {
-                if (inner) {
-                    walk(std::true_type{});
-                } else {
-                    walk(std::false_type{});
-                }
-            } else {
+            if (inner)
+                walk(std::true_type{});
+            else
                 walk(std::false_type{});
-            }
             store_c<T, RR, Quad>(Cv + cst, pb, len, acc);
         }
     };
