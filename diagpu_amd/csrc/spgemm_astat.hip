@@ -29,11 +29,11 @@
 // [i0 + kRB - s, n) as one more row per lane (its staged window holds them,
 // since n <= i0 + kRB).
 //
-// A workgroup has kWaves waves; wave w evaluates C diagonals w, w + kWaves,
-// ... over the block's kRB = 64 R rows, R rows per lane (lane l: rows l,
-// l + 64, ..., l + 64 (R - 1) of the shifted window; R + 1 in the longer
-// last block), R = 2, 4, 8 or 16 chosen per launch from the plan's shape
-// and occupancy (launch_astat).  The plan entries come as records
+// A workgroup has W = kWaves waves, or one per C diagonal for plans of
+// fewer; wave w evaluates C diagonals w, w + W, ... over the block's kRB =
+// 64 R rows, R rows per lane (lane l: rows l, l + 64, ..., l + 64 (R - 1)
+// of the shifted window; R + 1 in the longer last block), R = 2, 4, 8 or 16
+// chosen per launch from the plan's shape and occupancy (launch_astat).  The plan entries come as records
 // {a, lo, hi, b} (diagpu_spgemm_astat_prepare): a the A diagonal's index,
 // [lo, hi) the C positions where both operands hold an element, b the B
 // index of C position 0.  Each term's B load is clamped into [lo, hi) and
@@ -43,6 +43,7 @@
 // stores after the records): there every entry takes every term, with no
 // clamp and no select.
 #include <algorithm>
+#include <atomic>
 #include <climits>
 #include <type_traits>
 
@@ -302,6 +303,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
     const int grp = unit % groups;
     const int r = (int)threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(r >> 6), lane = r & 63;
+    const int nw = (int)(blockDim.x >> 6);          // waves in this workgroup
     const int i0 = blk * kRB;                       // n < 2^30: rows fit int32
 
     // Stage A: one wave-instruction per 64 dwords of a diagonal's window
@@ -309,7 +311,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
     // diagonal (the address is always valid; a staged element that does not
     // exist is never used: its terms are outside [lo, hi)).
     const float* Aw = reinterpret_cast<const float*>(Av);
-    for (int d = wave; d < nA; d += kWaves) {
+    for (int d = wave; d < nA; d += nw) {
         const int o = A_off[d];
         const int64_t st = A_starts[d];
         const int len = n - (o < 0 ? -o : o);
@@ -334,8 +336,8 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
         // With Prefetch, a diagonal's metadata is loaded while the diagonal
         // before it runs (index clamped rather than tested: a load under a
         // branch is waited for where the branch joins).
-        const int stride = groups * kWaves;
-        int kc = grp * kWaves + wave;
+        const int stride = groups * nw;
+        int kc = grp * nw + wave;
         if (kc >= nC) return;
         // The metadata of diagonal k sits at byte offsets 4 k (C_off, C_len)
         // and 8 k (C_starts, pair_ptr), below 2^32 for nC < 2^29.
@@ -486,30 +488,46 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
         run(std::integral_constant<int, R>{});
 }
 
-// Workgroups of k_astat<T, *, R> that fit a CU by registers (its LDS aside),
-// looked up once per instantiation: the 16-wave workgroups fit twice at up
-// to 64 VGPRs, once above.
-template <typename T, int R> int wgs_by_regs()
+// Workgroups of W waves of k_astat<T, *, R> that fit a CU by registers (its
+// LDS aside), looked up once per instantiation and W: the 16-wave
+// workgroups fit twice at up to 64 VGPRs, once above.
+template <typename T, int R> int wgs_by_regs(int W)
 {
-    static const int v = [] {
-        int a = 0, b = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, (const void*)k_astat<T, false, R>,
-                                                        64 * kWaves, 0) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, (const void*)k_astat<T, true, R>,
-                                                        64 * kWaves, 0) != hipSuccess)
-            return 1;
-        return std::max(1, std::min(a, b));
-    }();
+    static std::atomic<int> cache[kWaves + 1];
+    int v = cache[W].load(std::memory_order_relaxed);
+    if (v) return v;
+    int a = 0, b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, (const void*)k_astat<T, false, R>,
+                                                    64 * W, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, (const void*)k_astat<T, true, R>,
+                                                    64 * W, 0) != hipSuccess)
+        v = 1;
+    else
+        v = std::max(1, std::min(a, b));
+    cache[W].store(v, std::memory_order_relaxed);
     return v;
 }
 
 // Workgroup slots of k_astat<T, *, R> on the GPU for nA A diagonals: by
 // registers and by the LDS the staged A rows take (160 KiB per CU).
-template <typename T, int R> int64_t astat_slots(int32_t nA)
+template <typename T, int R> int64_t astat_slots(int32_t nA, int W = kWaves)
 {
     const int64_t lds = (int64_t)nA * Astat<T, R>::kStage * (int64_t)sizeof(T);
     const int64_t by_lds = std::max<int64_t>(1, (160 * 1024) / lds);
-    return std::min<int64_t>(wgs_by_regs<T, R>(), by_lds) * (int64_t)cu_count();
+    return std::min<int64_t>(wgs_by_regs<T, R>(W), by_lds) * (int64_t)cu_count();
+}
+
+// Waves per workgroup: kWaves, or one per C diagonal where there are fewer
+// (a wave evaluates whole C diagonals, so the others would idle while
+// holding the CU's registers): more, smaller workgroups share a CU.
+// Measured (interleaved rounds, same bits): config 1's square (5 C
+// diagonals) 14.6 -> 11.9 us; config 2's square (13) level.  Spreading
+// more diagonals evenly over fewer waves (41 over 3 x 14 for gemm_diag at
+// n = 4096) was 5 % slower, so from kWaves diagonals the workgroups keep
+// kWaves waves.
+inline int waves_for(int64_t c_ndiag)
+{
+    return c_ndiag < kWaves ? (int)std::max<int64_t>(1, c_ndiag) : kWaves;
 }
 
 // One launch of k_astat<T, *, R> (arguments checked by the caller).
@@ -526,7 +544,8 @@ int launch_rows(const char* fn, int32_t n, const int32_t* A_off, const int64_t* 
     // Row blocks and their split: too few blocks to give every CU its
     // workgroups split each block's C diagonals over several workgroups (at
     // most one per wave's worth of diagonals).
-    const int64_t slots = astat_slots<T, R>(nA);
+    const int W = waves_for(c_ndiag);
+    const int64_t slots = astat_slots<T, R>(nA, W);
     // fp32 launches of 4 rows per lane and fewer than 16 rounds of
     // workgroups also split each block, over G = 2 or 4 workgroups, towards
     // 16 rounds (while every wave keeps at least kPrefetchDiagsPerWave C
@@ -545,7 +564,7 @@ int launch_rows(const char* fn, int32_t n, const int32_t* A_off, const int64_t* 
     auto split = [&](int64_t blocks) {
         if (blocks >= slots) return G;
         return std::max<int64_t>(G, std::min<int64_t>(ceil_div<int64_t>(slots, blocks),
-                                                      ceil_div<int64_t>(c_ndiag, kWaves)));
+                                                      ceil_div<int64_t>(c_ndiag, W)));
     };
     // ceil((n + kLead) / kRB) blocks of R rows per lane, the last covering
     // the rows the line-aligned shift leaves (at most kLead - 1 per
@@ -570,13 +589,13 @@ int launch_rows(const char* fn, int32_t n, const int32_t* A_off, const int64_t* 
     // the metadata prefetch pays where waves walk many diagonals (config 5:
     // ~575 each) and costs where they walk one or two (the 7-point stencil's
     // square: 25 C diagonals over 16 waves, 31 -> 34 us)
-    const bool prefetch = c_ndiag >= kPrefetchDiagsPerWave * groups * kWaves;
+    const bool prefetch = c_ndiag >= kPrefetchDiagsPerWave * groups * W;
     // Quad (fp32, 4 rows per lane): batches of four entries in the
     // every-term form, for plans of >= 3 entries per C diagonal on average
     // (make_banded(100000, 16) squared 27.9 -> 26.3 us, config 3's square
     // 7.45 -> 7.33 ms; config 5, 1.8 entries per C diagonal, lost 1 %)
     const bool quad = n_pairs >= 3 * c_ndiag;
-    const dim3 grid((unsigned)(per_xcd * kNumXcd)), block(64 * kWaves);
+    const dim3 grid((unsigned)(per_xcd * kNumXcd)), block(64 * W);
     const int4* rec = reinterpret_cast<const int4*>(records);
     const int32_t* aext = records + 4 * n_pairs + 2;
     auto go = [&](auto pf, auto qd) {
