@@ -436,7 +436,7 @@ def compare_kernels(plan, sets, reps: int, alg: int, flops: int, complex_values:
     # read the set its predecessor read last)
     launch = [0]
 
-    def run_rounds(group, order_of):
+    def run_rounds(order_of):
         for r in range(rounds):
             gpu_spin(stream, 100.0)
             order = order_of(r)
@@ -456,9 +456,9 @@ def compare_kernels(plan, sets, reps: int, alg: int, flops: int, complex_values:
         s = (r // 2) % len(legs)
         order = legs[s:] + legs[:s]
         return order[::-1] if r % 2 else order
-    run_rounds(legs, interleaved)
+    run_rounds(interleaved)
     for k in alone:
-        run_rounds([k], lambda r, k=k: [k])
+        run_rounds(lambda r, k=k: [k])
     esz = 8 if complex_values else 4
     check = plan.info.c_nnz * esz <= CHECK_BYTES
     ref = None
