@@ -98,6 +98,16 @@ PROTOTYPES: dict[str, tuple] = {
         _vp,
         _vp, _sz,
         C.POINTER(SpgemmInfo), _vp]),
+    "diagpu_spgemm_symbolic_astat": (C.c_int, [
+        _i32,
+        _vp, _vp, _vp, _i32,
+        _vp, _vp, _vp, _i32,
+        _vp, _vp, _vp, _i64,
+        _vp, _vp, _i64,
+        _vp,
+        _vp, _sz,
+        _vp, C.POINTER(_i32),
+        C.POINTER(SpgemmInfo), _vp]),
     "diagpu_spgemm_symbolic_noalloc": (C.c_int, [
         _i32,
         _vp, _vp, _vp, _i32,

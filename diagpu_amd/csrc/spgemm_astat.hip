@@ -49,6 +49,7 @@
 
 #include "common.hpp"
 #include "elem.hpp"
+#include "spgemm_internal.hpp"
 
 namespace diagpu {
 namespace {
@@ -110,33 +111,50 @@ __device__ __forceinline__ int find_start(const int64_t* s, int32_t cnt, int64_t
     return -1;
 }
 
-__global__ __launch_bounds__(kPrepBlock) void k_astat_prepare(
-    int32_t n, const int32_t* __restrict__ A_off, const int64_t* __restrict__ A_starts, int32_t nA,
-    const int32_t* __restrict__ B_off, const int64_t* __restrict__ B_starts, int32_t nB,
-    const int32_t* __restrict__ C_off, const int64_t* __restrict__ pair_ptr, int64_t c_ndiag,
-    const diagpu_gpair* __restrict__ pairs, int64_t n_pairs, int4* __restrict__ records,
-    int32_t* __restrict__ flag)
+// A's and B's starts and offsets, staged in LDS by every workgroup of a
+// prepare kernel when both fit (kPrepTable diagonals each).
+struct PrepTables {
+    int64_t sa[kPrepTable], sb[kPrepTable];
+    int32_t oa[kPrepTable], ob[kPrepTable];
+};
+
+// Stages the tables (every lane of the workgroup calls it); true if staged.
+__device__ __forceinline__ bool stage_tables(PrepTables& t, const int32_t* __restrict__ A_off,
+                                             const int64_t* __restrict__ A_starts, int32_t nA,
+                                             const int32_t* __restrict__ B_off,
+                                             const int64_t* __restrict__ B_starts, int32_t nB)
 {
-    __shared__ int64_t sa[kPrepTable], sb[kPrepTable];
-    __shared__ int32_t oa[kPrepTable], ob[kPrepTable];
     const bool staged = nA <= kPrepTable && nB <= kPrepTable;
     if (staged) {
         for (int i = (int)threadIdx.x; i < nA; i += kPrepBlock) {
-            sa[i] = A_starts[i];
-            oa[i] = A_off[i];
+            t.sa[i] = A_starts[i];
+            t.oa[i] = A_off[i];
         }
         for (int i = (int)threadIdx.x; i < nB; i += kPrepBlock) {
-            sb[i] = B_starts[i];
-            ob[i] = B_off[i];
+            t.sb[i] = B_starts[i];
+            t.ob[i] = B_off[i];
         }
         __syncthreads();
     }
-    const int64_t k = (int64_t)blockIdx.x * kPrepBlock + threadIdx.x;
-    if (k >= c_ndiag) return;
+    return staged;
+}
+
+// The records of C diagonal k's entries [pair_ptr[k], pair_ptr[k + 1]) of a
+// plan with c_ndiag diagonals and n_pairs entries; raise(1) for an entry not
+// in the symbolic form or a pair_ptr that is no partition, raise(2) for a B
+// index beyond 2^30 - 1.
+template <typename Raise>
+__device__ __forceinline__ void prepare_diag(
+    int64_t k, int32_t n, const int32_t* __restrict__ A_off, const int64_t* __restrict__ A_starts,
+    int32_t nA, const int32_t* __restrict__ B_off, const int64_t* __restrict__ B_starts, int32_t nB,
+    const int32_t* __restrict__ C_off, const int64_t* __restrict__ pair_ptr, int64_t c_ndiag,
+    const diagpu_gpair* __restrict__ pairs, int64_t n_pairs, int4* __restrict__ records,
+    const PrepTables& t, bool staged, Raise raise)
+{
     const int64_t g0 = pair_ptr[k], g1 = pair_ptr[k + 1];
     if (g0 < 0 || g1 < g0 || g1 > n_pairs || (k == 0 && g0 != 0) ||
         (k == c_ndiag - 1 && g1 != n_pairs)) {
-        flag[0] = 1;   // every writer stores the same value
+        raise(1);
         return;
     }
     const int64_t dc = C_off[k];
@@ -144,11 +162,11 @@ __global__ __launch_bounds__(kPrepBlock) void k_astat_prepare(
     auto absl = [](int64_t x) { return x < 0 ? -x : x; };
     for (int64_t g = g0; g < g1; ++g) {
         const diagpu_gpair p = pairs[g];
-        const int a = find_start(staged ? sa : A_starts, nA, (int64_t)p.ab);
-        const int bi = find_start(staged ? sb : B_starts, nB, (int64_t)p.bb);
+        const int a = find_start(staged ? t.sa : A_starts, nA, (int64_t)p.ab);
+        const int bi = find_start(staged ? t.sb : B_starts, nB, (int64_t)p.bb);
         bool ok = a >= 0 && bi >= 0;
         if (ok) {
-            const int64_t da = staged ? oa[a] : A_off[a], db = staged ? ob[bi] : B_off[bi];
+            const int64_t da = staged ? t.oa[a] : A_off[a], db = staged ? t.ob[bi] : B_off[bi];
             ok = da + db == dc && dc > -(int64_t)n && dc < n &&
                  (int64_t)p.ash == min0(da) - min0(dc) &&
                  (int64_t)p.bsh == da + min0(db) - min0(dc) && (int64_t)p.al == n - absl(da) &&
@@ -159,7 +177,7 @@ __global__ __launch_bounds__(kPrepBlock) void k_astat_prepare(
         const int64_t b = (int64_t)p.bb + p.bsh;
         int4 r = int4{0, 0, 0, 0};
         if (!ok) {
-            flag[0] = 1;
+            raise(1);
         } else if (plo >= phi) {
             // No position holds both operands (an entry of the symbolic form
             // always has one; kept so that no record can read past B): a
@@ -167,12 +185,71 @@ __global__ __launch_bounds__(kPrepBlock) void k_astat_prepare(
             // min(max(p, 1), 0) = 0 reads B[0].
             r = int4{a, 1, 1, 0};
         } else if (b < INT_MIN || b + phi > ((int64_t)1 << 30)) {
-            flag[1] = 1;   // the kernel forms 4 (b + c) in 32 bits
+            raise(2);   // the kernel forms 4 (b + c) in 32 bits
         } else {
             r = int4{a, plo, phi, (int)b};
         }
         records[g] = r;
     }
+}
+
+__global__ __launch_bounds__(kPrepBlock) void k_astat_prepare(
+    int32_t n, const int32_t* __restrict__ A_off, const int64_t* __restrict__ A_starts, int32_t nA,
+    const int32_t* __restrict__ B_off, const int64_t* __restrict__ B_starts, int32_t nB,
+    const int32_t* __restrict__ C_off, const int64_t* __restrict__ pair_ptr, int64_t c_ndiag,
+    const diagpu_gpair* __restrict__ pairs, int64_t n_pairs, int4* __restrict__ records,
+    int32_t* __restrict__ flag)
+{
+    __shared__ PrepTables t;
+    const bool staged = stage_tables(t, A_off, A_starts, nA, B_off, B_starts, nB);
+    const int64_t k = (int64_t)blockIdx.x * kPrepBlock + threadIdx.x;
+    if (k >= c_ndiag) return;
+    // every writer of a flag stores the same value
+    prepare_diag(k, n, A_off, A_starts, nA, B_off, B_starts, nB, C_off, pair_ptr, c_ndiag, pairs,
+                 n_pairs, records, t, staged, [&](int bit) { flag[bit - 1] = 1; });
+}
+
+// The same records built inside the symbolic call
+// (diagpu_spgemm_symbolic_astat) when it takes the multi-launch path (the
+// one-launch kernel writes them with the entries), queued behind that phase
+// on its stream, so one read-back returns both.  The plan's counts come from
+// the phase's state record on the device: state_counts[0] C diagonals,
+// state_counts[2] entries (each bounded by its capacity).  Nothing runs when
+// the phase raised a flag (state_flags[0]: its plan is incomplete).  Errors
+// are ORed into state_flags[1] (zeroed by the symbolic phase): 1 an entry not
+// in the symbolic form, 2 a B index beyond 2^30 - 1.
+// Workgroup 0 also writes the 4 ints after the records, {0, 0, smallest,
+// largest A offset}.
+__global__ __launch_bounds__(kPrepBlock) void k_astat_records(
+    int32_t n, const int32_t* __restrict__ A_off, const int64_t* __restrict__ A_starts, int32_t nA,
+    const int32_t* __restrict__ B_off, const int64_t* __restrict__ B_starts, int32_t nB,
+    const int32_t* __restrict__ C_off, const int64_t* __restrict__ pair_ptr, int64_t c_cap,
+    const diagpu_gpair* __restrict__ pairs, int64_t p_cap, const int64_t* state_counts,
+    int32_t* state_flags, int32_t* __restrict__ records)
+{
+    if (state_flags[0]) return;
+    const int64_t c_ndiag = min(state_counts[0], c_cap);
+    const int64_t n_pairs = min(state_counts[2], p_cap);
+    if (blockIdx.x == 0 && threadIdx.x < 64) {
+        int lo = INT_MAX, hi = INT_MIN;
+        for (int d = (int)threadIdx.x; d < nA; d += 64) {
+            lo = min(lo, A_off[d]);
+            hi = max(hi, A_off[d]);
+        }
+        for (int m = 32; m >= 1; m >>= 1) {
+            lo = min(lo, __shfl_xor(lo, m));
+            hi = max(hi, __shfl_xor(hi, m));
+        }
+        if (threadIdx.x == 0)
+            reinterpret_cast<int4*>(records)[n_pairs] = int4{0, 0, lo, hi};
+    }
+    __shared__ PrepTables t;
+    const bool staged = stage_tables(t, A_off, A_starts, nA, B_off, B_starts, nB);
+    const int64_t k = (int64_t)blockIdx.x * kPrepBlock + threadIdx.x;
+    if (k >= c_ndiag) return;
+    prepare_diag(k, n, A_off, A_starts, nA, B_off, B_starts, nB, C_off, pair_ptr, c_ndiag, pairs,
+                 n_pairs, reinterpret_cast<int4*>(records), t, staged,
+                 [&](int bit) { atomicOr(state_flags + 1, bit); });
 }
 
 // flag[0..1] = 0 (the error flags above); flag[2..3] = the smallest and
@@ -690,6 +767,23 @@ int launch_astat(const char* fn, int32_t n, const int32_t* A_off, const int64_t*
 }
 
 }  // namespace
+
+int launch_astat_records(hipStream_t s, int32_t n, const int32_t* A_off,
+                         const int64_t* A_starts, int32_t nA, const int32_t* B_off,
+                         const int64_t* B_starts, int32_t nB, const int32_t* C_off,
+                         const int64_t* pair_ptr, int64_t c_bound, int64_t c_capacity,
+                         const diagpu_gpair* pairs, int64_t pair_capacity,
+                         const int64_t* state_counts, int32_t* state_flags, int32_t* records)
+{
+    const int64_t c_grid = std::min(c_bound, c_capacity);
+    hipLaunchKernelGGL(k_astat_records,
+                       dim3((unsigned)std::max<int64_t>(1, ceil_div<int64_t>(c_grid, kPrepBlock))),
+                       dim3(kPrepBlock), 0, s, n, A_off, A_starts, nA, B_off, B_starts, nB, C_off,
+                       pair_ptr, c_capacity, pairs, pair_capacity, state_counts, state_flags,
+                       records);
+    return check_launch("diagpu_spgemm_symbolic_astat");
+}
+
 }  // namespace diagpu
 
 extern "C" {

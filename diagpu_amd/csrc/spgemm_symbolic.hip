@@ -43,6 +43,7 @@
 
 #include "common.hpp"
 #include "scan.hpp"
+#include "spgemm_internal.hpp"
 
 namespace diagpu {
 namespace {
@@ -109,7 +110,7 @@ Layout layout_for(int32_t n, int32_t na, int32_t nb)
     L.off_wprefix = o; o = align256(o + sizeof(int32_t) * L.nwords);
     L.off_wsum = o;    o = align256(o + sizeof(int64_t) * L.nwblocks);
     L.off_part = o;    o = align256(o + 2 * sizeof(int64_t) * L.nkblocks);
-    L.off_state = o;   o = align256(o + sizeof(SymState) + sizeof(int32_t) * kMaxFastGroups);
+    L.off_state = o;   o = align256(o + sizeof(SymState) + 2 * sizeof(int32_t) * kMaxFastGroups);
     L.total = o;
     return L;
 }
@@ -415,10 +416,11 @@ __global__ __launch_bounds__(kBlock) void k_pair_fill(
 // exchange their totals once, and each wave then writes its diagonals'
 // starts, pair_ptr and GPairs (slot ranks from the same ballot: B order).
 // Everything a workgroup combines goes through one LDS exchange and one
-// barrier per step (eight in all).  Counts, nnz, useful flops and the
-// operands' value extents are computed by every workgroup and written by
-// workgroup 0; each workgroup writes its largest entry count (wg_max) and
-// the host takes the maximum.  If the structures exceed the LDS budget the
+// barrier per step (eight in all, nine with the A-stationary records).
+// Counts, nnz, useful flops and the operands' value extents are computed by
+// every workgroup and written by workgroup 0; each workgroup writes its
+// largest entry count (wg_max) and, with the records, its flag word (wg_rec),
+// and the host combines them.  If the structures exceed the LDS budget the
 // kernel only raises kFlagFallback.
 // ---------------------------------------------------------------------------
 
@@ -485,7 +487,7 @@ __global__ __launch_bounds__(kFastBlock) void k_sym_fast(
     int32_t* __restrict__ C_off, int32_t* __restrict__ C_len, int64_t* __restrict__ C_starts,
     int64_t c_cap, int64_t* __restrict__ pair_ptr, diagpu_gpair* __restrict__ pairs,
     int64_t p_cap, int32_t* __restrict__ lookup, SymState* __restrict__ st,
-    int32_t* __restrict__ wg_max)
+    int32_t* __restrict__ wg_max, int32_t* __restrict__ records, int32_t* __restrict__ wg_rec)
 {
     extern __shared__ uint32_t lds[];
     __shared__ int32_t s32[8][kFastWaves];        // one slot per combined value
@@ -768,6 +770,8 @@ __global__ __launch_bounds__(kFastBlock) void k_sym_fast(
     if (np > p_cap) flags |= kFlagPairCapacity;
     report(flags, nC, nnz, np, fl);
     if (flags) return;
+    if (records && wg == 0 && tid == 0)   // the 4 ints after the records
+        reinterpret_cast<int4*>(records)[np] = int4{0, 0, amin, amax};
 
     // 4. each wave's run of C diagonals: counts, then one exchange
     const int64_t R = k1 - k0;
@@ -806,7 +810,11 @@ __global__ __launch_bounds__(kFastBlock) void k_sym_fast(
     if (wg == G - 1 && tid == 0) pair_ptr[nC] = np;
 
     // 5. the run's starts, pair_ptr, C offsets and lengths, and GPairs (B
-    //    order within each C diagonal)
+    //    order within each C diagonal); with `records`, each entry's record
+    //    as diagpu_spgemm_astat_prepare forms it ({A index, lo, hi, b}; every
+    //    entry here is in the symbolic form), rflag set for a B index beyond
+    //    2^30 - 1
+    int32_t rflag = 0;
     for (int64_t r = r0; r < r1; ++r) {
         const int64_t k = k0 + r;
         const int dc = rows[r];
@@ -833,10 +841,30 @@ __global__ __launch_bounds__(kFastBlock) void k_sym_fast(
                 g.bsh = (int)da + imin0(db) - minc;
                 g.al = alen[ai];
                 g.bl = blen[b];
-                pairs[slot + __popcll(m & ((1ull << lane) - 1ull))] = g;
+                const int64_t at = slot + __popcll(m & ((1ull << lane) - 1ull));
+                pairs[at] = g;
+                if (records) {
+                    const int plo = i32max(0, i32max(-g.ash, -g.bsh));
+                    const int phi = i32min(g.al - g.ash, g.bl - g.bsh);
+                    const int64_t bq = (int64_t)g.bb + g.bsh;
+                    int4 rec = int4{ai, plo, phi, (int)bq};
+                    if (plo >= phi) {
+                        rec = int4{ai, 1, 1, 0};    // never fires (see k_astat_prepare)
+                    } else if (bq < INT_MIN || bq + phi > ((int64_t)1 << 30)) {
+                        rec = int4{0, 0, 0, 0};
+                        rflag = 1;
+                    }
+                    reinterpret_cast<int4*>(records)[at] = rec;
+                }
             }
             slot += __popcll(m);
         }
+    }
+    if (records) {   // one word per workgroup: the host ORs them
+        rflag = wave_reduce(rflag, i32or);
+        if (lane0) s32[7][wave] = rflag;
+        __syncthreads();
+        if (tid == 0) wg_rec[wg] = combine_waves(s32[7], i32or);
     }
 
     // 6. lookup: every offset of the 2n - 1, grid-stride over all workgroups
@@ -943,9 +971,11 @@ int run_symbolic(
     int64_t* pair_ptr, diagpu_gpair* pairs, int64_t pair_capacity,
     int32_t* c_lookup, bool use_scratch,
     void* workspace, size_t workspace_bytes,
+    int32_t* records, int32_t* records_status,
     diagpu_spgemm_info* info, void* stream)
 {
     if (!info) return fail(DIAGPU_ERR_ARG, "%s: info is NULL", fn);
+    if (records && !records_status) return fail(DIAGPU_ERR_ARG, "%s: records_status is NULL", fn);
     if (n < 1 || n > (1 << 30))
         return fail(DIAGPU_ERR_ARG, "%s: n=%d outside [1, 2^30]", fn, n);
     if (a_ndiag < 0 || b_ndiag < 0 || c_capacity < 0 || pair_capacity < 0)
@@ -993,8 +1023,9 @@ int run_symbolic(
     int32_t* wg_max = reinterpret_cast<int32_t*>(st + 1);   // after the state record
     struct {
         SymState h;
-        int32_t m[kMaxFastGroups];
+        int32_t m[2 * kMaxFastGroups];   // wg_max[0 .. G), then wg_rec[0 .. G)
     } back;
+    int32_t rec_flags = 0;   // the records step's flags (1: form, 2: B index)
     SymState& h = back.h;
     int rc = DIAGPU_OK;
     DrainOnExit drain;
@@ -1014,16 +1045,20 @@ int run_symbolic(
         const int64_t gmax = cu_count() < kMaxFastGroups ? cu_count() : kMaxFastGroups;
         G = G < 1 ? 1 : (G > gmax ? gmax : G);
         drain.armed = use_scratch;
+        // the kernel writes the records itself (with each entry), and one
+        // flag word per workgroup after wg_max
+        int32_t* wg_rec = wg_max + G;
         hipLaunchKernelGGL(k_sym_fast, dim3((unsigned)G), dim3(kFastBlock), kFastLdsBytes, s, n,
                            A_off, A_len, A_starts, a_ndiag, B_off, B_len, B_starts, b_ndiag,
                            C_off, C_len, C_starts, c_capacity, pair_ptr, pairs, pair_capacity,
-                           c_lookup, st, wg_max);
+                           c_lookup, st, wg_max, records, wg_rec);
         rc = check_launch(fn);
         if (rc) return rc;
         // one synchronous, stream-ordered copy: the kernel and everything
         // before it on `s` are complete when it returns (it costs about
         // 9 us less than an asynchronous copy plus a stream synchronisation)
-        rc = check_hip(hipMemcpyWithStream(&back, st, sizeof(SymState) + sizeof(int32_t) * G,
+        const size_t words = (records ? 2 : 1) * (size_t)G;
+        rc = check_hip(hipMemcpyWithStream(&back, st, sizeof(SymState) + sizeof(int32_t) * words,
                                            hipMemcpyDeviceToHost, s), fn);
         if (rc) return rc;
         drain.armed = false;
@@ -1031,6 +1066,8 @@ int run_symbolic(
             int32_t mx = 0;
             for (int64_t g = 0; g < G && !h.flags; ++g) mx = back.m[g] > mx ? back.m[g] : mx;
             h.max_pairs = mx;
+            if (records && !h.flags)
+                for (int64_t g = 0; g < G; ++g) rec_flags |= back.m[G + g] ? 2 : 0;
             done = true;
         }
     }
@@ -1064,9 +1101,16 @@ int run_symbolic(
                            pair_capacity, st);
         rc = check_launch(fn);
         if (rc) return rc;
+        if (records) {
+            rc = launch_astat_records(s, n, A_off, A_starts, a_ndiag, B_off, B_starts, b_ndiag,
+                                      C_off, pair_ptr, c_cap, c_capacity, pairs, pair_capacity,
+                                      &st->c_ndiag, &st->flags, records);
+            if (rc) return rc;
+        }
         rc = check_hip(hipMemcpyWithStream(&h, st, sizeof(h), hipMemcpyDeviceToHost, s), fn);
         if (rc) return rc;
         drain.armed = false;
+        rec_flags = h.pad;
     }
     info->c_ndiag = h.c_ndiag;
     info->c_nnz = h.c_nnz;
@@ -1087,6 +1131,13 @@ int run_symbolic(
     if (h.flags & kFlagPairCapacity || h.n_pairs > pair_capacity)
         return fail(DIAGPU_ERR_CAPACITY, "%s: %lld pairs exceed pair_capacity=%lld", fn,
                     (long long)h.n_pairs, (long long)pair_capacity);
+    if (records) {
+        *records_status =
+            (rec_flags & 1) ? fail(DIAGPU_ERR_ARG,
+                                   "%s: a plan entry is not in the symbolic plan's form", fn)
+            : (rec_flags & 2) ? fail(DIAGPU_ERR_CAPACITY, "%s: B indices beyond 2^30 - 1", fn)
+                              : DIAGPU_OK;
+    }
     return DIAGPU_OK;
 }
 
@@ -1121,7 +1172,26 @@ DIAGPU_API int diagpu_spgemm_symbolic(
     return diagpu::run_symbolic("diagpu_spgemm_symbolic", n, A_off, A_len, A_starts, a_ndiag,
                                 B_off, B_len, B_starts, b_ndiag, C_off, C_len, C_starts,
                                 c_capacity, pair_ptr, pairs, pair_capacity, c_lookup, false,
-                                workspace, workspace_bytes, info, stream);
+                                workspace, workspace_bytes, nullptr, nullptr, info, stream);
+}
+
+DIAGPU_API int diagpu_spgemm_symbolic_astat(
+    int32_t n,
+    const int32_t* A_off, const int32_t* A_len, const int64_t* A_starts, int32_t a_ndiag,
+    const int32_t* B_off, const int32_t* B_len, const int64_t* B_starts, int32_t b_ndiag,
+    int32_t* C_off, int32_t* C_len, int64_t* C_starts, int64_t c_capacity,
+    int64_t* pair_ptr, diagpu_gpair* pairs, int64_t pair_capacity,
+    int32_t* c_lookup,
+    void* workspace, size_t workspace_bytes,
+    int32_t* records, int32_t* records_status,
+    diagpu_spgemm_info* info, void* stream)
+{
+    if (!records)
+        return diagpu::fail(DIAGPU_ERR_ARG, "diagpu_spgemm_symbolic_astat: records is NULL");
+    return diagpu::run_symbolic("diagpu_spgemm_symbolic_astat", n, A_off, A_len, A_starts,
+                                a_ndiag, B_off, B_len, B_starts, b_ndiag, C_off, C_len, C_starts,
+                                c_capacity, pair_ptr, pairs, pair_capacity, c_lookup, false,
+                                workspace, workspace_bytes, records, records_status, info, stream);
 }
 
 DIAGPU_API int diagpu_spgemm_symbolic_noalloc(
@@ -1135,7 +1205,7 @@ DIAGPU_API int diagpu_spgemm_symbolic_noalloc(
     return diagpu::run_symbolic("diagpu_spgemm_symbolic_noalloc", n, A_off, A_len, A_starts,
                                 a_ndiag, B_off, B_len, B_starts, b_ndiag, C_off, C_len, C_starts,
                                 c_capacity, pair_ptr, pairs, pair_capacity, c_lookup, true,
-                                nullptr, 0, info, stream);
+                                nullptr, 0, nullptr, nullptr, info, stream);
 }
 
 }  // extern "C"

@@ -59,6 +59,13 @@ class SpgemmPlan:
                  ("pairs", torch.uint8, self.p_cap * GPAIR_BYTES)]
         if want_lookup:
             parts.append(("lookup", torch.int32, 2 * self.n - 1))
+        # where the A-stationary kernel may take the plan, the symbolic call
+        # also builds that kernel's records (diagpu_spgemm_symbolic_astat):
+        # one stream sync for both
+        self._fused = (4096 <= self.n < 1 << 30 and self.p_cap < 1 << 28
+                       and na <= max(_lib.ASTAT_MAX_A, _lib.ASTAT_MAX_A_C64))
+        if self._fused:
+            parts.append(("records", torch.int32, 4 * self.p_cap + 4))
         esz = {torch.uint8: 1, torch.int32: 4, torch.int64: 8}
         sizes = [-(-cnt * esz[dt] // 256) * 256 for _, dt, cnt in parts]
         self._buf = torch.empty(sum(sizes), dtype=torch.uint8, device=dev)
@@ -72,7 +79,9 @@ class SpgemmPlan:
         self.info = _lib.SpgemmInfo()
         self._band = None
         self._astat = None
-        self._sym_fn = getattr(_lib.load(), "diagpu_spgemm_symbolic")
+        self._rstat = C.c_int32(0)
+        self._sym_fn = getattr(_lib.load(), "diagpu_spgemm_symbolic_astat" if self._fused
+                               else "diagpu_spgemm_symbolic")
         self._sym_args, self._sym_caps, self._sym_ops = None, None, ()
         self.symbolic()
 
@@ -98,8 +107,9 @@ class SpgemmPlan:
 
     def symbolic(self) -> None:
         """(Re)builds the C structure and pair plan from the operands'
-        offsets, lengths and starts (diagpu_spgemm_symbolic; one stream
-        sync)."""
+        offsets, lengths and starts (diagpu_spgemm_symbolic, or
+        diagpu_spgemm_symbolic_astat with the A-stationary records; one
+        stream sync)."""
         self._band = None
         self._astat = None
         A, B = self.A, self.B
@@ -119,11 +129,22 @@ class SpgemmPlan:
                               self._addr("C_off"), self._addr("C_len"), self._addr("C_starts"),
                               self.c_cap, self._addr("ptr"), self._addr("pairs"), self.p_cap,
                               self._addr("lookup"), self._addr("workspace"),
-                              self._parts["workspace"][2], C.byref(self.info))
+                              self._parts["workspace"][2])
+            if self._fused:
+                self._sym_args += (self._addr("records"), C.byref(self._rstat))
+            self._sym_args += (C.byref(self.info),)
             self._sym_caps = (self.c_cap, self.p_cap)
         st = self._sym_fn(*self._sym_args, _stream_handle(self.stream))
         if st:
             _lib.check(st)
+        if self._fused:
+            rs = self._rstat.value
+            if rs == _lib.OK:
+                self._astat = True                # in the records part (viewed on demand)
+            elif rs == _lib.ERR_CAPACITY:
+                self._astat = False           # B indices beyond 2^30: not this kernel
+            else:
+                _lib.check(rs)
 
     # structure views (device tensors) --------------------------------------
     def c_offsets(self) -> torch.Tensor:
@@ -157,7 +178,7 @@ class SpgemmPlan:
         bufs = [self._buf]
         if self._band is not None:
             bufs.append(self._band[0])
-        if self._astat is not None and self._astat is not False:
+        if isinstance(self._astat, torch.Tensor):
             bufs.append(self._astat)
         for t in bufs:
             t.record_stream(stream)
@@ -210,8 +231,13 @@ class SpgemmPlan:
         return 4 * (len(ho) * BAND_ROWS + self.B.offsets.numel() * wb) + 16 * self.info.n_pairs
 
     def astat_records(self) -> torch.Tensor:
-        """Records of diagpu_spgemm_astat_prepare for this plan (computed
-        once; one stream sync); int32 [4 n_pairs + 4]."""
+        """Records of diagpu_spgemm_astat_prepare for this plan; int32
+        [4 n_pairs + 4].  Built by the symbolic call where the kernel may
+        take the plan, else here, once (diagpu_spgemm_astat_prepare, one
+        stream sync; also after `_astat` is reset to None, which makes it
+        check the plan's entries again)."""
+        if self._astat is True:
+            self._astat = self._view("records")[: 4 * self.info.n_pairs + 4]
         if self._astat is None or self._astat is False:
             A = self.A
             rec = torch.empty(4 * self.info.n_pairs + 4, dtype=torch.int32,
@@ -276,6 +302,8 @@ class SpgemmPlan:
             return False
         if self._astat is False:                  # refused before: B indices beyond 2^30
             return False
+        if self._astat is True:                   # built by the symbolic call
+            return True
         try:
             self.astat_records()
         except _lib.DiagpuError as e:
@@ -344,13 +372,14 @@ class SpgemmPlan:
                       _stream_handle(self.stream))
             return
         if kernel == "astat":
-            rec = self.astat_records()
+            rec = (self._addr("records") if self._astat is True
+                   else self.astat_records().data_ptr())
             A = self.A
             _lib.call("diagpu_spgemm_numeric_astat_f32" if dt == torch.float32
                       else "diagpu_spgemm_numeric_astat_c64", self.n, A.offsets.data_ptr(),
                       A.starts.data_ptr(), A.offsets.numel(), A_vals.data_ptr(), B_vals.data_ptr(),
                       self.C_off.data_ptr(), self.C_len.data_ptr(), self.C_starts.data_ptr(),
-                      self.info.c_ndiag, self.ptr.data_ptr(), rec.data_ptr(), self.info.n_pairs,
+                      self.info.c_ndiag, self.ptr.data_ptr(), rec, self.info.n_pairs,
                       C_vals.data_ptr(), _stream_handle(self.stream))
             return
         if kernel == "band":

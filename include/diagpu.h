@@ -380,6 +380,32 @@ DIAGPU_API int diagpu_spgemm_astat_prepare(int32_t n, const int32_t* A_off,
                                            const diagpu_gpair* pairs, int64_t n_pairs,
                                            int32_t* records, void* stream);
 
+/* diagpu_spgemm_symbolic and, in the same call, the records of
+ * diagpu_spgemm_astat_prepare for the plan it builds: one stream
+ * synchronisation for both (the records step runs on the device behind the
+ * symbolic phase and reads its counts there), for callers that build a plan
+ * per product, such as a matrix-power chain.  Same arguments, outputs and
+ * errors as diagpu_spgemm_symbolic, plus records (4 pair_capacity + 4
+ * int32).  When the call returns DIAGPU_OK, records[0 .. 4 n_pairs) hold the
+ * plan's records, records[4 n_pairs .. 4 n_pairs + 3] = {0, 0, smallest,
+ * largest A offset}, and *records_status is what diagpu_spgemm_astat_prepare
+ * would return for the plan: DIAGPU_OK, or DIAGPU_ERR_CAPACITY if a B index
+ * exceeds 2^30 - 1 (the records are then unusable; the plan is complete and
+ * the other numeric entry points take it), DIAGPU_ERR_ARG if an entry fails
+ * the prepare step's check (not expected of the plans this call builds);
+ * diagpu_last_error() describes a non-zero *records_status.  No reference
+ * counterpart. */
+DIAGPU_API int diagpu_spgemm_symbolic_astat(
+    int32_t n,
+    const int32_t* A_off, const int32_t* A_len, const int64_t* A_starts, int32_t a_ndiag,
+    const int32_t* B_off, const int32_t* B_len, const int64_t* B_starts, int32_t b_ndiag,
+    int32_t* C_off, int32_t* C_len, int64_t* C_starts, int64_t c_capacity,
+    int64_t* pair_ptr, diagpu_gpair* pairs, int64_t pair_capacity,
+    int32_t* c_lookup,
+    void* workspace, size_t workspace_bytes,
+    int32_t* records, int32_t* records_status,
+    diagpu_spgemm_info* info, void* stream);
+
 /* The numeric phase of diagpu_spgemm_numeric_f32 (same C, bit for bit) with
  * each workgroup holding one block of 64 R rows of every A diagonal (plus the
  * 32 rows before it; R = 4, 8 or 16 rows per lane, chosen per launch) in LDS

@@ -278,11 +278,29 @@ public:
         size_t ws_bytes = 0;
         check(diagpu_spgemm_symbolic_workspace(n, a_ndiag, b_ndiag, &ws_bytes));
         DeviceArray<char> ws(ws_bytes);
-        check(diagpu_spgemm_symbolic(n, dA_off, dA_len, dA_starts, a_ndiag, dB_off, dB_len, dB_starts,
-                                     b_ndiag, C_off_.data(), C_len_.data(), C_starts_.data(), ccap,
-                                     ptr_.data(), pairs_.data(), pcap,
-                                     want_lookup ? lookup_.data() : nullptr, ws.data(), ws_bytes,
-                                     &info_, stream));
+        // Where the A-stationary kernel may take the plan, the symbolic call
+        // also builds its records (diagpu_spgemm_symbolic_astat: one stream
+        // synchronisation for both).
+        const bool fused = int64_t(n) >= 4096 && int64_t(n) < (int64_t(1) << 30) &&
+                           pcap < (int64_t(1) << 28) &&
+                           a_ndiag <= std::max(DIAGPU_ASTAT_MAX_A, DIAGPU_ASTAT_MAX_A_C64);
+        int32_t rstat = DIAGPU_OK;
+        if (fused) {
+            records_.resize(size_t(4 * pcap + 4));
+            check(diagpu_spgemm_symbolic_astat(
+                n, dA_off, dA_len, dA_starts, a_ndiag, dB_off, dB_len, dB_starts, b_ndiag,
+                C_off_.data(), C_len_.data(), C_starts_.data(), ccap, ptr_.data(), pairs_.data(),
+                pcap, want_lookup ? lookup_.data() : nullptr, ws.data(), ws_bytes,
+                records_.data(), &rstat, &info_, stream));
+            if (rstat != DIAGPU_OK && rstat != DIAGPU_ERR_CAPACITY) check(rstat);
+            astat_prepared_ = rstat == DIAGPU_OK;
+        } else {
+            check(diagpu_spgemm_symbolic(n, dA_off, dA_len, dA_starts, a_ndiag, dB_off, dB_len,
+                                         dB_starts, b_ndiag, C_off_.data(), C_len_.data(),
+                                         C_starts_.data(), ccap, ptr_.data(), pairs_.data(), pcap,
+                                         want_lookup ? lookup_.data() : nullptr, ws.data(),
+                                         ws_bytes, &info_, stream));
+        }
         nA_ = a_ndiag;
         nB_ = b_ndiag;
         A_off_.resize(a_ndiag);
@@ -310,7 +328,9 @@ public:
         astat_auto_ = !uses_band() && sized && na <= DIAGPU_ASTAT_MAX_A && !thin_mid;
         astat_auto_c64_ = sized && na <= DIAGPU_ASTAT_MAX_A_C64 &&
                           (int64_t(n) >= (1 << 16) || np >= 3 * na);
-        if (astat_auto_ || astat_auto_c64_) {
+        if (fused && rstat == DIAGPU_ERR_CAPACITY) {   // B indices beyond 2^30
+            astat_auto_ = astat_auto_c64_ = false;
+        } else if ((astat_auto_ || astat_auto_c64_) && !astat_prepared_) {
             try {
                 prepare_astat(stream);
             } catch (const Error& e) {

@@ -91,6 +91,19 @@ def test_spgemm_argument_errors():
     bad = list(args); bad[18] = 16
     assert lib.diagpu_spgemm_symbolic(*bad) == _lib.ERR_CAPACITY
     assert b"workspace" in lib.diagpu_last_error()
+    # the same call with the A-stationary records: both records pointers are
+    # required, and the symbolic checks come before any HIP call
+    rstat = C.c_int32(-1)
+    fused = args[:19] + [fake, C.byref(rstat)] + args[19:]
+    bad = list(fused); bad[19] = None
+    assert lib.diagpu_spgemm_symbolic_astat(*bad) == _lib.ERR_ARG
+    assert b"records" in lib.diagpu_last_error()
+    bad = list(fused); bad[20] = None
+    assert lib.diagpu_spgemm_symbolic_astat(*bad) == _lib.ERR_ARG
+    assert b"records_status" in lib.diagpu_last_error()
+    bad = list(fused); bad[18] = 16
+    assert lib.diagpu_spgemm_symbolic_astat(*bad) == _lib.ERR_CAPACITY
+    assert rstat.value == -1                  # untouched when the symbolic phase fails
     # numeric
     assert lib.diagpu_spgemm_numeric_f32(0, fake, fake, fake, fake, fake, 1, fake, fake, 1,
                                          fake, None) == _lib.ERR_ARG

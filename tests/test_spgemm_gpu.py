@@ -692,6 +692,74 @@ def test_astat_prepare_b_index_bound(dev):
             assert not plan.uses_astat()
 
 
+@pytest.mark.parametrize("case", ["stencil", "band", "random", "wide_a", "wide_b"])
+def test_symbolic_astat_records_match_prepare(dev, case):
+    """diagpu_spgemm_symbolic_astat builds, inside the symbolic call, the
+    records and the 4-int tail that diagpu_spgemm_astat_prepare writes for
+    the same plan, on the one-launch symbolic path and on the multi-launch
+    path (the wide cases), and the A-stationary product from them has the
+    gather's bits."""
+    rng = np.random.default_rng(91)
+    if case == "stencil":
+        n, oa, ob = 1 << 20, list(range(-4, 5)), [-16384, -128, -1, 0, 1, 128, 16384]
+    elif case == "band":
+        n, oa, ob = 5000, list(range(-10, 11)), list(range(-10, 11))
+    elif case == "random":
+        n = 70000
+        oa = rng.choice(np.arange(-4096, 4097), size=128, replace=False)
+        ob = rng.choice(np.arange(-4096, 4097), size=40, replace=False)
+    elif case == "wide_a":
+        n, oa, ob = 600_000, [-599_999, 0, 599_999], [-599_999, -1, 2, 599_999]
+    else:
+        n = (1 << 22) + 3
+        oa, ob = [-(1 << 22) - 2, -5, 0, 7, (1 << 22) + 2], [-3, 0, 1, (1 << 21)]
+    A = workloads.hm_random(n, oa, seed=92, device=dev)
+    B = workloads.hm_random(n, ob, seed=93, device=dev)
+    plan = SpgemmPlan(A, B)
+    assert plan._fused and plan._astat is True    # built by the symbolic call
+    fused = plan.astat_records().clone()
+    assert fused.numel() == 4 * plan.info.n_pairs + 4
+    plan._astat = None                       # the separate prepare step, on the same plan
+    sep = plan.astat_records().clone()
+    assert torch.equal(fused, sep), case
+    plan._astat = fused
+    Cg = plan.multiply(A.values, B.values, kernel="gather")
+    Ca = plan.multiply(A.values, B.values, kernel="astat")
+    assert torch.equal(Cg.view(torch.int32), Ca.view(torch.int32)), case
+
+
+def test_symbolic_astat_records_b_index_bound(dev):
+    """The records step inside the symbolic call applies the prepare step's
+    2^30 bound on B indices: with B's starts moved so that the largest b + hi
+    is 2^30 the plan's records are those of the unmoved plan with b moved;
+    one index further the call still returns the plan (DIAGPU_OK) but reports
+    DIAGPU_ERR_CAPACITY for the records, so the automatic choice skips the
+    A-stationary kernel and forcing it raises that error."""
+    from diagpu_amd.workloads import HM
+    n = 5000
+    A = workloads.hm_random(n, [-9, -4, 0, 3, 11], 94, dev)
+    B = workloads.hm_random(n, [-30, -1, 0, 2, 7, 40], 95, dev)
+    plan0 = SpgemmPlan(A, B)
+    rec = plan0.astat_records().cpu().numpy().astype(np.int64)
+    body = rec[: 4 * plan0.info.n_pairs].reshape(-1, 4)
+    top = int((body[:, 3] + body[:, 2]).max())
+    for shift, ok in ((2**30 - top, True), (2**30 - top + 1, False)):
+        Bs = HM(n, B.offsets, B.lengths, B.starts + shift, B.values, None)
+        plan = SpgemmPlan(A, Bs)
+        assert plan.info.n_pairs == plan0.info.n_pairs
+        if ok:
+            got = plan.astat_records().cpu().numpy().astype(np.int64)
+            gb = got[: 4 * plan.info.n_pairs].reshape(-1, 4)
+            assert np.array_equal(gb[:, :3], body[:, :3])
+            assert np.array_equal(gb[:, 3], body[:, 3] + shift)
+            assert np.array_equal(got[-4:], rec[-4:])
+        else:
+            assert plan._astat is False and not plan.uses_astat()
+            with pytest.raises(_lib.DiagpuError) as e:
+                plan.astat_records()
+            assert e.value.status == _lib.ERR_CAPACITY and "2^30" in str(e.value)
+
+
 def _drop_diagonals(plan, empty):
     """Remove every plan entry of the C diagonals `empty` (their pair_ptr
     ranges become empty); returns the kept entries' mask."""
