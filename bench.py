@@ -19,6 +19,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -536,16 +537,20 @@ def time_spgemm(cfg: int, seed: int, reps: int, complex_values: bool = False,
     torch.cuda.synchronize()
     sym_wall_ms = (time.perf_counter() - t0) * 1e3
     # symbolic phase: a synchronous call (it returns with the counts on the
-    # host), timed as a caller waits for it, 20 calls; beside it the HIP-event
-    # span of 3 calls on the stream (which also counts the idle stream while
-    # each call's launch travels from the host)
+    # host), timed as a caller waits for it, 20 calls each timed (median;
+    # the mean beside it); beside them the HIP-event span of 3 calls on the
+    # stream (which also counts the idle stream while each call's launch
+    # travels from the host)
     for _ in range(2):
         plan.symbolic()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
+    sym_calls = []
     for _ in range(20):
+        t0 = time.perf_counter()
         plan.symbolic()
-    sym_ms = (time.perf_counter() - t0) * 1e3 / 20
+        sym_calls.append((time.perf_counter() - t0) * 1e3)
+    sym_ms = statistics.median(sym_calls)
+    sym_mean_ms = statistics.fmean(sym_calls)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for _ in range(3):
@@ -572,7 +577,8 @@ def time_spgemm(cfg: int, seed: int, reps: int, complex_values: bool = False,
         "C_nnz": plan.info.c_nnz, "numeric_ms": round(ms, 5),
         "numeric_min_ms": auto["min_ms"], "numeric_max_ms": auto["max_ms"],
         "kernel": kern,
-        "symbolic_ms": round(sym_ms, 5), "symbolic_event_span_ms": round(sym_ev_ms, 5),
+        "symbolic_ms": round(sym_ms, 5), "symbolic_mean_ms": round(sym_mean_ms, 5),
+        "symbolic_event_span_ms": round(sym_ev_ms, 5),
         "symbolic_wall_ms_first": round(sym_wall_ms, 3),
         "GFLOPs": round(flops / (ms * 1e6), 1), "useful_flops": flops,
         "GBs": round(alg / (ms * 1e6), 1), "frac_hbm": round(alg / (ms * 1e6) / HBM_PEAK_GBS, 4),
@@ -607,20 +613,24 @@ def time_spgemm_banded(reps: int, cpu_seconds: float):
                        name=f"spgemm_make_banded_n{n}_w{w}")
 
 
-def time_taylor(order: int = 6, t: float = 0.05):
+def time_taylor(order: int = 6, t: float = 0.05, chains: int = 9):
     """Taylor chain exp(tH) ~ sum_k (tH)^k/k! on the 7-point stencil of SpGEMM
-    config 4 (n = 2^20): one warm-up chain, one timed chain as a caller runs
-    it (total_ms), then one chain whose phases are stream-synchronised for
-    the split (the plan of every product is built on the device)."""
+    config 4 (n = 2^20): one warm-up chain, then `chains` chains each timed
+    as a caller runs it (total_ms: their median), then one chain whose
+    phases are stream-synchronised for the split (the plan of every product
+    is built on the device)."""
     import torch
     from diagpu_amd import chain, workloads
     H = workloads.hm_stencil7(128, 128, 64, device="cuda")
     chain.taylor_expm(H, t, order)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    chain.taylor_expm(H, t, order)
-    torch.cuda.synchronize()
-    total = time.perf_counter() - t0
+    times = []
+    for _ in range(chains):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        chain.taylor_expm(H, t, order)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    total = statistics.median(times)
     st = chain.ChainStats()
     t0 = time.perf_counter()
     S = chain.taylor_expm(H, t, order, st)
@@ -634,7 +644,8 @@ def time_taylor(order: int = 6, t: float = 0.05):
     flops = sum(st.useful_flops)
     return {"workload": "taylor_expm_stencil7_cfg4", "n": H.n, "order": order, "t": t,
             "S_diags": S.ndiag, "S_nnz": S.nnz, "total_ms": round(total * 1e3, 3),
-            "total_ms_phase_synced": round(total_split * 1e3, 3),
+            "total_min_ms": round(min(times) * 1e3, 3), "total_max_ms": round(max(times) * 1e3, 3),
+            "chains": chains, "total_ms_phase_synced": round(total_split * 1e3, 3),
             "symbolic_ms": round(sum(st.symbolic) * 1e3, 3),
             "numeric_ms": round(sum(st.numeric) * 1e3, 3),
             "axpby_ms": round(sum(st.axpby) * 1e3, 3),

@@ -152,6 +152,12 @@ PROTOTYPES: dict[str, tuple] = {
                                                   _i64, _vp, _vp, _i64, _vp, _vp]),
     "diagpu_spgemm_numeric_astat_c64": (C.c_int, [_i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp,
                                                   _i64, _vp, _vp, _i64, _vp, _vp]),
+    "diagpu_spgemm_numeric_astat_scaled_f32": (C.c_int, [
+        _i32, _vp, _vp, _i32, _vp, C.c_float, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64,
+        C.c_float, _vp, _vp]),
+    "diagpu_spgemm_numeric_astat_scaled_c64": (C.c_int, [
+        _i32, _vp, _vp, _i32, _vp, Complex64, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64,
+        Complex64, _vp, _vp]),
 }
 
 # diagpu.h: DIAGPU_ASTAT_MAX_A, DIAGPU_ASTAT_MAX_A_C64, DIAGPU_SYMBOLIC_SCRATCH_BYTES

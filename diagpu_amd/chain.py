@@ -7,7 +7,11 @@ Every product builds its C structure and pair plan on the GPU
 (diagpu_spgemm_symbolic; one stream sync returns the counts) and fills C with
 diagpu_spgemm_numeric_f32 (or _c64).  Sums and scalings use
 diagpu_dia_axpby_f32 (or _c64) over the union of the operands' diagonals; the
-union itself is a merge of two short sorted offset lists on the host.  Values
+union itself is a merge of two short sorted offset lists on the host.  A
+Taylor step I + ((t/j) H) S whose plan the A-stationary kernel takes is one
+fused product instead (diagpu_spgemm_numeric_astat_scaled_*: H scaled in
+LDS, I added to the main diagonal's sums), with no scaling pass over H and
+no identity pass over the product.  Values
 are float32 or complex64; a complex factor or operand makes the result
 complex (propagator(H, dt, order) builds exp(-i dt H), and to_recon hands it
 to the SpMV path).
@@ -302,10 +306,65 @@ def taylor_expm(H: HM, t, order: int, stats: ChainStats | None = None) -> HM:
     if stats is None:
         return _taylor_steps(H, t, order, S)
     for j in range(order - 1, 0, -1):
-        Hj = _timed(ax, axpby, t / j, H, 0.0, None)
-        S = multiply(Hj, S, stats) if _narrow_first(Hj) else multiply(S, Hj, stats)
-        S = _timed(ax, add_identity, S)
+        S = _horner_step_synced(H, t / j, S, stats)
     return S
+
+
+def _has_main(H: HM, S: HM) -> bool:
+    """Whether H S has a main diagonal: an offset of H has its negation in S."""
+    hs = set(_host_offsets(S))
+    return any(-d in hs for d in _host_offsets(H))
+
+
+def _fused(plan: SpgemmPlan, H: HM) -> bool:
+    """Whether a Horner step whose plan has H as its A operand runs as one
+    fused product (SpgemmPlan.numeric_scaled): the A-stationary kernel takes
+    the plan."""
+    return plan.kernel_for(H.values.dtype) == "astat"
+
+
+def _horner_step_synced(H: HM, alpha, S: HM, stats: ChainStats) -> HM:
+    """I + (alpha H) S with each phase stream-synchronised into `stats`:
+    the plan (symbolic), the product (numeric; fused with the scaling and
+    the identity where _fused) and, unfused, the scaling and identity add
+    (axpby)."""
+    narrow = _narrow_first(H)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    plan = SpgemmPlan(H, S) if narrow else SpgemmPlan(S, H)
+    fused = narrow and _fused(plan, H)   # the kernel's set-up belongs to the plan
+    inf = plan.info
+    C = HM(H.n, plan.c_offsets(), plan.c_lengths(), plan.c_starts(),
+           _c_values(inf.c_nnz, H.values))
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    if fused:
+        sigma = 1.0 if _has_main(H, S) else 0.0
+        if inf.c_ndiag:
+            plan.numeric_scaled(H.values, S.values, C.values, alpha, sigma)
+        C.host_offsets = _sumset(H.n, _host_offsets(H), _host_offsets(S))   # while it runs
+        torch.cuda.synchronize()
+        stats.numeric.append(time.perf_counter() - t1)
+        if not sigma:
+            C = _timed(stats.axpby, add_identity, C)
+    else:
+        Hj = _timed(stats.axpby, axpby, alpha, H, 0.0, None)   # H's structure: the plan's
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        if inf.c_ndiag:
+            if narrow:
+                plan.numeric(Hj.values, S.values, C.values)
+            else:
+                plan.numeric(S.values, Hj.values, C.values)
+        C.host_offsets = _sumset(H.n, _host_offsets(H), _host_offsets(S))   # while it runs
+        torch.cuda.synchronize()
+        stats.numeric.append(time.perf_counter() - t2)
+        C = _timed(stats.axpby, add_identity, C)
+    stats.symbolic.append(t1 - t0)
+    stats.c_ndiag.append(inf.c_ndiag)
+    stats.n_pairs.append(inf.n_pairs)
+    stats.useful_flops.append(inf.useful_flops)
+    return C
 
 
 # A stream per device for building plans beside the products (default
@@ -331,20 +390,31 @@ def _taylor_steps(H: HM, t, order: int, S: HM) -> HM:
     main = torch.cuda.current_stream(H.values.device)
     side = _side_stream(H.values.device)
     side.wait_stream(main)                      # S's structure, H's values
+    narrow = _narrow_first(H)
     for j in range(order - 1, 0, -1):
-        Hj = axpby(t / j, H, 0.0, None)
-        A, B = (Hj, S) if _narrow_first(Hj) else (S, Hj)
+        # the plan needs the operands' structure only: H's is (t/j) H's
         with torch.cuda.stream(side):
-            plan = SpgemmPlan(A, B, stream=side)
-            plan.prepare(A.values.dtype)
+            plan = SpgemmPlan(H, S, stream=side) if narrow else SpgemmPlan(S, H, stream=side)
+            fused = narrow and _fused(plan, H)   # the kernel's set-up, on the side stream
         plan.hand_over(main)
         inf = plan.info
-        C = HM(A.n, plan.c_offsets(), plan.c_lengths(), plan.c_starts(),
-               _c_values(inf.c_nnz, A.values))
-        if inf.c_ndiag:
-            plan.numeric(A.values, B.values, C.values)
-        C.host_offsets = _sumset(A.n, _host_offsets(A), _host_offsets(B))   # while the product runs
-        S = add_identity(C)
+        C = HM(H.n, plan.c_offsets(), plan.c_lengths(), plan.c_starts(),
+               _c_values(inf.c_nnz, H.values))
+        if fused:
+            # one pass: (t/j) H scaled in LDS, I added to the main diagonal
+            sigma = 1.0 if _has_main(H, S) else 0.0
+            if inf.c_ndiag:
+                plan.numeric_scaled(H.values, S.values, C.values, t / j, sigma)
+        else:
+            Hj = axpby(t / j, H, 0.0, None)
+            if inf.c_ndiag:
+                if narrow:
+                    plan.numeric(Hj.values, S.values, C.values)
+                else:
+                    plan.numeric(S.values, Hj.values, C.values)
+            sigma = 0.0
+        C.host_offsets = _sumset(H.n, _host_offsets(H), _host_offsets(S))   # while the product runs
+        S = C if sigma else add_identity(C)
         if S.offsets is not C.offsets:
             side.wait_stream(main)              # a new structure, written on main
     return S

@@ -32,6 +32,20 @@ __device__ __forceinline__ cf32 mad(cf32 acc, float a, cf32 x)
     return r;
 }
 
+// alpha * x rounded once per real part (fp32: one multiply; complex: each
+// part one fused multiply-add over the other product, written out so that
+// no compiler contraction choice changes it)
+__device__ __forceinline__ float scale_(float a, float x) { return a * x; }
+__device__ __forceinline__ cf32 scale_(cf32 a, cf32 x)
+{
+    cf32 r;
+    r.re = fma_(a.re, x.re, -(a.im * x.im));
+    r.im = fma_(a.re, x.im, a.im * x.re);
+    return r;
+}
+__device__ __forceinline__ float add_(float a, float b) { return a + b; }
+__device__ __forceinline__ cf32 add_(cf32 a, cf32 b) { return cf32{a.re + b.re, a.im + b.im}; }
+
 __device__ __forceinline__ float sel(bool c, float a, float b) { return c ? a : b; }
 __device__ __forceinline__ double sel(bool c, double a, double b) { return c ? a : b; }
 __device__ __forceinline__ cf32 sel(bool c, cf32 a, cf32 b)

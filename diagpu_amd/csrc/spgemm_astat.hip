@@ -349,14 +349,18 @@ __device__ __forceinline__ void store_c(T* cd, int pb, int len, const T (&acc)[R
 // (for waves that walk many diagonals).  tail5: the last block also takes
 // the rows the line-aligned shift leaves after it, R + 1 rows per lane (else
 // one more block of at most kLead - 1 rows per diagonal covers them).
-template <typename T, bool Prefetch, int R, bool Quad = false>
+// Epi: C = (alpha A) B + sigma I -- the staged A rows are scaled in LDS
+// (scale_, once per staged element, before any term reads them), so the
+// terms are those of the plain kernel on the operand alpha A, and sigma is
+// added to the main diagonal's sums before they are stored.
+template <typename T, bool Prefetch, int R, bool Quad = false, bool Epi = false>
 __global__ __launch_bounds__(64 * kWaves) void k_astat(
     int32_t n, const int32_t* __restrict__ A_off, const int64_t* __restrict__ A_starts, int32_t nA,
     const T* __restrict__ Av, const T* __restrict__ Bv, const int32_t* __restrict__ C_off,
     const int32_t* __restrict__ C_len, const int64_t* __restrict__ C_starts, int32_t nC,
     const int64_t* __restrict__ pair_ptr, const int4* __restrict__ records,
     const int32_t* __restrict__ aext, T* __restrict__ Cv, int32_t blocks, int32_t groups,
-    int32_t per_xcd, int32_t tail5)
+    int32_t per_xcd, int32_t tail5, T alpha, T sigma)
 {
     // A's smallest and largest offset (written by diagpu_spgemm_astat_prepare
     // after the records)
@@ -404,6 +408,11 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
     }
     __builtin_amdgcn_s_waitcnt(0);   // this wave's direct loads have landed in LDS
     __syncthreads();
+    if constexpr (Epi) {
+        T* A_s = reinterpret_cast<T*>(A_l);
+        for (int e = r; e < nA * kStage; e += 64 * nw) A_s[e] = scale_(alpha, A_s[e]);
+        __syncthreads();
+    }
 
     // RR rows per lane: R, and with tail5 R + 1 in the last block, whose
     // staged window also holds the rows [i0 + kRB - s, n) that no later block
@@ -556,6 +565,11 @@ __global__ __launch_bounds__(64 * kWaves) void k_astat(
                 walk(std::true_type{});
             else
                 walk(std::false_type{});
+            if constexpr (Epi) {
+                if (dc == 0)
+#pragma unroll
+                    for (int j = 0; j < RR; ++j) acc[j] = add_(acc[j], sigma);
+            }
             store_c<T, RR, Quad>(Cv + cst, pb, len, acc);
         }
     };
@@ -613,7 +627,7 @@ int launch_rows(const char* fn, int32_t n, const int32_t* A_off, const int64_t* 
                 int32_t nA, const T* A_vals, const T* B_vals, const int32_t* C_off,
                 const int32_t* C_len, const int64_t* C_starts, int64_t c_ndiag,
                 const int64_t* pair_ptr, const int32_t* records, int64_t n_pairs, T* C_vals,
-                void* stream)
+                void* stream, bool epi, T alpha, T sigma)
 {
     constexpr int kRB = Astat<T, R>::kRB, kLead = Astat<T, R>::kLead, kStage = Astat<T, R>::kStage;
     constexpr int kMax = Astat<T, R>::kMax;
@@ -675,23 +689,25 @@ int launch_rows(const char* fn, int32_t n, const int32_t* A_off, const int64_t* 
     const dim3 grid((unsigned)(per_xcd * kNumXcd)), block(64 * W);
     const int4* rec = reinterpret_cast<const int4*>(records);
     const int32_t* aext = records + 4 * n_pairs + 2;
-    auto go = [&](auto pf, auto qd) {
+    auto go3 = [&](auto pf, auto qd, auto ep) {
         constexpr bool kPf = decltype(pf)::value, kQd = decltype(qd)::value;
+        constexpr bool kEp = decltype(ep)::value;
         // more than 64 KiB of dynamic LDS must be allowed explicitly
         const int st = check_hip(
-            hipFuncSetAttribute((const void*)k_astat<T, kPf, R, kQd>,
+            hipFuncSetAttribute((const void*)k_astat<T, kPf, R, kQd, kEp>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
                                 kStage * kMax * (int)sizeof(T)),
             fn);
         if (st) return st;
-        hipLaunchKernelGGL((k_astat<T, kPf, R, kQd>), grid, block, lds, as_stream(stream), n, A_off,
-                           A_starts, nA, A_vals, B_vals, C_off, C_len, C_starts, (int32_t)c_ndiag,
-                           pair_ptr, rec, aext, C_vals, (int32_t)blocks, (int32_t)groups, per_xcd,
-                           tail5);
+        hipLaunchKernelGGL((k_astat<T, kPf, R, kQd, kEp>), grid, block, lds, as_stream(stream), n,
+                           A_off, A_starts, nA, A_vals, B_vals, C_off, C_len, C_starts,
+                           (int32_t)c_ndiag, pair_ptr, rec, aext, C_vals, (int32_t)blocks,
+                           (int32_t)groups, per_xcd, tail5, alpha, sigma);
         return check_launch(fn);
     };
     using yes = std::true_type;
     using no = std::false_type;
+    auto go = [&](auto pf, auto qd) { return epi ? go3(pf, qd, yes{}) : go3(pf, qd, no{}); };
     if constexpr (sizeof(T) == 4 && R == 4) {
         if (quad) return prefetch ? go(yes{}, yes{}) : go(no{}, yes{});
     }
@@ -703,7 +719,7 @@ int launch_astat(const char* fn, int32_t n, const int32_t* A_off, const int64_t*
                  int32_t nA, const T* A_vals, const T* B_vals, const int32_t* C_off,
                  const int32_t* C_len, const int64_t* C_starts, int64_t c_ndiag,
                  const int64_t* pair_ptr, const int32_t* records, int64_t n_pairs, T* C_vals,
-                 void* stream)
+                 void* stream, bool epi = false, T alpha = T{}, T sigma = T{})
 {
     constexpr int kMax = astat_cap<T>();
     // the kernel addresses metadata and records by 32-bit byte offsets
@@ -721,7 +737,7 @@ int launch_astat(const char* fn, int32_t n, const int32_t* A_off, const int64_t*
         return fail(DIAGPU_ERR_ARG, "%s: a pointer is NULL", fn);
 #define DIAGPU_ASTAT_LAUNCH(RV)                                                                   \
     launch_rows<T, RV>(fn, n, A_off, A_starts, nA, A_vals, B_vals, C_off, C_len, C_starts, c_ndiag, \
-                       pair_ptr, records, n_pairs, C_vals, stream)
+                       pair_ptr, records, n_pairs, C_vals, stream, epi, alpha, sigma)
     // Rows per lane.  A wave's time per C diagonal is a chain of dependent
     // loads; longer blocks put more rows into each chain and need fewer
     // rounds of workgroups, where n gives at least 4 rounds of them.
@@ -854,6 +870,33 @@ DIAGPU_API int diagpu_spgemm_numeric_astat_c64(
                                       reinterpret_cast<const cf32*>(B_vals), C_off, C_len,
                                       C_starts, c_ndiag, pair_ptr, records, n_pairs,
                                       reinterpret_cast<cf32*>(C_vals), stream);
+}
+
+DIAGPU_API int diagpu_spgemm_numeric_astat_scaled_f32(
+    int32_t n, const int32_t* A_off, const int64_t* A_starts, int32_t nA, const float* A_vals,
+    float alpha, const float* B_vals, const int32_t* C_off, const int32_t* C_len,
+    const int64_t* C_starts, int64_t c_ndiag, const int64_t* pair_ptr, const int32_t* records,
+    int64_t n_pairs, float sigma, float* C_vals, void* stream)
+{
+    return diagpu::launch_astat<float>("diagpu_spgemm_numeric_astat_scaled_f32", n, A_off,
+                                       A_starts, nA, A_vals, B_vals, C_off, C_len, C_starts,
+                                       c_ndiag, pair_ptr, records, n_pairs, C_vals, stream, true,
+                                       alpha, sigma);
+}
+
+DIAGPU_API int diagpu_spgemm_numeric_astat_scaled_c64(
+    int32_t n, const int32_t* A_off, const int64_t* A_starts, int32_t nA,
+    const diagpu_complex64* A_vals, diagpu_complex64 alpha, const diagpu_complex64* B_vals,
+    const int32_t* C_off, const int32_t* C_len, const int64_t* C_starts, int64_t c_ndiag,
+    const int64_t* pair_ptr, const int32_t* records, int64_t n_pairs, diagpu_complex64 sigma,
+    diagpu_complex64* C_vals, void* stream)
+{
+    using diagpu::cf32;
+    return diagpu::launch_astat<cf32>(
+        "diagpu_spgemm_numeric_astat_scaled_c64", n, A_off, A_starts, nA,
+        reinterpret_cast<const cf32*>(A_vals), reinterpret_cast<const cf32*>(B_vals), C_off, C_len,
+        C_starts, c_ndiag, pair_ptr, records, n_pairs, reinterpret_cast<cf32*>(C_vals), stream,
+        true, cf32{alpha.re, alpha.im}, cf32{sigma.re, sigma.im});
 }
 
 }  // extern "C"

@@ -400,6 +400,41 @@ class SpgemmPlan:
         if st:
             _lib.check(st)
 
+    def numeric_scaled(self, A_vals: torch.Tensor, B_vals: torch.Tensor, C_vals: torch.Tensor,
+                       alpha, sigma=0.0) -> None:
+        """C = (alpha A) B + sigma I in one pass on the A-stationary kernel
+        (diagpu_spgemm_numeric_astat_scaled_f32 / _c64): A scaled in LDS,
+        sigma added to C's main diagonal (none where C has no main
+        diagonal).  fp32: the bits of numeric() on the operand fl(alpha A)
+        plus fl(c + sigma) on the main diagonal.  Only for plans the
+        automatic choice runs on that kernel (kernel_for(dtype) ==
+        "astat"); ValueError otherwise."""
+        dt = A_vals.dtype
+        if dt not in (torch.float32, torch.complex64):
+            raise TypeError(f"unsupported value dtype {dt}")
+        for t, nm in ((A_vals, "A_vals"), (B_vals, "B_vals"), (C_vals, "C_vals")):
+            _check_dev(t, dt, nm)
+        inf = self.info
+        if A_vals.numel() < inf.a_extent or B_vals.numel() < inf.b_extent:
+            raise ValueError(f"A_vals / B_vals hold {A_vals.numel()} / {B_vals.numel()} values; "
+                             f"the plan's operands need {inf.a_extent} / {inf.b_extent}")
+        if C_vals.numel() < inf.c_nnz:
+            raise ValueError(f"C_vals has {C_vals.numel()} elements, needs {inf.c_nnz}")
+        if self.kernel_for(dt) != "astat":
+            raise ValueError("numeric_scaled: the A-stationary kernel does not take this plan")
+        rec = self._addr("records") if self._astat is True else self._astat.data_ptr()
+        A = self.A
+        if dt == torch.float32:
+            name, a, s = "diagpu_spgemm_numeric_astat_scaled_f32", float(alpha), float(sigma)
+        else:
+            za, zs = complex(alpha), complex(sigma)
+            name = "diagpu_spgemm_numeric_astat_scaled_c64"
+            a, s = _lib.Complex64(za.real, za.imag), _lib.Complex64(zs.real, zs.imag)
+        _lib.call(name, self.n, A.offsets.data_ptr(), A.starts.data_ptr(), A.offsets.numel(),
+                  A_vals.data_ptr(), a, B_vals.data_ptr(), self._addr("C_off"),
+                  self._addr("C_len"), self._addr("C_starts"), inf.c_ndiag, self._addr("ptr"),
+                  rec, inf.n_pairs, s, C_vals.data_ptr(), _stream_handle(self.stream))
+
     def multiply(self, A_vals: torch.Tensor, B_vals: torch.Tensor,
                  kernel: str = "auto") -> torch.Tensor:
         Cv = torch.empty(max(1, self.info.c_nnz), dtype=A_vals.dtype, device=A_vals.device)

@@ -436,6 +436,31 @@ DIAGPU_API int diagpu_spgemm_numeric_astat_c64(
     const int32_t* C_len, const int64_t* C_starts, int64_t c_ndiag, const int64_t* pair_ptr,
     const int32_t* records, int64_t n_pairs, diagpu_complex64* C_vals, void* stream);
 
+/* C = (alpha A) B + sigma I in one pass: diagpu_spgemm_numeric_astat_f32 /
+ * _c64 (same arguments, limits and records) with each staged A element
+ * scaled once in LDS before any term reads it, and sigma added to the sums of
+ * C's main diagonal (offset 0) before they are stored; a C without a main
+ * diagonal gets no sigma (add it with diagpu_dia_axpby_*).  fp32: the C of
+ * diagpu_spgemm_numeric_astat_f32 on the operand fl(alpha a), bit for bit,
+ * with fl(c + sigma) on the main diagonal.  Complex: each part of alpha a is
+ * one fused multiply-add over the other product.  No reference counterpart:
+ * the reference ships no matrix-power driver (spmspm/gather_flat.cuh:13-14
+ * describes one).  For the Taylor chain's Horner step
+ * S_j = I + ((t/j) H) S_{j+1}, which otherwise takes a scaling pass over H
+ * and an identity pass over C around the product. */
+DIAGPU_API int diagpu_spgemm_numeric_astat_scaled_f32(
+    int32_t n, const int32_t* A_off, const int64_t* A_starts, int32_t nA, const float* A_vals,
+    float alpha, const float* B_vals, const int32_t* C_off, const int32_t* C_len,
+    const int64_t* C_starts, int64_t c_ndiag, const int64_t* pair_ptr, const int32_t* records,
+    int64_t n_pairs, float sigma, float* C_vals, void* stream);
+
+DIAGPU_API int diagpu_spgemm_numeric_astat_scaled_c64(
+    int32_t n, const int32_t* A_off, const int64_t* A_starts, int32_t nA,
+    const diagpu_complex64* A_vals, diagpu_complex64 alpha, const diagpu_complex64* B_vals,
+    const int32_t* C_off, const int32_t* C_len, const int64_t* C_starts, int64_t c_ndiag,
+    const int64_t* pair_ptr, const int32_t* records, int64_t n_pairs, diagpu_complex64 sigma,
+    diagpu_complex64* C_vals, void* stream);
+
 /* ======================================================================
  * gemm_diag: row-packed operands, HM-layout C
  * ====================================================================== */

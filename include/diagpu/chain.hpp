@@ -193,15 +193,14 @@ inline DeviceHMT<T> axpby(typename NoDeduce<HMScalar<T>>::type alpha, const Devi
     return Z;
 }
 
-// C = A * B; the plan is built on the device for this product.
+// The product's structure from a built plan (values allocated, not
+// initialised; the host offsets arrive once `stream` has run the copies).
 template <typename T>
-inline DeviceHMT<T> multiply(const DeviceHMT<T>& A, const DeviceHMT<T>& B, hipStream_t stream = 0)
+inline DeviceHMT<T> product_structure(int n, const SpgemmPlan& plan, hipStream_t stream)
 {
-    SpgemmPlan plan(A.n, A.off.data(), A.len.data(), A.starts.data(), A.ndiag(), B.off.data(),
-                    B.len.data(), B.starts.data(), B.ndiag(), false, stream);
     const auto& inf = plan.info();
     DeviceHMT<T> C;
-    C.n = A.n;
+    C.n = n;
     C.nnz = inf.c_nnz;
     const size_t nc = static_cast<size_t>(inf.c_ndiag);
     C.offsets.resize(nc);
@@ -214,8 +213,18 @@ inline DeviceHMT<T> multiply(const DeviceHMT<T>& A, const DeviceHMT<T>& B, hipSt
         check_hip(hipMemcpyAsync(C.len.data(), plan.c_lengths(), nc * sizeof(int), hipMemcpyDeviceToDevice, stream), "hipMemcpyAsync");
         check_hip(hipMemcpyAsync(C.starts.data(), plan.c_starts(), nc * sizeof(int64_t), hipMemcpyDeviceToDevice, stream), "hipMemcpyAsync");
         check_hip(hipMemcpyAsync(C.offsets.data(), plan.c_offsets(), nc * sizeof(int), hipMemcpyDeviceToHost, stream), "hipMemcpyAsync");
-        plan.numeric(A.vals.data(), B.vals.data(), C.vals.data(), stream);
     }
+    return C;
+}
+
+// C = A * B; the plan is built on the device for this product.
+template <typename T>
+inline DeviceHMT<T> multiply(const DeviceHMT<T>& A, const DeviceHMT<T>& B, hipStream_t stream = 0)
+{
+    SpgemmPlan plan(A.n, A.off.data(), A.len.data(), A.starts.data(), A.ndiag(), B.off.data(),
+                    B.len.data(), B.starts.data(), B.ndiag(), false, stream);
+    DeviceHMT<T> C = product_structure<T>(A.n, plan, stream);
+    if (C.offsets.size()) plan.numeric(A.vals.data(), B.vals.data(), C.vals.data(), stream);
     // the plan's buffers are released when it goes out of scope
     check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
     return C;
@@ -270,6 +279,43 @@ inline void add_identity(DeviceHMT<T>& S, typename NoDeduce<HMScalar<T>>::type s
     check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");       // before I is freed
 }
 
+// One Horner step I + (alpha H) S.  Where H goes first (narrow_first) and
+// the A-stationary kernel takes the plan, one fused product:
+// diagpu_spgemm_numeric_astat_scaled_* scales H in LDS and adds I to the
+// product's main diagonal (fp32: the bits of the unfused step on finite
+// values whose scaled elements are normal or zero).  Otherwise (alpha H)
+// is formed by axpby, multiplied, and I added in place.  Synchronises
+// before returning, so S may be freed.
+template <typename T>
+inline DeviceHMT<T> horner_step(const DeviceHMT<T>& H, typename NoDeduce<HMScalar<T>>::type alpha,
+                                const DeviceHMT<T>& S, hipStream_t stream = 0)
+{
+    using S_t = HMScalar<T>;
+    if (narrow_first(H)) {
+        SpgemmPlan plan(H.n, H.off.data(), H.len.data(), H.starts.data(), H.ndiag(), S.off.data(),
+                        S.len.data(), S.starts.data(), S.ndiag(), false, stream);
+        const bool fused = std::is_same<T, float>::value ? plan.uses_astat() : plan.uses_astat_c64();
+        if (fused) {
+            DeviceHMT<T> C = product_structure<T>(H.n, plan, stream);
+            // C has a main diagonal where some offset of H has its negation in S
+            bool has0 = false;
+            for (int h : H.offsets)
+                has0 = has0 || std::binary_search(S.offsets.begin(), S.offsets.end(), -h);
+            if (C.offsets.size())
+                plan.numeric_scaled(H.vals.data(), HMValue<T>::to_c(alpha), S.vals.data(),
+                                    HMValue<T>::to_c(S_t(has0 ? 1 : 0)), C.vals.data(), stream);
+            check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");   // C's host offsets
+            if (!has0) add_identity<T>(C, S_t(1), stream);                      // (synchronises)
+            return C;
+        }
+    }
+    const DeviceHMT<T> Hj = axpby<T>(alpha, H, S_t(0), nullptr, stream);
+    // multiply syncs before its operands may be freed
+    DeviceHMT<T> C = narrow_first(Hj) ? multiply(Hj, S, stream) : multiply(S, Hj, stream);
+    add_identity<T>(C, S_t(1), stream);
+    return C;
+}
+
 // S = sum_{k=0..order} (t H)^k / k! in Horner form:
 //   S_order = I + (t/order) H,  S_j = I + S_{j+1} * ((t/j) H),  S = S_1,
 // one device-planned SpGEMM per step of the wide S_{j+1} and the narrow
@@ -285,12 +331,8 @@ inline DeviceHMT<T> taylor_expm(const DeviceHMT<T>& H, typename NoDeduce<HMScala
     if (order == 0) return identity_hm<T>(H.n);
     const DeviceHMT<T> I = identity_hm<T>(H.n);
     DeviceHMT<T> S = axpby<T>(t / static_cast<float>(order), H, S_t(1), &I, stream);
-    for (int j = order - 1; j >= 1; --j) {
-        const DeviceHMT<T> Hj = axpby<T>(t / static_cast<float>(j), H, S_t(0), nullptr, stream);
-        // multiply syncs before the old S is freed
-        S = narrow_first(Hj) ? multiply(Hj, S, stream) : multiply(S, Hj, stream);
-        add_identity<T>(S, S_t(1), stream);
-    }
+    for (int j = order - 1; j >= 1; --j)
+        S = horner_step<T>(H, t / static_cast<float>(j), S, stream);
     check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
     return S;
 }

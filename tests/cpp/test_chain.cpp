@@ -12,6 +12,7 @@
 #include <cmath>
 #include <complex>
 #include <cstdio>
+#include <cstring>
 #include <random>
 #include <set>
 #include <vector>
@@ -162,6 +163,33 @@ static void test_axpby()
     char det[96];
     const bool ok = compare(Z, W, B, 1.2e-7, {-7, 0, 1, 3, 400}, det, sizeof det);
     report("axpby on the union of diagonals", ok, det);
+}
+
+// The fused Horner step I + (a H) S (diagpu_spgemm_numeric_astat_scaled_f32:
+// H scaled in LDS, I added to the product's main diagonal) against the
+// unfused one (axpby, product, add_identity): the same offsets and bits, at
+// an n the A-stationary kernel takes; with and without a main diagonal in
+// the product (then I is added on the union, as unfused).
+static void test_horner_fused(const char* name, int n, const std::vector<int>& ho,
+                              const std::vector<int>& so)
+{
+    const HMMatrix Hh = random_hm(n, ho, 11), Sh = random_hm(n, so, 12);
+    const diagpu::DeviceHM H = diagpu::DeviceHM::upload(Hh), S = diagpu::DeviceHM::upload(Sh);
+    const float a = 0.37f;
+    const diagpu::SpgemmPlan plan(n, H.off.data(), H.len.data(), H.starts.data(), H.ndiag(),
+                                  S.off.data(), S.len.data(), S.starts.data(), S.ndiag());
+    const HMMatrix F = diagpu::horner_step<float>(H, a, S).download();
+    const diagpu::DeviceHM Hj = diagpu::axpby<float>(a, H, 0.0f, nullptr);
+    diagpu::DeviceHM P = diagpu::multiply(Hj, S);
+    diagpu::add_identity<float>(P, 1.0f);
+    const HMMatrix U = P.download();
+    const bool same = F.diag_offsets == U.diag_offsets && F.values.size() == U.values.size() &&
+                      std::memcmp(F.values.data(), U.values.data(),
+                                  F.values.size() * sizeof(float)) == 0;
+    char det[96];
+    std::snprintf(det, sizeof det, "A-stationary plan %d, %d C diagonals, %zu values",
+                  (int)plan.uses_astat(), (int)F.diag_offsets.size(), F.values.size());
+    report(name, same && plan.uses_astat(), det);
 }
 
 // ---- complex propagator ----------------------------------------------------
@@ -391,6 +419,9 @@ int main()
         test_propagator("exp(-i 0.05 H), complex Hermitian, order 10", 120, {0, 1, 3, 17}, true, 0.05f, 10);
         test_propagator("exp(-i 0.1 H), real H promoted, order 12", 96, {0, 2, 5}, false, 0.1f, 12);
         test_propagator_applied();
+        test_horner_fused("fused Horner step, fp32 bits", 8192, {-3, -1, 0, 1, 4},
+                          {-40, -2, 0, 5, 9, 33});
+        test_horner_fused("fused Horner step, no main diagonal", 6000, {-2, 1}, {-5, 3});
     } catch (const std::exception& e) {
         std::printf("  exception: %s\n", e.what());
         g_all = false;

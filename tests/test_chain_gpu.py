@@ -209,3 +209,115 @@ def test_complex_chain_order_and_kernel(dev):
     wide = chain.as_complex(hm_random(4096, list(range(-_lib.ASTAT_MAX_A_C64, 1)), 3, dev))
     assert not chain._narrow_first(wide)
     assert chain._narrow_first(hm_random(4096, list(range(-200, 1)), 3, dev))   # fp32: always
+
+
+# ---- the fused Horner step (diagpu_spgemm_numeric_astat_scaled_*) ----------
+
+_S7 = [-16384, -128, -1, 0, 1, 128, 16384]      # the 7-point stencil's offsets at n = 2^20
+
+
+def _with_main(C_vals, C_offsets, C_starts, n, sigma):
+    """C + sigma I where C has a main diagonal (offset 0), in fp32/c64."""
+    out = C_vals.clone()
+    offs = C_offsets.cpu().tolist()
+    if 0 in offs:
+        s = int(C_starts[offs.index(0)])
+        out[s: s + n] += sigma
+    return out
+
+
+@pytest.mark.parametrize("n,a_offs,b_offs", [
+    (8192, [-3, -1, 0, 1, 4], [-40, -2, 0, 5, 9, 33]),             # 4 rows per lane
+    (8192, list(range(-20, 21, 2)), list(range(-30, 31, 3))),       # four-entry batches
+    (1 << 20, [-16384, -128, -1, 0, 1, 128, 16384], [-2, 0, 3]),    # 16 rows per lane
+    (1 << 20, _S7, _sumset(_sumset(_S7, _S7, 1 << 20), _S7, 1 << 20)),  # 8 rows per lane
+    (6000, [-2, 1], [-5, 3]),                                       # C without a main diagonal
+    (1 << 18, [-700, -3, 0, 2, 900], [-4000, -10, 0, 10, 4000]),    # the longer last block
+])
+def test_numeric_scaled_f32_bits(dev, n, a_offs, b_offs):
+    """C = (alpha A) B + sigma I from one fused pass has the bits of the
+    plain A-stationary product on the operand fl(alpha A) (scaled by torch)
+    with fl(c + sigma) added to the main diagonal, for every rows-per-lane
+    layout the kernel chooses; sigma is dropped where C has no main diagonal."""
+    from diagpu_amd.spgemm import SpgemmPlan
+    A, B = hm_random(n, a_offs, 21, dev), hm_random(n, b_offs, 22, dev)
+    plan = SpgemmPlan(A, B)
+    assert plan.kernel_for(torch.float32) == "astat"
+    alpha, sigma = 0.37, 1.0
+    fused = plan.multiply(A.values, B.values)                     # buffer of the right size
+    plan.numeric_scaled(A.values, B.values, fused, alpha, sigma)
+    scaled = (A.values * torch.tensor(alpha, dtype=torch.float32, device=dev)).contiguous()
+    plain = plan.multiply(scaled, B.values, kernel="astat")
+    want = _with_main(plain, plan.c_offsets(), plan.c_starts(), n, sigma)
+    torch.cuda.synchronize()
+    assert torch.equal(fused.view(torch.int32), want.view(torch.int32))
+    # a second call on the same C buffer overwrites it (nothing accumulates)
+    plan.numeric_scaled(A.values, B.values, fused, alpha, sigma)
+    assert torch.equal(fused.view(torch.int32), want.view(torch.int32))
+
+
+@pytest.mark.parametrize("n,a_offs,b_offs", [
+    (1 << 20, [-16384, -128, -1, 0, 1, 128, 16384], [-129, -1, 0, 2, 16385]),
+    (8192, [-3, -1, 0, 1, 4], [-40, -2, 0, 5, 9, 33]),
+])
+def test_numeric_scaled_c64(dev, n, a_offs, b_offs):
+    """Complex values: the fused pass against the plain product of the
+    operand alpha A scaled by torch, within 1e-6 of |alpha| sum |a| |b|
+    (plus |sigma| on the main diagonal); the bound's sums come from the same
+    plan on |A|, |B| in fp32."""
+    from diagpu_amd.spgemm import SpgemmPlan
+    Ar, Br = hm_random(n, a_offs, 23, dev), hm_random(n, b_offs, 24, dev)
+    A = chain.as_complex(Ar)
+    B = chain.as_complex(Br)
+    A.values = torch.complex(Ar.values, torch.roll(Ar.values, 3)).contiguous()
+    B.values = torch.complex(Br.values, -torch.roll(Br.values, 5)).contiguous()
+    plan = SpgemmPlan(A, B)
+    assert plan.kernel_for(torch.complex64) == "astat"
+    alpha, sigma = complex(0.0, -0.02), complex(1.0, 0.5)
+    fused = plan.multiply(A.values, B.values)
+    plan.numeric_scaled(A.values, B.values, fused, alpha, sigma)
+    scaled = (A.values * alpha).contiguous()
+    want = _with_main(plan.multiply(scaled, B.values, kernel="astat"), plan.c_offsets(),
+                      plan.c_starts(), n, sigma)
+    ab = plan.multiply(A.values.abs().contiguous(), B.values.abs().contiguous(), kernel="gather")
+    bound = 1e-6 * (abs(alpha) * ab + abs(sigma)) + 1e-30
+    torch.cuda.synchronize()
+    assert bool(((fused - want).abs() <= bound).all())
+
+
+def test_numeric_scaled_refuses_other_kernels(dev):
+    """numeric_scaled runs only where the A-stationary kernel takes the plan
+    (here n < 4096: the gather's)."""
+    from diagpu_amd.spgemm import SpgemmPlan
+    A = hm_random(1000, [-1, 0, 1], 25, dev)
+    plan = SpgemmPlan(A, A)
+    assert plan.kernel_for(torch.float32) == "gather"
+    C = plan.multiply(A.values, A.values)
+    with pytest.raises(ValueError):
+        plan.numeric_scaled(A.values, A.values, C, 2.0, 1.0)
+
+
+@pytest.mark.parametrize("complex_values", [False, True])
+def test_fused_chain_matches_unfused(dev, monkeypatch, complex_values):
+    """The Taylor chain with its fused Horner steps against the same chain
+    with every step unfused (scaling pass, product, identity add): the same
+    offsets, the same fp32 bits (no scaled element of the stencil is
+    subnormal), complex values within 1e-6 of the result's largest element;
+    the phase-synchronised form takes the fused steps too (one axpby: the
+    first step's I + (t/order) H) and gives the same values."""
+    H = hm_stencil7(128, 128, 64, dev)
+    t, order = (complex(0.0, -0.02), 6) if complex_values else (0.05, 6)
+    S1 = chain.taylor_expm(H, t, order)
+    st = chain.ChainStats()
+    S2 = chain.taylor_expm(H, t, order, st)
+    monkeypatch.setattr(chain, "_fused", lambda plan, H: False)
+    S0 = chain.taylor_expm(H, t, order)
+    torch.cuda.synchronize()
+    assert len(st.axpby) == 1 and len(st.numeric) == order - 1
+    assert S1.offsets.cpu().tolist() == S0.offsets.cpu().tolist() == S2.offsets.cpu().tolist()
+    assert torch.equal(S1.values, S2.values)
+    if complex_values:
+        tol = 1e-6 * S0.values.abs().max().item()
+        assert (S1.values - S0.values).abs().max().item() <= tol
+    else:
+        assert torch.equal(S1.values.view(torch.int32), S0.values.view(torch.int32))
