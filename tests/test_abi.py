@@ -218,6 +218,23 @@ def test_complex_and_krylov_argument_errors():
     assert astat_c(_lib.ASTAT_MAX_A_C64 + 1, 5) == _lib.ERR_CAPACITY
     assert astat_c(3, 200) == _lib.ERR_ARG
     assert astat_c(3, 0) == _lib.OK
+    # the fused (alpha A) B + sigma I entry points: the same checks, the same limits
+    one = _lib.Complex64(1.0, 0.0)
+    for name, a, s, cap in (("diagpu_spgemm_numeric_astat_scaled_f32", 2.0, 1.0, _lib.ASTAT_MAX_A),
+                            ("diagpu_spgemm_numeric_astat_scaled_c64", one, one,
+                             _lib.ASTAT_MAX_A_C64)):
+        sc = lambda nA, nC, n=100, npairs=1: _status(name, n, fake, fake, nA, fake, a, fake,
+                                                     fake, fake, fake, nC, fake, fake, npairs, s,
+                                                     fake, None)
+        assert sc(0, 5) == _lib.ERR_ARG
+        assert sc(3, 5, 1 << 30) == _lib.ERR_ARG
+        assert sc(3, 1 << 29, 1 << 29) == _lib.ERR_ARG
+        assert sc(3, 5, 100, 1 << 28) == _lib.ERR_ARG
+        assert sc(cap + 1, 5) == _lib.ERR_CAPACITY
+        assert sc(3, 200) == _lib.ERR_ARG
+        assert sc(3, 0) == _lib.OK
+        bad = [100, fake, fake, 3, None, a, fake, fake, fake, fake, 5, fake, fake, 1, s, fake, None]
+        assert _status(name, *bad) == _lib.ERR_ARG                # A values NULL
 
 
 def test_astat_max_a_matches_header():
