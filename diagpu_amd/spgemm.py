@@ -406,9 +406,11 @@ class SpgemmPlan:
         (diagpu_spgemm_numeric_astat_scaled_f32 / _c64): A scaled in LDS,
         sigma added to C's main diagonal (none where C has no main
         diagonal).  fp32: the bits of numeric() on the operand fl(alpha A)
-        plus fl(c + sigma) on the main diagonal.  Only for plans the
-        automatic choice runs on that kernel (kernel_for(dtype) ==
-        "astat"); ValueError otherwise."""
+        plus fl(c + sigma) on the main diagonal.  For any plan that kernel
+        takes (its limits, as numeric(kernel="astat"): at most
+        DIAGPU_ASTAT_MAX_A A diagonals, or DIAGPU_ASTAT_MAX_A_C64 for complex
+        values, 4096 <= n < 2^30, B indices below 2^30); ValueError
+        otherwise."""
         dt = A_vals.dtype
         if dt not in (torch.float32, torch.complex64):
             raise TypeError(f"unsupported value dtype {dt}")
@@ -420,8 +422,19 @@ class SpgemmPlan:
                              f"the plan's operands need {inf.a_extent} / {inf.b_extent}")
         if C_vals.numel() < inf.c_nnz:
             raise ValueError(f"C_vals has {C_vals.numel()} elements, needs {inf.c_nnz}")
-        if self.kernel_for(dt) != "astat":
+        cap = _lib.ASTAT_MAX_A if dt == torch.float32 else _lib.ASTAT_MAX_A_C64
+        if (self.A.offsets.numel() > cap or not 4096 <= self.n < 1 << 30
+                or inf.c_ndiag >= 1 << 29 or inf.n_pairs >= 1 << 28):
             raise ValueError("numeric_scaled: the A-stationary kernel does not take this plan")
+        if self._astat is not True:
+            try:
+                self.astat_records()
+            except _lib.DiagpuError as e:
+                if e.status != _lib.ERR_CAPACITY:
+                    raise
+                self._astat = False
+                raise ValueError("numeric_scaled: B indices beyond the A-stationary "
+                                 "kernel's 2^30") from e
         rec = self._addr("records") if self._astat is True else self._astat.data_ptr()
         A = self.A
         if dt == torch.float32:

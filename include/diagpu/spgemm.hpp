@@ -416,13 +416,13 @@ public:
     // C_vals = (alpha A) B + sigma I in one pass on the A-stationary kernel
     // (diagpu_spgemm_numeric_astat_scaled_f32 / _c64: A scaled in LDS, sigma
     // added to C's main diagonal, none where C has no main diagonal);
-    // asynchronous on `stream`.  For plans the automatic choice runs on that
-    // kernel (uses_astat / uses_astat_c64); DIAGPU_ERR_ARG otherwise.
+    // asynchronous on `stream` (a plan not yet prepared for that kernel
+    // synchronises once to prepare).  For any plan the kernel takes, as
+    // numeric() with NumericKernel::AStationary (its limits are errors).
     void numeric_scaled(const float* dA_vals, float alpha, const float* dB_vals, float sigma,
                         float* dC_vals, hipStream_t stream = 0) const
     {
-        if (!uses_astat())
-            throw Error(DIAGPU_ERR_ARG, "SpgemmPlan::numeric_scaled: not an A-stationary plan");
+        if (!astat_prepared_) prepare_astat(stream);
         check(diagpu_spgemm_numeric_astat_scaled_f32(
             n_, A_off_.data(), A_starts_.data(), nA_, dA_vals, alpha, dB_vals, C_off_.data(),
             C_len_.data(), C_starts_.data(), info_.c_ndiag, ptr_.data(), records_.data(),
@@ -432,8 +432,7 @@ public:
                         const diagpu_complex64* dB_vals, diagpu_complex64 sigma,
                         diagpu_complex64* dC_vals, hipStream_t stream = 0) const
     {
-        if (!uses_astat_c64())
-            throw Error(DIAGPU_ERR_ARG, "SpgemmPlan::numeric_scaled: not an A-stationary plan");
+        if (!astat_prepared_) prepare_astat(stream);
         check(diagpu_spgemm_numeric_astat_scaled_c64(
             n_, A_off_.data(), A_starts_.data(), nA_, dA_vals, alpha, dB_vals, C_off_.data(),
             C_len_.data(), C_starts_.data(), info_.c_ndiag, ptr_.data(), records_.data(),

@@ -271,3 +271,15 @@ def test_symbolic_noalloc_rejects_beyond_scratch():
     assert lib.diagpu_spgemm_symbolic_noalloc(n, fake, fake, fake, 3, fake, fake, fake, 3, fake,
                                               fake, fake, 9, fake, fake, 9, None, None,
                                               None) == _lib.ERR_ARG
+
+
+def test_package_modules_import():
+    """Every module of the package imports on a host without a GPU (the GPU
+    tests would otherwise be the first to meet a broken module)."""
+    import importlib
+
+    import diagpu_amd
+    names = [f.stem for f in Path(diagpu_amd.__file__).parent.glob("*.py") if f.stem != "__init__"]
+    assert {"spgemm", "chain", "spmv", "krylov", "workloads", "_lib", "build"} <= set(names)
+    for name in names:
+        importlib.import_module(f"diagpu_amd.{name}")

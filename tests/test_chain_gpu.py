@@ -285,16 +285,28 @@ def test_numeric_scaled_c64(dev, n, a_offs, b_offs):
     assert bool(((fused - want).abs() <= bound).all())
 
 
-def test_numeric_scaled_refuses_other_kernels(dev):
-    """numeric_scaled runs only where the A-stationary kernel takes the plan
-    (here n < 4096: the gather's)."""
+def test_numeric_scaled_limits_and_forced_plans(dev):
+    """numeric_scaled refuses a plan the A-stationary kernel cannot take
+    (n < 4096) and takes one the automatic choice leaves to another kernel
+    (the tridiagonal square at n = 2^19 goes to the gather), with the same
+    bits as the forced plain kernel on the torch-scaled operand."""
     from diagpu_amd.spgemm import SpgemmPlan
     A = hm_random(1000, [-1, 0, 1], 25, dev)
     plan = SpgemmPlan(A, A)
-    assert plan.kernel_for(torch.float32) == "gather"
     C = plan.multiply(A.values, A.values)
     with pytest.raises(ValueError):
         plan.numeric_scaled(A.values, A.values, C, 2.0, 1.0)
+    n = 1 << 19
+    A = hm_random(n, [-1, 0, 1], 26, dev)
+    plan = SpgemmPlan(A, A)
+    assert plan.kernel_for(torch.float32) == "gather"
+    fused = plan.multiply(A.values, A.values)
+    plan.numeric_scaled(A.values, A.values, fused, -1.5, 2.0)
+    scaled = (A.values * torch.tensor(-1.5, dtype=torch.float32, device=dev)).contiguous()
+    want = _with_main(plan.multiply(scaled, A.values, kernel="astat"), plan.c_offsets(),
+                      plan.c_starts(), n, 2.0)
+    torch.cuda.synchronize()
+    assert torch.equal(fused.view(torch.int32), want.view(torch.int32))
 
 
 @pytest.mark.parametrize("complex_values", [False, True])
