@@ -302,9 +302,12 @@ def taylor_expm(H: HM, t, order: int, stats: ChainStats | None = None) -> HM:
         return identity(H.n, dev, H.values.dtype)
     ax = stats.axpby if stats else None
     _host_offsets(H)                             # once: every product's offsets follow
+    # everything queued before S_order: H's structure is complete once it is
+    ready = torch.cuda.Event()
+    ready.record(torch.cuda.current_stream(dev))
     S = _timed(ax, axpby, t / order, H, 1.0, _unit(H.n, dev, H.values.dtype))
     if stats is None:
-        return _taylor_steps(H, t, order, S)
+        return _taylor_steps(H, t, order, S, ready)
     for j in range(order - 1, 0, -1):
         S = _horner_step_synced(H, t / j, S, stats)
     return S
@@ -380,16 +383,22 @@ def _side_stream(device) -> torch.cuda.Stream:
     return st
 
 
-def _taylor_steps(H: HM, t, order: int, S: HM) -> HM:
+def _taylor_steps(H: HM, t, order: int, S: HM, ready: torch.cuda.Event) -> HM:
     """The Horner steps of taylor_expm with each product's plan built on a
     side stream while the previous product runs: a plan needs only its
     operands' structure (the previous plan's C arrays, complete once its
     symbolic phase has returned), so its one stream sync waits for its own
     symbolic phase, not for the product queued before it.  Products,
-    scalings and identity adds stay on the caller's stream, in order."""
+    scalings and identity adds stay on the caller's stream, in order.
+    `ready`: recorded on the caller's stream before S was formed; where S
+    shares H's structure, the first plan waits for it only, not for the
+    pass that formed S's values."""
     main = torch.cuda.current_stream(H.values.device)
     side = _side_stream(H.values.device)
-    side.wait_stream(main)                      # S's structure, H's values
+    if S.offsets is H.offsets and S.starts is H.starts and S.lengths is H.lengths:
+        side.wait_event(ready)                  # H's structure
+    else:
+        side.wait_stream(main)                  # S's structure, formed on main
     narrow = _narrow_first(H)
     for j in range(order - 1, 0, -1):
         # the plan needs the operands' structure only: H's is (t/j) H's
