@@ -333,3 +333,27 @@ def test_fused_chain_matches_unfused(dev, monkeypatch, complex_values):
         assert (S1.values - S0.values).abs().max().item() <= tol
     else:
         assert torch.equal(S1.values.view(torch.int32), S0.values.view(torch.int32))
+
+
+def test_fused_chain_without_main_diagonal(dev, monkeypatch):
+    """A Taylor chain whose H has no main diagonal, at an n the fused steps
+    take: S_4 = I + (t/4) H gets a structure of its own (the first plan then
+    waits for it on the caller's stream), a product without a main diagonal
+    takes sigma = 0 and I on the union, the next one sigma = 1 in the kernel;
+    the same offsets and bits as with every step unfused, and against the
+    float64 recurrence for S x."""
+    n, t, order = 8192, 0.3, 4
+    H = hm_random(n, [-2, 1], 31, dev)
+    S1 = chain.taylor_expm(H, t, order)
+    monkeypatch.setattr(chain, "_fused", lambda plan, H: False)
+    S0 = chain.taylor_expm(H, t, order)
+    torch.cuda.synchronize()
+    assert S1.offsets.cpu().tolist() == S0.offsets.cpu().tolist()
+    assert torch.equal(S1.values.view(torch.int32), S0.values.view(torch.int32))
+    rng = np.random.default_rng(1)
+    x = rng.uniform(-1.0, 1.0, n)
+    want, v = x.copy(), x.copy()
+    for k in range(1, order + 1):
+        v = matvec64(H, v)
+        want += t ** k / math.factorial(k) * v
+    assert np.all(np.abs(matvec64(S1, x) - want) <= 1e-5 * order * math.exp(2 * t))
