@@ -292,7 +292,11 @@ def taylor_expm(H: HM, t, order: int, stats: ChainStats | None = None) -> HM:
     narrow (t/j) H (S_{j+1} is a polynomial in H, so the two commute; the
     narrow factor goes first where the A-stationary kernel holds it:
     _narrow_first), and an in-place add of I to the product's main
-    diagonal (a full union pass only when the product lacks that diagonal)."""
+    diagonal (a full union pass only when the product lacks that diagonal).
+    Where the A-stationary kernel takes a step's plan with H first, the
+    scaling, the product and the add of I are one fused launch
+    (SpgemmPlan.numeric_scaled); the values are those of the unfused step
+    (fp32 bit for bit, complex to rounding)."""
     if order < 0:
         raise ValueError("order must be >= 0")
     dev = H.values.device

@@ -10,7 +10,8 @@
 //
 // No reference counterpart: the reference describes a matrix-power chain
 // (spmspm/gather_flat.cuh:13-14,110-117) but ships no driver for it.  The
-// Taylor chain needs this to scale H and to add each power into the sum.
+// Taylor chain uses it to form I + (t/K) H and, in steps not fused into the
+// product (diagpu_spgemm_numeric_astat_scaled_*), to scale H and to add I.
 //
 // Work: (Z diagonal, span) items, spans fastest, in contiguous ranges per
 // workgroup, so a workgroup looks up X's and Y's diagonal (two binary
