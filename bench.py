@@ -631,6 +631,28 @@ def time_taylor(order: int = 6, t: float = 0.05, chains: int = 9):
         torch.cuda.synchronize()
         times.append(time.perf_counter() - t0)
     total = statistics.median(times)
+    # the matrix-power chain H^6 on the same stencil: plans built beside the
+    # products (chain.power), and each plan on the caller's stream after the
+    # product before it (chain.multiply in a loop), medians of `chains` each
+    def timed(fn):
+        ts = []
+        for _ in range(chains):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    def serial_power():
+        P = H
+        for _ in range(order - 1):
+            P = chain.multiply(H, P)
+        return P
+    chain.power(H, order)
+    serial_power()
+    power_ms = timed(lambda: chain.power(H, order)) * 1e3
+    power_serial_ms = timed(serial_power) * 1e3
     st = chain.ChainStats()
     t0 = time.perf_counter()
     S = chain.taylor_expm(H, t, order, st)
@@ -646,6 +668,7 @@ def time_taylor(order: int = 6, t: float = 0.05, chains: int = 9):
             "S_diags": S.ndiag, "S_nnz": S.nnz, "total_ms": round(total * 1e3, 3),
             "total_min_ms": round(min(times) * 1e3, 3), "total_max_ms": round(max(times) * 1e3, 3),
             "chains": chains, "total_ms_phase_synced": round(total_split * 1e3, 3),
+            "power_ms": round(power_ms, 3), "power_serial_ms": round(power_serial_ms, 3),
             "symbolic_ms": round(sum(st.symbolic) * 1e3, 3),
             "numeric_ms": round(sum(st.numeric) * 1e3, 3),
             "axpby_ms": round(sum(st.axpby) * 1e3, 3),

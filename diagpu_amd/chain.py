@@ -248,9 +248,41 @@ def power(H: HM, k: int, stats: ChainStats | None = None) -> HM:
     factors commute)."""
     if k < 1:
         raise ValueError("k must be >= 1")
+    if stats is None:
+        return _power_steps(H, k)
     P = H
     for _ in range(k - 1):
         P = multiply(H, P, stats) if _narrow_first(H) else multiply(P, H, stats)
+    return P
+
+
+def _power_steps(H: HM, k: int) -> HM:
+    """power() with each product's plan built on the side stream while the
+    previous product runs (as _taylor_steps): a plan needs only the
+    operands' structure, and P_{j-1}'s is the previous plan's C arrays,
+    complete once its symbolic phase has returned.  Products stay on the
+    caller's stream, in order."""
+    main = torch.cuda.current_stream(H.values.device)
+    side = _side_stream(H.values.device)
+    side.wait_stream(main)                      # H's structure
+    narrow = _narrow_first(H)
+    _host_offsets(H)
+    P = H
+    for _ in range(k - 1):
+        with torch.cuda.stream(side):
+            plan = SpgemmPlan(H, P, stream=side) if narrow else SpgemmPlan(P, H, stream=side)
+            plan.prepare(H.values.dtype)
+        plan.hand_over(main)
+        inf = plan.info
+        C = HM(H.n, plan.c_offsets(), plan.c_lengths(), plan.c_starts(),
+               _c_values(inf.c_nnz, H.values))
+        if inf.c_ndiag:
+            if narrow:
+                plan.numeric(H.values, P.values, C.values)
+            else:
+                plan.numeric(P.values, H.values, C.values)
+        C.host_offsets = _sumset(H.n, _host_offsets(H), _host_offsets(P))   # while it runs
+        P = C
     return P
 
 

@@ -357,3 +357,21 @@ def test_fused_chain_without_main_diagonal(dev, monkeypatch):
         v = matvec64(H, v)
         want += t ** k / math.factorial(k) * v
     assert np.all(np.abs(matvec64(S1, x) - want) <= 1e-5 * order * math.exp(2 * t))
+
+
+@pytest.mark.parametrize("complex_values", [False, True])
+def test_power_pipelined_matches_synced(dev, complex_values):
+    """power() with its plans built beside the products (no stats) against
+    the phase-synchronised chain (stats) on the 7-point stencil at n = 2^20:
+    the same offsets and the same bits (the same kernels in the same order
+    on the same operands), and the host offsets it carries equal the
+    device's."""
+    H = hm_stencil7(128, 128, 64, dev)
+    if complex_values:
+        H = chain.as_complex(H)
+        H.values = torch.complex(H.values.real, 0.25 * torch.roll(H.values.real, 7)).contiguous()
+    P1 = chain.power(H, 5)
+    P2 = chain.power(H, 5, chain.ChainStats())
+    torch.cuda.synchronize()
+    assert P1.offsets.cpu().tolist() == P2.offsets.cpu().tolist() == P1.host_offsets
+    assert torch.equal(P1.values.view(torch.int32), P2.values.view(torch.int32))
